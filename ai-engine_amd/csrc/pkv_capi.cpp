@@ -1,0 +1,494 @@
+// pkv_capi.cpp -- the extern "C" boundary of libpagedkv (include/pagedkv.h).
+//
+// Validates every argument on the host (shapes, ranges, alignment, device),
+// records a per-handle error string, and enqueues the HIP kernels on the
+// caller's stream.  No C++ exception crosses the boundary.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "pkv_internal.h"
+
+namespace {
+
+thread_local std::string g_thread_error;
+
+int fail(pkv_pool* p, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (p)
+    p->last_error = buf;
+  else
+    g_thread_error = buf;
+  return code;
+}
+
+int hip_fail(pkv_pool* p, hipError_t e, const char* what) {
+  return fail(p, PKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
+}
+
+bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Makes the pool's device current for the duration of a call.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+#define CHECK_POOL(p)                                                   \
+  do {                                                                  \
+    if (!(p)) return fail(nullptr, PKV_ERR_INVALID, "pool is NULL");    \
+    (p)->last_error.clear();                                            \
+  } while (0)
+
+int check_layer(pkv_pool* p, int layer) {
+  if (layer < 0 || layer >= p->n_layers)
+    return fail(p, PKV_ERR_INVALID, "layer %d out of range [0, %d)", layer,
+                p->n_layers);
+  return PKV_OK;
+}
+
+// Ensure the decode workspace holds `counter_bytes` of counters followed by
+// `total - counter_bytes` of partials.  Counters are zeroed on (re)allocation
+// and the kernels leave them zero.
+int ensure_workspace(pkv_pool* p, size_t total, size_t counter_bytes) {
+  size_t part_need = total - counter_bytes;
+  size_t part_have = p->ws_bytes - p->ws_counter_bytes;
+  if (p->ws && p->ws_counter_bytes >= counter_bytes && part_have >= part_need)
+    return PKV_OK;
+  size_t cb = std::max(counter_bytes, p->ws_counter_bytes);
+  size_t pb = std::max(part_need, part_have);
+  size_t bytes = cb + pb + pb / 4;  // headroom against regrowth
+  if (p->ws) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(p, e, "hipDeviceSynchronize");
+    (void)hipFree(p->ws);
+    p->ws = nullptr;
+    p->ws_bytes = p->ws_counter_bytes = 0;
+  }
+  void* ws = nullptr;
+  hipError_t e = hipMalloc(&ws, bytes);
+  if (e != hipSuccess)
+    return fail(p, PKV_ERR_OOM, "workspace hipMalloc(%zu): %s", bytes,
+                hipGetErrorString(e));
+  e = hipMemset(ws, 0, cb);
+  if (e != hipSuccess) {
+    (void)hipFree(ws);
+    return hip_fail(p, e, "hipMemset(workspace counters)");
+  }
+  p->ws = static_cast<char*>(ws);
+  p->ws_bytes = bytes;
+  p->ws_counter_bytes = cb;
+  return PKV_OK;
+}
+
+// ---- compaction planning ------------------------------------------------
+// Moves m = (s -> d).  A move whose destination is still some other move's
+// source must wait until that block has been read: the chain is built from
+// a move whose dst is free, then repeatedly the move that fills the block
+// just vacated.  Moves left over form cycles; each cycle first parks one
+// block (dst = -1) and finally restores it (src = -1).
+int plan_compaction(pkv_pool* p, const int32_t* src, const int32_t* dst, int n,
+                    std::vector<int32_t>& ops, std::vector<int32_t>& starts) {
+  const int N = p->num_blocks;
+  std::vector<int32_t> move_from(N, -1);  // move_from[d] = s
+  std::vector<int32_t> move_to(N, -1);    // move_to[s] = d
+  for (int i = 0; i < n; ++i) {
+    int s = src[i], d = dst[i];
+    if (s < 0 || s >= N || d < 0 || d >= N)
+      return fail(p, PKV_ERR_INVALID, "compact: pair %d (%d -> %d) out of range [0, %d)", i, s, d, N);
+    if (move_to[s] != -1)
+      return fail(p, PKV_ERR_INVALID, "compact: source block %d appears twice", s);
+    if (move_from[d] != -1)
+      return fail(p, PKV_ERR_INVALID, "compact: destination block %d appears twice", d);
+    move_to[s] = d;
+    move_from[d] = s;
+  }
+  std::vector<char> done(N, 0);  // indexed by source block
+  starts.clear();
+  ops.clear();
+  for (int i = 0; i < n; ++i) {
+    int s = src[i], d = dst[i];
+    if (s == d) {
+      done[s] = 1;
+      continue;
+    }
+    if (move_to[d] != -1) continue;  // d is still someone's source: not a chain head
+    starts.push_back((int32_t)(ops.size() / 2));
+    // execute s -> d, then the move that fills s, and so on
+    int cs = s, cd = d;
+    while (true) {
+      ops.push_back(cs);
+      ops.push_back(cd);
+      done[cs] = 1;
+      int prev = move_from[cs];
+      if (prev == -1 || prev == cs || done[prev]) break;
+      cd = cs;
+      cs = prev;
+    }
+  }
+  for (int i = 0; i < n; ++i) {
+    int s = src[i];
+    if (done[s]) continue;
+    // s lies on a cycle s -> d -> ... -> s.  Park the block that moves into
+    // s's destination chain end: walk backwards from s.
+    starts.push_back((int32_t)(ops.size() / 2));
+    int first_dst = move_to[s];
+    ops.push_back(first_dst);  // park first_dst's content (it moves on)
+    ops.push_back(-1);
+    int cs = s, cd = first_dst;
+    while (true) {
+      ops.push_back(cs);
+      ops.push_back(cd);
+      done[cs] = 1;
+      int prev = move_from[cs];
+      if (prev == first_dst) break;  // first_dst's content is parked
+      cd = cs;
+      cs = prev;
+    }
+    ops.push_back(-1);  // parked content -> its destination
+    ops.push_back(cs);
+    done[first_dst] = 1;
+  }
+  starts.push_back((int32_t)(ops.size() / 2));
+  return PKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pkv_version(void) { return "pagedkv 0.1 gfx950"; }
+
+const char* pkv_last_error(const pkv_pool* pool) {
+  return pool ? pool->last_error.c_str() : g_thread_error.c_str();
+}
+
+int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
+                    int block_size, int n_kv_head, int head_dim, int dtype,
+                    int device) {
+  g_thread_error.clear();
+  if (!out) return fail(nullptr, PKV_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (n_layers <= 0 || num_blocks <= 0 || n_kv_head <= 0)
+    return fail(nullptr, PKV_ERR_INVALID,
+                "n_layers (%d), num_blocks (%d), n_kv_head (%d) must be > 0",
+                n_layers, num_blocks, n_kv_head);
+  if (!is_pow2(block_size) || block_size < 16 || block_size > 256)
+    return fail(nullptr, PKV_ERR_UNSUPPORTED,
+                "block_size %d: must be a power of two in [16, 256]", block_size);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(nullptr, PKV_ERR_UNSUPPORTED, "head_dim %d: must be 64, 128 or 256", head_dim);
+  if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)
+    return fail(nullptr, PKV_ERR_INVALID, "dtype %d unknown", dtype);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(nullptr, PKV_ERR_INVALID, "device %d not available (%d devices)", device, ndev);
+
+  pkv_pool* p = new (std::nothrow) pkv_pool();
+  if (!p) return fail(nullptr, PKV_ERR_OOM, "host allocation failed");
+  p->n_layers = n_layers;
+  p->num_blocks = num_blocks;
+  p->block_size = block_size;
+  p->n_kv_head = n_kv_head;
+  p->head_dim = head_dim;
+  p->dtype = dtype;
+  p->device = device;
+  p->elem_bytes = pkv::dtype_bytes(dtype);
+  p->row_bytes = (size_t)head_dim * p->elem_bytes;
+  p->block_bytes = (size_t)block_size * n_kv_head * p->row_bytes;
+  p->layer_bytes = (size_t)num_blocks * p->block_bytes;
+  size_t total = p->layer_bytes * 2 * (size_t)n_layers;
+
+  DeviceGuard dg(device);
+  if (!dg.ok) {
+    delete p;
+    return fail(nullptr, PKV_ERR_HIP, "hipSetDevice(%d) failed", device);
+  }
+  void* base = nullptr;
+  hipError_t e = hipMalloc(&base, total);
+  if (e != hipSuccess) {
+    delete p;
+    return fail(nullptr, PKV_ERR_OOM, "pool hipMalloc(%zu bytes): %s", total, hipGetErrorString(e));
+  }
+  void* err = nullptr;
+  e = hipMalloc(&err, 256);
+  if (e == hipSuccess) e = hipMemset(base, 0, total);  // Tensor::zeros
+  if (e == hipSuccess) e = hipMemset(err, 0, 256);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    (void)hipFree(base);
+    if (err) (void)hipFree(err);
+    delete p;
+    return fail(nullptr, PKV_ERR_HIP, "pool init: %s", hipGetErrorString(e));
+  }
+  p->base = static_cast<char*>(base);
+  p->err = static_cast<uint32_t*>(err);
+  *out = p;
+  return PKV_OK;
+}
+
+int pkv_pool_destroy(pkv_pool* p) {
+  if (!p) return PKV_OK;
+  DeviceGuard dg(p->device);
+  (void)hipDeviceSynchronize();
+  if (p->base) (void)hipFree(p->base);
+  if (p->err) (void)hipFree(p->err);
+  if (p->ws) (void)hipFree(p->ws);
+  delete p;
+  return PKV_OK;
+}
+
+int pkv_pool_shape(const pkv_pool* p, int* n_layers, int* num_blocks,
+                   int* block_size, int* n_kv_head, int* head_dim, int* dtype) {
+  if (!p) return fail(nullptr, PKV_ERR_INVALID, "pool is NULL");
+  if (n_layers) *n_layers = p->n_layers;
+  if (num_blocks) *num_blocks = p->num_blocks;
+  if (block_size) *block_size = p->block_size;
+  if (n_kv_head) *n_kv_head = p->n_kv_head;
+  if (head_dim) *head_dim = p->head_dim;
+  if (dtype) *dtype = p->dtype;
+  return PKV_OK;
+}
+
+size_t pkv_pool_layer_bytes(const pkv_pool* p) { return p ? p->layer_bytes : 0; }
+
+int pkv_pool_layer_ptrs(const pkv_pool* pc, int layer, void** k, void** v) {
+  pkv_pool* p = const_cast<pkv_pool*>(pc);
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (k) *k = p->layer_k(layer);
+  if (v) *v = p->layer_v(layer);
+  return PKV_OK;
+}
+
+static int pool_rw(pkv_pool* p, int layer, int which, size_t off, size_t n,
+                   void* host, bool read) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (which != PKV_K && which != PKV_V)
+    return fail(p, PKV_ERR_INVALID, "which must be PKV_K or PKV_V");
+  if (off > p->layer_bytes || n > p->layer_bytes - off)
+    return fail(p, PKV_ERR_INVALID, "byte range [%zu, %zu) beyond layer (%zu bytes)", off, off + n, p->layer_bytes);
+  if (n && !host) return fail(p, PKV_ERR_INVALID, "host buffer is NULL");
+  if (n == 0) return PKV_OK;
+  DeviceGuard dg(p->device);
+  char* dev = (which == PKV_K ? p->layer_k(layer) : p->layer_v(layer)) + off;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess)
+    e = read ? hipMemcpy(host, dev, n, hipMemcpyDeviceToHost)
+             : hipMemcpy(dev, host, n, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(p, e, read ? "pool read" : "pool write");
+  return PKV_OK;
+}
+
+int pkv_pool_read(pkv_pool* p, int layer, int which, size_t off, size_t n, void* host_dst) {
+  return pool_rw(p, layer, which, off, n, host_dst, true);
+}
+
+int pkv_pool_write(pkv_pool* p, int layer, int which, size_t off, const void* host_src, size_t n) {
+  return pool_rw(p, layer, which, off, n, const_cast<void*>(host_src), false);
+}
+
+int pkv_pool_fill_normal(pkv_pool* p, uint64_t seed, void* stream) {
+  CHECK_POOL(p);
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_fill_normal(p, seed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "fill_normal launch");
+  return PKV_OK;
+}
+
+int pkv_append(pkv_pool* p, int layer, const void* k, const void* v,
+               const int32_t* slot_mapping, int n_tokens, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (n_tokens < 0) return fail(p, PKV_ERR_INVALID, "n_tokens %d < 0", n_tokens);
+  if (n_tokens == 0) return PKV_OK;
+  if (!k || !v || !slot_mapping) return fail(p, PKV_ERR_INVALID, "k, v and slot_mapping must be non-NULL");
+  if (!aligned16(k) || !aligned16(v))
+    return fail(p, PKV_ERR_INVALID, "k and v must be 16-byte aligned");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_append(p, layer, k, v, slot_mapping, n_tokens,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "append launch");
+  return PKV_OK;
+}
+
+int pkv_gather_seq(pkv_pool* p, int layer, const int32_t* block_table, int len,
+                   void* out_k, void* out_v, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (len < 0) return fail(p, PKV_ERR_INVALID, "len %d < 0", len);
+  if (len == 0) return PKV_OK;
+  if (!block_table || !out_k || !out_v)
+    return fail(p, PKV_ERR_INVALID, "block_table, out_k and out_v must be non-NULL");
+  if (!aligned16(out_k) || !aligned16(out_v))
+    return fail(p, PKV_ERR_INVALID, "out_k and out_v must be 16-byte aligned");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_gather(p, layer, block_table, len, out_k, out_v,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "gather launch");
+  return PKV_OK;
+}
+
+int pkv_copy_blocks(pkv_pool* p, const int32_t* src, const int32_t* dst, int n, void* stream) {
+  CHECK_POOL(p);
+  if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
+  if (n == 0) return PKV_OK;
+  if (!src || !dst) return fail(p, PKV_ERR_INVALID, "src and dst must be non-NULL");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_copy_blocks(p, src, dst, n, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "copy_blocks launch");
+  return PKV_OK;
+}
+
+int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, int n, void* stream) {
+  CHECK_POOL(p);
+  if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
+  if (n == 0) return PKV_OK;
+  if (!src_host || !dst_host) return fail(p, PKV_ERR_INVALID, "src_host and dst_host must be non-NULL");
+  std::vector<int32_t> ops, starts;
+  if (int rc = plan_compaction(p, src_host, dst_host, n, ops, starts)) return rc;
+  int n_chains = (int)starts.size() - 1;
+  if (n_chains <= 0) return PKV_OK;
+  DeviceGuard dg(p->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Plan buffers: uploaded synchronously w.r.t. the host copy, freed after
+  // the launch completes (stream sync) so the call is self-contained.
+  size_t ob = ops.size() * sizeof(int32_t), sb = starts.size() * sizeof(int32_t);
+  void* dplan = nullptr;
+  hipError_t e = hipMalloc(&dplan, ob + sb);
+  if (e != hipSuccess) return fail(p, PKV_ERR_OOM, "compact plan hipMalloc: %s", hipGetErrorString(e));
+  int32_t* d_ops = static_cast<int32_t*>(dplan);
+  int32_t* d_starts = d_ops + ops.size();
+  e = hipMemcpyAsync(d_ops, ops.data(), ob, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(d_starts, starts.data(), sb, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = pkv::launch_compact(p, d_ops, d_starts, n_chains, s);
+  hipError_t e2 = hipStreamSynchronize(s);
+  (void)hipFree(dplan);
+  if (e != hipSuccess) return hip_fail(p, e, "compact");
+  if (e2 != hipSuccess) return hip_fail(p, e2, "compact sync");
+  return PKV_OK;
+}
+
+size_t pkv_decode_workspace_bytes(const pkv_pool* p, int batch, int n_head, int max_context_len) {
+  if (!p || batch <= 0 || n_head <= 0) return 0;
+  return pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, nullptr);
+}
+
+int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_len) {
+  CHECK_POOL(p);
+  if (batch <= 0 || n_head <= 0 || max_context_len <= 0 || n_head % p->n_kv_head != 0)
+    return fail(p, PKV_ERR_INVALID, "reserve_decode: bad shape (batch %d, n_head %d, max_context_len %d)",
+                batch, n_head, max_context_len);
+  DeviceGuard dg(p->device);
+  size_t cb = 0;
+  size_t need = pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, &cb);
+  return ensure_workspace(p, need, cb);
+}
+
+int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* context_lens, int max_context_len, int batch,
+                         int n_head, float scale, const void* k_new, const void* v_new,
+                         void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", batch);
+  if (batch == 0) return PKV_OK;
+  if (!q || !out || !block_tables || !context_lens)
+    return fail(p, PKV_ERR_INVALID, "q, out, block_tables and context_lens must be non-NULL");
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return fail(p, PKV_ERR_INVALID, "k_new and v_new must both be set or both be NULL");
+  if (!aligned16(q) || !aligned16(out) || (k_new && (!aligned16(k_new) || !aligned16(v_new))))
+    return fail(p, PKV_ERR_INVALID, "q, out, k_new, v_new must be 16-byte aligned");
+  if (max_blocks_per_seq <= 0 || max_context_len <= 0)
+    return fail(p, PKV_ERR_INVALID, "max_blocks_per_seq (%d) and max_context_len (%d) must be > 0",
+                max_blocks_per_seq, max_context_len);
+  if (n_head <= 0 || n_head % p->n_kv_head != 0)
+    return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
+  if (!pkv::decode_supported(p, n_head))
+    return fail(p, PKV_ERR_UNSUPPORTED, "decode: n_head/n_kv_head = %d not in {1,2,4,8}",
+                n_head / p->n_kv_head);
+  if (out_dtype != PKV_F32 && out_dtype != p->dtype)
+    return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
+  if (!(scale == scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
+  DeviceGuard dg(p->device);
+  size_t cb = 0;
+  size_t need = pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, &cb);
+  if (int rc = ensure_workspace(p, need, cb)) return rc;
+  pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
+                    max_context_len, batch, n_head, scale, k_new, v_new};
+  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "decode launch");
+  return PKV_OK;
+}
+
+int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
+                          const int32_t* cu_q_lens, const int32_t* context_lens,
+                          const int32_t* block_tables, int max_blocks_per_seq, int n_seqs,
+                          int max_q_len, int max_context_len, int n_head, float scale,
+                          void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (n_seqs < 0) return fail(p, PKV_ERR_INVALID, "n_seqs %d < 0", n_seqs);
+  if (n_seqs == 0 || max_q_len == 0) return PKV_OK;
+  if (!q || !out || !cu_q_lens || !context_lens || !block_tables)
+    return fail(p, PKV_ERR_INVALID, "q, out, cu_q_lens, context_lens, block_tables must be non-NULL");
+  if (!aligned16(q) || !aligned16(out))
+    return fail(p, PKV_ERR_INVALID, "q and out must be 16-byte aligned");
+  if (max_q_len < 0 || max_blocks_per_seq <= 0 || max_context_len <= 0)
+    return fail(p, PKV_ERR_INVALID, "max_q_len, max_blocks_per_seq, max_context_len must be > 0");
+  if (n_head <= 0 || n_head % p->n_kv_head != 0)
+    return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
+  if (!pkv::prefill_supported(p, n_head))
+    return fail(p, PKV_ERR_UNSUPPORTED, "prefill: shape not supported");
+  if (out_dtype != PKV_F32 && out_dtype != p->dtype)
+    return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
+  DeviceGuard dg(p->device);
+  pkv::PrefillArgs a{q, out, out_dtype, cu_q_lens, context_lens, block_tables,
+                     max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale};
+  hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "prefill launch");
+  return PKV_OK;
+}
+
+int pkv_pool_check(pkv_pool* p) {
+  CHECK_POOL(p);
+  DeviceGuard dg(p->device);
+  uint32_t bits = 0;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(&bits, p->err, 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && bits) e = hipMemset(p->err, 0, 4);
+  if (e != hipSuccess) return hip_fail(p, e, "pool check");
+  if (bits) {
+    std::string what;
+    if (bits & PKV_EBIT_SLOT) what += " slot-out-of-range";
+    if (bits & PKV_EBIT_BLOCK) what += " block-id-out-of-range";
+    if (bits & PKV_EBIT_LENGTH) what += " context-length-out-of-range";
+    return fail(p, PKV_ERR_DEVICE_DATA, "device data errors:%s", what.c_str());
+  }
+  return PKV_OK;
+}
+
+}  // extern "C"

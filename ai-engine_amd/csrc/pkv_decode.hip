@@ -1,0 +1,570 @@
+// pkv_decode.hip -- paged decode attention with fused KV append (gfx950).
+//
+// Replaces, for one layer of a decode step, the reference's per-row
+// KvPool::write + gather_seq + pad + cat + build_mask + sdpa sequence
+// (crates/ai-engine-candle/src/paged/transformer.rs:271-292,
+//  crates/ai-engine-candle/src/paged/attention.rs:11-28,57-136) by one launch.
+//
+// Work decomposition: one wavefront per (sequence b, kv head g, context
+// partition p).  The wave carries the whole GQA query group of g (R query
+// heads h = g*R .. g*R+R-1, attention.rs:128-136) so every K/V byte of the
+// partition is read from HBM exactly once per decode step.
+//
+// Per tile of TILE tokens:
+//   * K: each lane loads 16-byte fragments of its token's row straight from
+//     the block (block-table indirection resolved per 16-token sub-tile with
+//     v_readlane from a per-partition table slice held in one VGPR) into the
+//     B operand of v_mfma_f32_16x16x32_{bf16,f16} (v_mfma_f32_16x16x4f32 for
+//     f32 pools); the Q group is the A operand.  S = Q K^T lands with token =
+//     lane % 16 and head = 4 * (lane / 16) + register.  The four lanes of a
+//     token read 64 contiguous bytes per instruction.
+//   * Online softmax in the exp2 domain (scores pre-multiplied by
+//     scale * log2 e), running max and partial sums per 16-lane row, row
+//     max/sum by DPP row rotations.
+//   * P goes through a 1-2 KB LDS slice of the wave; V is read with fully
+//     coalesced 16-byte loads (consecutive lanes = consecutive 16 bytes of a
+//     row) and P.V is accumulated in fp32 FMAs, so the softmax weights never
+//     lose precision.
+// Split-context: a sequence with n_parts > 1 partitions writes (m, l, O)
+// partials; the last wave of (b, g) to finish (agent-scope atomic counter)
+// merges them with log-sum-exp weights and resets the counter, so a whole
+// layer is one launch and no second pass is needed.
+//
+// Fused append: with k_new/v_new given, the wave owning the last partition
+// of (b, g) stores the new token's K/V row at position context_len-1
+// (slot = table[pos / bs] * bs + pos % bs, block_table.rs:55-58) and uses
+// the new row from the input for that token, i.e. write-then-attend exactly
+// as transformer.rs:276-277.
+#include "pkv_device.h"
+#include "pkv_internal.h"
+
+namespace pkv {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+// Largest decode tile in tokens (K and V of one tile are held in registers
+// while the tile is processed); 64 or 32.
+#ifndef PKV_DECODE_TILE
+#define PKV_DECODE_TILE 64
+#endif
+
+template <int DT, int HD, int R>
+struct DCfg {
+  static constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
+  static constexpr int RB = HD * E;                // row bytes
+  static constexpr int NF = RB / 64;               // QK fragments per lane per row
+  static constexpr int NST0 = 16 / NF;
+  static constexpr int NSTMAX = PKV_DECODE_TILE / 16;
+  static constexpr int NST = NST0 < 1 ? 1 : (NST0 > NSTMAX ? NSTMAX : NST0);  // sub-tiles
+  static constexpr int TILE = 16 * NST;            // tokens per tile
+  static constexpr int CH = RB / 16;               // 16-byte chunks per row
+  static constexpr int TPL = 64 / CH;              // tokens per V load
+  static constexpr int NV = TILE / TPL;            // V loads per tile
+  static constexpr int EPL = 16 / E;               // elements per chunk
+  static constexpr int RP = R <= 4 ? 4 : R;        // LDS pitch of a P row
+  static constexpr int RG = (R + 3) / 4;           // MFMA row groups with heads
+  static_assert(CH <= 64, "row wider than a wave of 16-byte chunks");
+  static_assert(TILE % TPL == 0, "tile/V-load mismatch");
+};
+
+struct DecodeKArgs {
+  char* k_pool;
+  char* v_pool;
+  const char* q;
+  void* out;
+  int out_f32;
+  const int32_t* block_tables;
+  int mbps;
+  const int32_t* context_lens;
+  int max_context_len;
+  int batch;
+  int kvh;
+  int num_blocks;
+  int bs_log2;
+  int part_tokens;
+  int max_parts;
+  float scale_log2;
+  const char* k_new;
+  const char* v_new;
+  float* part_ml;
+  float* part_o;
+  uint32_t* counters;
+  uint32_t* err;
+};
+
+template <int EPL>
+__device__ __forceinline__ void store_out(void* out, size_t elem_off, int out_f32,
+                                          int dt, const float (&x)[EPL]) {
+  if (out_f32) {
+    float* o = reinterpret_cast<float*>(out) + elem_off;
+#pragma unroll
+    for (int i = 0; i < EPL; i += 4)
+      *reinterpret_cast<f32x4*>(o + i) = f32x4{x[i], x[i + 1], x[i + 2], x[i + 3]};
+  } else if (EPL == 8) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo = dt == PKV_BF16 ? f32_to_bf16_bits(x[2 * i]) : f32_to_f16_bits(x[2 * i]);
+      uint32_t hi = dt == PKV_BF16 ? f32_to_bf16_bits(x[2 * i + 1]) : f32_to_f16_bits(x[2 * i + 1]);
+      w[i] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + elem_off) = w;
+  } else {
+    // f32 pool with f32 output is the only EPL == 4 case (handled above);
+    // 16-bit outputs of an f32 pool are rejected on the host.
+  }
+}
+
+template <int DT, int HD, int R>
+__global__ void __launch_bounds__(kWavesPerBlock * kWave)
+    decode_kernel(DecodeKArgs a) {
+  using C = DCfg<DT, HD, R>;
+  __shared__ float p_lds_all[kWavesPerBlock][C::TILE * C::RP];
+
+  // The wave index is uniform within a wave; readfirstlane tells the
+  // compiler so, which keeps every per-wave quantity in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  float* p_lds = p_lds_all[wave];
+
+  const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
+  const int g = (int)(item % a.kvh);
+  const long long bp = item / a.kvh;
+  const int p = (int)(bp % a.max_parts);
+  const int b = (int)(bp / a.max_parts);
+  if (b >= a.batch) return;
+
+  const int H = a.kvh * R;
+  const int BS = 1 << a.bs_log2;
+  int ctx = a.context_lens[b];
+  bool clamped = false;
+  if (ctx > a.max_context_len || ctx > a.mbps * BS || ctx < 0) {
+    if (lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
+    ctx = ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
+    clamped = true;
+  }
+  const int PT = a.part_tokens;
+  const int n_parts = (ctx + PT - 1) / PT;
+  const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
+  const int tg = lane / C::CH;  // token group of a V load
+
+  if (ctx == 0) {
+    if (p == 0 && lane < C::CH) {
+      float z[C::EPL];
+#pragma unroll
+      for (int e = 0; e < C::EPL; ++e) z[e] = 0.0f;
+#pragma unroll
+      for (int h = 0; h < R; ++h)
+        store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
+                          a.out_f32, DT, z);
+    }
+    return;
+  }
+  if (p >= n_parts) return;
+
+  const int t_begin = p * PT;
+  const int t_end = min(ctx, t_begin + PT);
+  const int blk_begin = t_begin >> a.bs_log2;
+  const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= 64 (plan)
+  const int new_pos = (a.k_new != nullptr && !clamped) ? ctx - 1 : -1;
+
+  // Block-table slice of this partition: lane i holds entry blk_begin + i.
+  int tbl = 0;
+  if (lane < nblk) {
+    int e = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
+    if (e < 0 || e >= a.num_blocks) {
+      atomicOr(a.err, PKV_EBIT_BLOCK);
+      e = 0;
+    }
+    tbl = e;
+  }
+
+  const size_t head_off = (size_t)g * C::RB;
+  const size_t slot_stride = (size_t)a.kvh * C::RB;
+  const char* knew_row = a.k_new ? a.k_new + ((size_t)b * a.kvh + g) * C::RB : nullptr;
+  const char* vnew_row = a.v_new ? a.v_new + ((size_t)b * a.kvh + g) * C::RB : nullptr;
+
+  // Fused append: store the new token's row (write before attend).
+  if (new_pos >= 0 && p == n_parts - 1) {
+    int blk = readlane_i(tbl, (new_pos >> a.bs_log2) - blk_begin);
+    size_t off = ((size_t)blk * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
+    if (lane < C::CH) {
+      st16(a.k_pool + off + lane * 16, ld16(knew_row + lane * 16));
+      st16(a.v_pool + off + lane * 16, ld16(vnew_row + lane * 16));
+    }
+  }
+
+  // Loads address a row as a wave-uniform base (pool + head + physical
+  // block, an SGPR pair) plus a 32-bit per-lane offset (slot in block,
+  // 16-byte fragment), which keeps the address math scalar.
+  const char* kh = a.k_pool + head_off;
+  const char* vh = a.v_pool + head_off;
+  const size_t blk_stride = (size_t)BS * slot_stride;
+  const int tmask = BS - 1;
+  const int lg = a.bs_log2;
+
+  // ---- Q group as MFMA A operand: row = head (lane % 16), k-slice lane / 16
+  const int G = lane >> 4;
+  const int col = lane & 15;
+  u32x4 qf[C::NF];
+  {
+    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * C::RB;
+#pragma unroll
+    for (int f = 0; f < C::NF; ++f)
+      qf[f] = col < R ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
+  }
+
+  // K fragments of one tile: sub-tile st, token lane % 16, k-slice lane / 16.
+  // Tokens past t_end are clamped to t_end - 1 (a valid row; their scores are
+  // masked).  The new token's row comes from k_new, not from the pool.
+  auto load_k = [&](u32x4 (&kf)[C::NST][C::NF], int tile_base) {
+#pragma unroll
+    for (int st = 0; st < C::NST; ++st) {
+      const int t0 = min(tile_base + 16 * st, t_end - 1);
+      const int tok = min(tile_base + 16 * st + col, t_end - 1);
+      const uint32_t off = (uint32_t)((tok & tmask) * slot_stride) + 16 * G;
+      // block_size >= 16: the 16 tokens of a sub-tile share one block
+      const char* base = kh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
+#pragma unroll
+      for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(base + off + 64 * f);
+    }
+    if (new_pos >= tile_base && new_pos < tile_base + C::TILE) {
+#pragma unroll
+      for (int st = 0; st < C::NST; ++st) {
+        const int tok = min(tile_base + 16 * st + col, t_end - 1);
+        if (tok == new_pos) {
+#pragma unroll
+          for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(knew_row + 64 * f + 16 * G);
+        }
+      }
+    }
+  };
+  // V chunks of one tile: load i covers TPL consecutive tokens (one block),
+  // lane = (token group tg, 16-byte chunk c): consecutive lanes read
+  // consecutive 16 bytes of a row.
+  auto load_v = [&](u32x4 (&vf)[C::NV], int tile_base) {
+#pragma unroll
+    for (int i = 0; i < C::NV; ++i) {
+      const int t0 = min(tile_base + i * C::TPL, t_end - 1);
+      const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
+      const char* base = vh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
+      vf[i] = ld16(base + (uint32_t)((tok & tmask) * slot_stride) + 16 * c);
+    }
+    if (new_pos >= tile_base && new_pos < tile_base + C::TILE) {
+#pragma unroll
+      for (int i = 0; i < C::NV; ++i) {
+        const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
+        if (tok == new_pos) vf[i] = ld16(vnew_row + 16 * c);
+      }
+    }
+  };
+
+  float m[4], lsum[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m[j] = -INFINITY;
+    lsum[j] = 0.0f;
+  }
+  float o[R][C::EPL];
+#pragma unroll
+  for (int h = 0; h < R; ++h)
+#pragma unroll
+    for (int e = 0; e < C::EPL; ++e) o[h][e] = 0.0f;
+
+  const int ntiles = (t_end - t_begin + C::TILE - 1) / C::TILE;
+  u32x4 kf[C::NST][C::NF];
+  load_k(kf, t_begin);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int tile_base = t_begin + t * C::TILE;
+    u32x4 vf[C::NV];
+    load_v(vf, tile_base);
+
+    f32x4 acc[C::NST];
+#pragma unroll
+    for (int st = 0; st < C::NST; ++st) {
+      acc[st] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int f = 0; f < C::NF; ++f) mfma_frag<DT>(qf[f], kf[st][f], acc[st]);
+    }
+    if (t + 1 < ntiles) load_k(kf, tile_base + C::TILE);
+
+    // ---- online softmax (exp2 domain) ----
+    float sc[C::NST][4];
+#pragma unroll
+    for (int st = 0; st < C::NST; ++st) {
+      bool valid = tile_base + 16 * st + col < t_end;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[st][j] = valid ? acc[st][j] * a.scale_log2 : -INFINITY;
+    }
+    float alpha[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float tmax = sc[0][j];
+#pragma unroll
+      for (int st = 1; st < C::NST; ++st) tmax = fmaxf(tmax, sc[st][j]);
+      tmax = row_max16(tmax);
+      float mnew = fmaxf(m[j], tmax);
+      alpha[j] = fast_exp2(m[j] - mnew);
+      m[j] = mnew;
+      float s = 0.0f;
+#pragma unroll
+      for (int st = 0; st < C::NST; ++st) {
+        sc[st][j] = fast_exp2(sc[st][j] - mnew);
+        s += sc[st][j];
+      }
+      lsum[j] = lsum[j] * alpha[j] + s;
+    }
+    if (G < C::RG) {
+#pragma unroll
+      for (int st = 0; st < C::NST; ++st)
+        *reinterpret_cast<f32x4*>(p_lds + (16 * st + col) * C::RP + 4 * G) =
+            f32x4{sc[st][0], sc[st][1], sc[st][2], sc[st][3]};
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- P.V in fp32 ----
+#pragma unroll
+    for (int h = 0; h < R; ++h) {
+      float ah = readlane_f(alpha[h & 3], 16 * (h >> 2));
+#pragma unroll
+      for (int e = 0; e < C::EPL; ++e) o[h][e] *= ah;
+    }
+#pragma unroll
+    for (int i = 0; i < C::NV; ++i) {
+      const float* pr = p_lds + (i * C::TPL + tg) * C::RP;
+      float ph[R];
+      if constexpr (R >= 4) {
+#pragma unroll
+        for (int h = 0; h < R; h += 4) {
+          f32x4 t4 = *reinterpret_cast<const f32x4*>(pr + h);
+          ph[h] = t4[0];
+          ph[h + 1] = t4[1];
+          ph[h + 2] = t4[2];
+          ph[h + 3] = t4[3];
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < R; ++h) ph[h] = pr[h];
+      }
+      float x[C::EPL];
+      widen16<DT, C::EPL>(vf[i], x);
+#pragma unroll
+      for (int h = 0; h < R; ++h)
+#pragma unroll
+        for (int e = 0; e < C::EPL; ++e) o[h][e] = fmaf(ph[h], x[e], o[h][e]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- partition epilogue ----
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lsum[j] = row_sum16(lsum[j]);
+#pragma unroll
+  for (int h = 0; h < R; ++h)
+#pragma unroll
+    for (int e = 0; e < C::EPL; ++e)
+#pragma unroll
+      for (int mk = C::CH; mk < 64; mk <<= 1) o[h][e] += shfl_xor_f(o[h][e], mk);
+
+  float mh[R], lh[R];
+#pragma unroll
+  for (int h = 0; h < R; ++h) {
+    mh[h] = readlane_f(m[h & 3], 16 * (h >> 2));
+    lh[h] = readlane_f(lsum[h & 3], 16 * (h >> 2));
+  }
+
+  if (n_parts == 1) {
+    if (lane < C::CH) {
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        float inv = 1.0f / lh[h];
+        float x[C::EPL];
+#pragma unroll
+        for (int e = 0; e < C::EPL; ++e) x[e] = o[h][e] * inv;
+        store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
+                          a.out_f32, DT, x);
+      }
+    }
+    return;
+  }
+
+  const size_t pair = (size_t)b * a.kvh + g;
+  float* ml = a.part_ml + (pair * a.max_parts + p) * R * 2;
+  float* po = a.part_o + (pair * a.max_parts + p) * R * HD;
+  if (lane < C::CH) {
+#pragma unroll
+    for (int h = 0; h < R; ++h)
+#pragma unroll
+      for (int e = 0; e < C::EPL; e += 4)
+        *reinterpret_cast<f32x4*>(po + h * HD + c * C::EPL + e) =
+            f32x4{o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]};
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < R; ++h) {
+      ml[2 * h] = mh[h];
+      ml[2 * h + 1] = lh[h];
+    }
+  }
+  __threadfence();
+  uint32_t prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(a.counters + pair, 1u, __ATOMIC_ACQ_REL,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  prev = (uint32_t)readlane_i((int)prev, 0);
+  if (prev != (uint32_t)(n_parts - 1)) return;
+  __threadfence();
+  if (lane == 0)
+    __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- merge the partitions of (b, g) ----
+  const float* mlb = a.part_ml + pair * a.max_parts * R * 2;
+  const float* pob = a.part_o + pair * a.max_parts * R * HD;
+  for (int idx = lane * 4; idx < R * HD; idx += 4 * kWave) {
+    const int h = idx / HD;
+    const int d = idx - h * HD;
+    float M = -INFINITY;
+    for (int pp = 0; pp < n_parts; ++pp) M = fmaxf(M, mlb[(pp * R + h) * 2]);
+    float L = 0.0f;
+    f32x4 acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int pp = 0; pp < n_parts; ++pp) {
+      float w = fast_exp2(mlb[(pp * R + h) * 2] - M);
+      L += w * mlb[(pp * R + h) * 2 + 1];
+      f32x4 v4 = *reinterpret_cast<const f32x4*>(pob + (pp * R + h) * HD + d);
+      acc4 += w * v4;
+    }
+    float inv = 1.0f / L;
+    size_t eo = ((size_t)b * H + g * R + h) * HD + d;
+    if (a.out_f32) {
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) = acc4 * inv;
+    } else {
+      uint32_t w0, w1;
+      if (DT == PKV_BF16) {
+        w0 = f32_to_bf16_bits(acc4[0] * inv) | (f32_to_bf16_bits(acc4[1] * inv) << 16);
+        w1 = f32_to_bf16_bits(acc4[2] * inv) | (f32_to_bf16_bits(acc4[3] * inv) << 16);
+      } else {
+        w0 = f32_to_f16_bits(acc4[0] * inv) | (f32_to_f16_bits(acc4[1] * inv) << 16);
+        w1 = f32_to_f16_bits(acc4[2] * inv) | (f32_to_f16_bits(acc4[3] * inv) << 16);
+      }
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + eo);
+      o32[0] = w0;
+      o32[1] = w1;
+    }
+  }
+}
+
+template <int DT, int HD, int R>
+hipError_t launch_t(const DecodeKArgs& k, long long items, hipStream_t s) {
+  unsigned grid = (unsigned)((items + kWavesPerBlock - 1) / kWavesPerBlock);
+  decode_kernel<DT, HD, R><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  return hipGetLastError();
+}
+
+template <int DT, int HD>
+hipError_t launch_r(int R, const DecodeKArgs& k, long long items, hipStream_t s) {
+  switch (R) {
+    case 1: return launch_t<DT, HD, 1>(k, items, s);
+    case 2: return launch_t<DT, HD, 2>(k, items, s);
+    case 4: return launch_t<DT, HD, 4>(k, items, s);
+    case 8: return launch_t<DT, HD, 8>(k, items, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DT>
+hipError_t launch_hd(int HD, int R, const DecodeKArgs& k, long long items, hipStream_t s) {
+  switch (HD) {
+    case 64: return launch_r<DT, 64>(R, k, items, s);
+    case 128: return launch_r<DT, 128>(R, k, items, s);
+    case 256: return launch_r<DT, 256>(R, k, items, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int ilog2i(int x) {
+  int r = 0;
+  while ((1 << r) < x) ++r;
+  return r;
+}
+
+}  // namespace
+
+bool decode_supported(const pkv_pool* p, int n_head) {
+  if (n_head <= 0 || n_head % p->n_kv_head != 0) return false;
+  int R = n_head / p->n_kv_head;
+  if (R != 1 && R != 2 && R != 4 && R != 8) return false;
+  return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
+}
+
+void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
+                 int* part_tokens, int* max_parts) {
+  (void)n_head;
+  long long pairs = (long long)batch * p->n_kv_head;
+  int mc = max_context_len > 0 ? max_context_len : 1;
+  // Partition length: 256 tokens (64 KB of K+V per bf16 head of 128) keeps
+  // partial traffic ~3% of the K/V stream; shorter partitions are used when
+  // the batch is too small to give every CU several waves.
+  int pt = 256;
+  while (pt > 64 && pairs * ((mc + pt - 1) / pt) < 4096) pt >>= 1;
+  // The per-partition table slice must fit one wave (<= 64 block ids).
+  while (pt > 64 && (pt >> ilog2i(p->block_size)) + 1 > 64) pt >>= 1;
+  *part_tokens = pt;
+  *max_parts = (mc + pt - 1) / pt;
+}
+
+size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
+                              int max_context_len, size_t* counter_bytes) {
+  int pt = 0, mp = 0;
+  decode_plan(p, batch, n_head, max_context_len, &pt, &mp);
+  size_t pairs = (size_t)batch * p->n_kv_head;
+  size_t R = (size_t)(n_head / p->n_kv_head);
+  size_t cb = ((pairs * 4 + 255) / 256) * 256;
+  if (counter_bytes) *counter_bytes = cb;
+  if (mp <= 1) return cb;
+  size_t ml = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
+  size_t po = pairs * mp * R * (size_t)p->head_dim * 4;
+  return cb + ml + po;
+}
+
+hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
+                         hipStream_t stream) {
+  int pt = 0, mp = 0;
+  decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
+  size_t pairs = (size_t)a.batch * p->n_kv_head;
+  int R = a.n_head / p->n_kv_head;
+  DecodeKArgs k{};
+  k.k_pool = p->layer_k(layer);
+  k.v_pool = p->layer_v(layer);
+  k.q = reinterpret_cast<const char*>(a.q);
+  k.out = a.out;
+  k.out_f32 = a.out_dtype == PKV_F32;
+  k.block_tables = a.block_tables;
+  k.mbps = a.max_blocks_per_seq;
+  k.context_lens = a.context_lens;
+  k.max_context_len = a.max_context_len;
+  k.batch = a.batch;
+  k.kvh = p->n_kv_head;
+  k.num_blocks = p->num_blocks;
+  k.bs_log2 = ilog2i(p->block_size);
+  k.part_tokens = pt;
+  k.max_parts = mp;
+  k.scale_log2 = a.scale * 1.4426950408889634f;
+  k.k_new = reinterpret_cast<const char*>(a.k_new);
+  k.v_new = reinterpret_cast<const char*>(a.v_new);
+  k.counters = reinterpret_cast<uint32_t*>(p->ws);
+  size_t cb = p->ws_counter_bytes;
+  size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
+  k.part_ml = reinterpret_cast<float*>(p->ws + cb);
+  k.part_o = reinterpret_cast<float*>(p->ws + cb + ml_bytes);
+  k.err = p->err;
+  long long items = (long long)pairs * mp;
+  switch (p->dtype) {
+    case PKV_F32: return launch_hd<PKV_F32>(p->head_dim, R, k, items, stream);
+    case PKV_F16: return launch_hd<PKV_F16>(p->head_dim, R, k, items, stream);
+    default: return launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream);
+  }
+}
+
+}  // namespace pkv

@@ -1,0 +1,114 @@
+// pkv_internal.h -- definitions shared by the C-ABI host code and the HIP
+// kernels of libpagedkv (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/pagedkv.h"
+
+// One handle = the reference's Vec<KvPool> (engine.rs:70-72).  Device memory
+// is a single slab laid out [layer][K|V][num_blocks][block_size][n_kv][hd].
+struct pkv_pool {
+  int n_layers = 0;
+  int num_blocks = 0;
+  int block_size = 0;
+  int n_kv_head = 0;
+  int head_dim = 0;
+  int dtype = 0;
+  int device = 0;
+  size_t elem_bytes = 0;
+  size_t row_bytes = 0;    // one (slot, kv head) row: head_dim * elem_bytes
+  size_t block_bytes = 0;  // one block of one layer's K (or V)
+  size_t layer_bytes = 0;  // one layer's K (or V): num_blocks * block_bytes
+  char* base = nullptr;    // device slab
+  uint32_t* err = nullptr; // device error word, bit set by kernels
+  // decode workspace: [counters][partials]; counters stay zero between calls
+  char* ws = nullptr;
+  size_t ws_bytes = 0;
+  size_t ws_counter_bytes = 0;
+  std::string last_error;
+
+  char* layer_k(int layer) const {
+    return base + (size_t)layer * 2 * layer_bytes;
+  }
+  char* layer_v(int layer) const { return layer_k(layer) + layer_bytes; }
+};
+
+// Device error bits (pkv_pool::err).
+enum : uint32_t {
+  PKV_EBIT_SLOT = 1u,      // append/gather slot out of range
+  PKV_EBIT_BLOCK = 2u,     // block table entry out of range
+  PKV_EBIT_LENGTH = 4u,    // context length beyond max_context_len / table
+};
+
+namespace pkv {
+
+inline size_t dtype_bytes(int dt) { return dt == PKV_F32 ? 4 : 2; }
+
+// Launchers (defined in the .hip files).  They validate nothing that the
+// C-ABI layer already validated, return hipError_t and enqueue on `stream`.
+hipError_t launch_append(const pkv_pool* p, int layer, const void* k,
+                         const void* v, const int32_t* slots, int n,
+                         hipStream_t stream);
+hipError_t launch_gather(const pkv_pool* p, int layer, const int32_t* table,
+                         int len, void* out_k, void* out_v,
+                         hipStream_t stream);
+hipError_t launch_copy_blocks(const pkv_pool* p, const int32_t* src,
+                              const int32_t* dst, int n, hipStream_t stream);
+// Compaction: ops[] holds (src, dst) pairs executed in order within each
+// chain; chain c is ops[chain_start[c] .. chain_start[c+1]).  src == -1
+// reads the chain's held copy, dst == -1 stores into it (cycles).
+hipError_t launch_compact(const pkv_pool* p, const int32_t* ops,
+                          const int32_t* chain_start, int n_chains,
+                          hipStream_t stream);
+hipError_t launch_fill_normal(const pkv_pool* p, uint64_t seed,
+                              hipStream_t stream);
+
+struct DecodeArgs {
+  const void* q;
+  void* out;
+  int out_dtype;
+  const int32_t* block_tables;
+  int max_blocks_per_seq;
+  const int32_t* context_lens;
+  int max_context_len;
+  int batch;
+  int n_head;
+  float scale;
+  const void* k_new;
+  const void* v_new;
+};
+
+// Partition length (tokens) and number of partitions the decode kernel uses
+// for a launch; both are functions of the pool shape and the arguments only.
+void decode_plan(const pkv_pool* p, int batch, int n_head,
+                 int max_context_len, int* part_tokens, int* max_parts);
+size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
+                              int max_context_len, size_t* counter_bytes);
+bool decode_supported(const pkv_pool* p, int n_head);
+hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
+                         hipStream_t stream);
+
+struct PrefillArgs {
+  const void* q;
+  void* out;
+  int out_dtype;
+  const int32_t* cu_q_lens;
+  const int32_t* context_lens;
+  const int32_t* block_tables;
+  int max_blocks_per_seq;
+  int n_seqs;
+  int max_q_len;
+  int max_context_len;
+  int n_head;
+  float scale;
+};
+bool prefill_supported(const pkv_pool* p, int n_head);
+hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
+                          hipStream_t stream);
+
+}  // namespace pkv

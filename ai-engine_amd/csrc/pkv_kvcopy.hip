@@ -1,0 +1,262 @@
+// pkv_kvcopy.hip -- byte-moving kernels of the paged KV pool (gfx950):
+//   append/scatter (KvPool::write, attention.rs:57-83),
+//   gather (KvPool::gather_seq, attention.rs:85-97),
+//   block copy (copy-on-write) and in-place compaction (no reference
+//   counterpart), and a counter-based N(0,1) fill for benchmarks.
+//
+// All of them are HBM-bound streams of 16-byte vectors: every thread moves
+// whole 16-byte chunks, consecutive lanes touch consecutive chunks, and each
+// thread issues all of its loads before its stores so that several requests
+// are in flight per lane.  Rows are head_dim * elem_bytes >= 128 bytes, so a
+// token row is always a whole number of 16-byte chunks.
+#include "pkv_device.h"
+#include "pkv_internal.h"
+
+namespace pkv {
+namespace {
+
+constexpr int kCopyThreads = 256;
+
+// One thread per 16-byte chunk of a token row; K and V in the same thread.
+__global__ void __launch_bounds__(kCopyThreads)
+    append_kernel(u32x4* __restrict__ kp, u32x4* __restrict__ vp,
+                  const u32x4* __restrict__ k, const u32x4* __restrict__ v,
+                  const int32_t* __restrict__ slots, int n, int row_vec,
+                  long long n_slots, uint32_t* err) {
+  long long i = (long long)blockIdx.x * kCopyThreads + threadIdx.x;
+  if (i >= (long long)n * row_vec) return;
+  int t = (int)(i / row_vec);
+  int c = (int)(i - (long long)t * row_vec);
+  int s = slots[t];
+  if (s < 0) return;  // padding token
+  if (s >= n_slots) {
+    if (c == 0) atomicOr(err, PKV_EBIT_SLOT);
+    return;
+  }
+  u32x4 a = k[i];
+  u32x4 b = v[i];
+  size_t o = (size_t)s * row_vec + c;
+  kp[o] = a;
+  vp[o] = b;
+}
+
+// out[p] = pool[blocks[p / bs] * bs + p % bs], K and V.
+__global__ void __launch_bounds__(kCopyThreads)
+    gather_kernel(const u32x4* __restrict__ kp, const u32x4* __restrict__ vp,
+                  u32x4* __restrict__ ok, u32x4* __restrict__ ov,
+                  const int32_t* __restrict__ table, int len, int row_vec,
+                  int bs_log2, int num_blocks, uint32_t* err) {
+  long long i = (long long)blockIdx.x * kCopyThreads + threadIdx.x;
+  if (i >= (long long)len * row_vec) return;
+  int p = (int)(i / row_vec);
+  int c = (int)(i - (long long)p * row_vec);
+  int blk = table[p >> bs_log2];
+  if (blk < 0 || blk >= num_blocks) {
+    if (c == 0) atomicOr(err, PKV_EBIT_BLOCK);
+    ok[i] = u32x4{0, 0, 0, 0};
+    ov[i] = u32x4{0, 0, 0, 0};
+    return;
+  }
+  size_t s = ((size_t)blk << bs_log2) + (p & ((1 << bs_log2) - 1));
+  size_t o = s * row_vec + c;
+  u32x4 a = kp[o];
+  u32x4 b = vp[o];
+  ok[i] = a;
+  ov[i] = b;
+}
+
+// Copy-on-write: grid.x = n pairs, grid.y = 2 * n_layers (K/V slabs),
+// grid.z = chunks of a block.  Each thread moves kVecPerThread chunks.
+constexpr int kVecPerThread = 8;
+
+__global__ void __launch_bounds__(kCopyThreads)
+    copy_blocks_kernel(char* __restrict__ base, size_t layer_bytes,
+                       int block_vec, const int32_t* __restrict__ src,
+                       const int32_t* __restrict__ dst, int num_blocks,
+                       uint32_t* err) {
+  int pair = blockIdx.x;
+  int s = src[pair], d = dst[pair];
+  if (s < 0 || d < 0 || s >= num_blocks || d >= num_blocks) {
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+      atomicOr(err, PKV_EBIT_BLOCK);
+    return;
+  }
+  char* slab = base + (size_t)blockIdx.y * layer_bytes;
+  const u32x4* from = reinterpret_cast<const u32x4*>(slab) + (size_t)s * block_vec;
+  u32x4* to = reinterpret_cast<u32x4*>(slab) + (size_t)d * block_vec;
+  int v0 = blockIdx.z * (kCopyThreads * kVecPerThread) + threadIdx.x;
+  u32x4 r[kVecPerThread];
+#pragma unroll
+  for (int j = 0; j < kVecPerThread; ++j) {
+    int v = v0 + j * kCopyThreads;
+    if (v < block_vec) r[j] = from[v];
+  }
+#pragma unroll
+  for (int j = 0; j < kVecPerThread; ++j) {
+    int v = v0 + j * kCopyThreads;
+    if (v < block_vec) to[v] = r[j];
+  }
+}
+
+// In-place compaction.  grid.x = chain, grid.y = 2 * n_layers, grid.z =
+// chunk of a block.  Each thread owns the same byte range of every block in
+// its chain and performs the chain's moves in order, so a block's old bytes
+// are read (by the same thread, same address) before they are overwritten;
+// no cross-thread ordering is needed.  A cycle's first move parks one block
+// in registers (dst == -1) and its last move writes it back (src == -1).
+__global__ void __launch_bounds__(kCopyThreads)
+    compact_kernel(char* __restrict__ base, size_t layer_bytes, int block_vec,
+                   const int32_t* __restrict__ ops,
+                   const int32_t* __restrict__ chain_start) {
+  int c = blockIdx.x;
+  int o0 = chain_start[c], o1 = chain_start[c + 1];
+  char* slab = base + (size_t)blockIdx.y * layer_bytes;
+  u32x4* pool = reinterpret_cast<u32x4*>(slab);
+  int v0 = blockIdx.z * (kCopyThreads * kVecPerThread) + threadIdx.x;
+  u32x4 held[kVecPerThread];
+  u32x4 r[kVecPerThread];
+  for (int o = o0; o < o1; ++o) {
+    int s = ops[2 * o], d = ops[2 * o + 1];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      int v = v0 + j * kCopyThreads;
+      if (v < block_vec) r[j] = s >= 0 ? pool[(size_t)s * block_vec + v] : held[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      int v = v0 + j * kCopyThreads;
+      if (v < block_vec) {
+        if (d >= 0)
+          pool[(size_t)d * block_vec + v] = r[j];
+        else
+          held[j] = r[j];
+      }
+    }
+  }
+}
+
+// SplitMix64 finaliser (Steele, Lea, Flood 2014) as a counter-based hash.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// N(0,1) by Box-Muller from two 32-bit uniforms of one hash.
+__device__ __forceinline__ float normal_at(uint64_t seed, uint64_t idx) {
+  uint64_t h = mix64(seed + 0x9e3779b97f4a7c15ull * (idx + 1));
+  float u1 = ((uint32_t)(h >> 40) + 1) * (1.0f / 16777217.0f);  // (0,1]
+  float u2 = (uint32_t)(h & 0xffffffu) * (1.0f / 16777216.0f);
+  return sqrtf(-2.0f * __logf(u1)) * __cosf(6.28318530718f * u2);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kCopyThreads)
+    fill_normal_kernel(char* __restrict__ base, size_t n_elems, uint64_t seed) {
+  // Each thread writes one 16-byte chunk (4 or 8 elements).
+  constexpr int EPL = DT == PKV_F32 ? 4 : 8;
+  size_t chunk = (size_t)blockIdx.x * kCopyThreads + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * kCopyThreads;
+  for (; chunk * EPL < n_elems; chunk += stride) {
+    u32x4 w;
+    if constexpr (DT == PKV_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = __float_as_uint(normal_at(seed, chunk * 4 + i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = normal_at(seed, chunk * 8 + 2 * i);
+        float b = normal_at(seed, chunk * 8 + 2 * i + 1);
+        uint32_t lo = DT == PKV_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);
+        uint32_t hi = DT == PKV_BF16 ? f32_to_bf16_bits(b) : f32_to_f16_bits(b);
+        w[i] = lo | (hi << 16);
+      }
+    }
+    reinterpret_cast<u32x4*>(base)[chunk] = w;
+  }
+}
+
+int ilog2(int x) {
+  int r = 0;
+  while ((1 << r) < x) ++r;
+  return r;
+}
+
+}  // namespace
+
+hipError_t launch_append(const pkv_pool* p, int layer, const void* k,
+                         const void* v, const int32_t* slots, int n,
+                         hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
+  long long total = (long long)n * row_vec;
+  unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
+  append_kernel<<<grid, kCopyThreads, 0, stream>>>(
+      reinterpret_cast<u32x4*>(p->layer_k(layer)),
+      reinterpret_cast<u32x4*>(p->layer_v(layer)),
+      reinterpret_cast<const u32x4*>(k), reinterpret_cast<const u32x4*>(v),
+      slots, n, row_vec, (long long)p->num_blocks * p->block_size, p->err);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const pkv_pool* p, int layer, const int32_t* table,
+                         int len, void* out_k, void* out_v,
+                         hipStream_t stream) {
+  if (len <= 0) return hipSuccess;
+  int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
+  long long total = (long long)len * row_vec;
+  unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
+  gather_kernel<<<grid, kCopyThreads, 0, stream>>>(
+      reinterpret_cast<const u32x4*>(p->layer_k(layer)),
+      reinterpret_cast<const u32x4*>(p->layer_v(layer)),
+      reinterpret_cast<u32x4*>(out_k), reinterpret_cast<u32x4*>(out_v), table,
+      len, row_vec, ilog2(p->block_size), p->num_blocks, p->err);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_blocks(const pkv_pool* p, const int32_t* src,
+                              const int32_t* dst, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  int block_vec = (int)(p->block_bytes / 16);
+  int per_block = kCopyThreads * kVecPerThread;
+  dim3 grid((unsigned)n, (unsigned)(2 * p->n_layers),
+            (unsigned)((block_vec + per_block - 1) / per_block));
+  copy_blocks_kernel<<<grid, kCopyThreads, 0, stream>>>(
+      p->base, p->layer_bytes, block_vec, src, dst, p->num_blocks, p->err);
+  return hipGetLastError();
+}
+
+hipError_t launch_compact(const pkv_pool* p, const int32_t* ops,
+                          const int32_t* chain_start, int n_chains,
+                          hipStream_t stream) {
+  if (n_chains <= 0) return hipSuccess;
+  int block_vec = (int)(p->block_bytes / 16);
+  int per_block = kCopyThreads * kVecPerThread;
+  dim3 grid((unsigned)n_chains, (unsigned)(2 * p->n_layers),
+            (unsigned)((block_vec + per_block - 1) / per_block));
+  compact_kernel<<<grid, kCopyThreads, 0, stream>>>(
+      p->base, p->layer_bytes, block_vec, ops, chain_start);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(const pkv_pool* p, uint64_t seed,
+                              hipStream_t stream) {
+  size_t total_bytes = p->layer_bytes * 2 * (size_t)p->n_layers;
+  size_t n_elems = total_bytes / p->elem_bytes;
+  unsigned grid = 8192;
+  switch (p->dtype) {
+    case PKV_F32:
+      fill_normal_kernel<PKV_F32><<<grid, kCopyThreads, 0, stream>>>(p->base, n_elems, seed);
+      break;
+    case PKV_F16:
+      fill_normal_kernel<PKV_F16><<<grid, kCopyThreads, 0, stream>>>(p->base, n_elems, seed);
+      break;
+    default:
+      fill_normal_kernel<PKV_BF16><<<grid, kCopyThreads, 0, stream>>>(p->base, n_elems, seed);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pkv

@@ -1,0 +1,346 @@
+"""pagedkv -- Python front end of libpagedkv, the MI355X paged-KV engine.
+
+Mirrors the reference's host API of the candle `engine = "paged"` path
+(crates/ai-engine-candle/src/paged/{block_table,attention}.rs) on top of the
+C ABI in include/pagedkv.h:
+
+  BlockAllocator / BlockTable   block_table.rs:5-58 (C++ host code)
+  PagedKvCache                  the reference's Vec<KvPool> (engine.rs:70-72)
+  PagedKvCache.layer(l) -> KvPool  KvPool::{write, gather_seq} (attention.rs:39-97)
+  KvPool.decode_attention       build_mask + sdpa of the decode step
+                                (attention.rs:11-28,100-136, transformer.rs:271-292)
+  KvPool.prefill_attention      prefill_seq's attention (transformer.rs:139-196)
+
+torch tensors are used only as device memory and for the current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Sequence
+
+from ._lib import (BF16, F16, F32, K, V, CapacityError, PagedKvError, check, lib,
+                   LIB_PATH)
+
+__all__ = [
+    "BlockAllocator", "BlockTable", "PagedKvCache", "KvPool", "CapacityError",
+    "PagedKvError", "F32", "F16", "BF16", "lib", "LIB_PATH", "torch_dtype",
+    "pkv_dtype",
+]
+
+
+# ---------------------------------------------------------------------------
+# host block bookkeeping (C++), block_table.rs:5-58
+# ---------------------------------------------------------------------------
+class BlockTable:
+    """One sequence's ordered physical block ids (block_table.rs:10-14)."""
+
+    def __init__(self) -> None:
+        self._h = lib().pkv_table_new()
+        if not self._h:
+            raise MemoryError("pkv_table_new")
+
+    def __del__(self) -> None:
+        h = getattr(self, "_h", None)
+        if h:
+            lib().pkv_table_free(h)
+            self._h = None
+
+    @property
+    def blocks(self) -> list[int]:
+        n = lib().pkv_table_len(self._h)
+        if n == 0:
+            return []
+        ptr = lib().pkv_table_blocks(self._h)
+        return [ptr[i] for i in range(n)]
+
+    def __len__(self) -> int:
+        return int(lib().pkv_table_len(self._h))
+
+
+class BlockAllocator:
+    """Fixed-size block pool with a LIFO free list (block_table.rs:16-58)."""
+
+    def __init__(self, num_blocks: int, block_size: int) -> None:
+        self._h = lib().pkv_allocator_new(num_blocks, block_size)
+        if not self._h:
+            raise ValueError("pkv_allocator_new: bad arguments or out of memory")
+        self.block_size = block_size
+
+    def __del__(self) -> None:
+        h = getattr(self, "_h", None)
+        if h:
+            lib().pkv_allocator_free(h)
+            self._h = None
+
+    def free_count(self) -> int:
+        return int(lib().pkv_allocator_free_count(self._h))
+
+    def blocks_for(self, n_tokens: int) -> int:
+        return int(lib().pkv_allocator_blocks_for(self._h, n_tokens))
+
+    def ensure_capacity(self, table: BlockTable, n_tokens: int) -> None:
+        """Raises CapacityError (nothing allocated) when the pool is short."""
+        check(lib().pkv_allocator_ensure_capacity(self._h, table._h, n_tokens))
+
+    def release(self, table: BlockTable) -> None:
+        lib().pkv_allocator_release(self._h, table._h)
+
+    def locate(self, table: BlockTable, pos: int) -> tuple[int, int]:
+        blk = ctypes.c_uint32()
+        slot = ctypes.c_size_t()
+        rc = lib().pkv_allocator_locate(self._h, table._h, pos, ctypes.byref(blk),
+                                        ctypes.byref(slot))
+        if rc != 0:
+            raise IndexError(f"position {pos} beyond the block table")
+        return int(blk.value), int(slot.value)
+
+    def slot(self, table: BlockTable, pos: int) -> int:
+        b, s = self.locate(table, pos)
+        return b * self.block_size + s
+
+
+# ---------------------------------------------------------------------------
+# device pool
+# ---------------------------------------------------------------------------
+def pkv_dtype(t) -> int:
+    import torch
+    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+    if t not in m:
+        raise TypeError(f"unsupported dtype {t}")
+    return m[t]
+
+
+def torch_dtype(d: int):
+    import torch
+    return {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[d]
+
+
+def _stream_ptr(stream) -> int | None:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream) or None
+
+
+def _dev_ptr(t) -> int:
+    return int(t.data_ptr())
+
+
+def _i32(x, device):
+    import torch
+    if isinstance(x, torch.Tensor):
+        t = x.to(device=device, dtype=torch.int32)
+    else:
+        t = torch.as_tensor(x, dtype=torch.int32).to(device)
+    return t.contiguous()
+
+
+class PagedKvCache:
+    """K/V pools of every layer on one GPU (the reference's Vec<KvPool>,
+    engine.rs:70-72; KvPool::new, attention.rs:39-55).  Zero-initialised,
+    layout [layer][K|V][num_blocks][block_size][n_kv_head][head_dim]."""
+
+    def __init__(self, n_layers: int, num_blocks: int, block_size: int, n_kv_head: int,
+                 head_dim: int, dtype=None, device: int = 0) -> None:
+        import torch
+        if dtype is None:
+            dtype = torch.float32
+        self.dtype = dtype
+        self.n_layers, self.num_blocks, self.block_size = n_layers, num_blocks, block_size
+        self.n_kv_head, self.head_dim, self.device_index = n_kv_head, head_dim, device
+        self.device = torch.device("cuda", device)
+        h = ctypes.c_void_p()
+        rc = lib().pkv_pool_create(ctypes.byref(h), n_layers, num_blocks, block_size,
+                                   n_kv_head, head_dim, pkv_dtype(dtype), device)
+        check(rc, None)
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        h = getattr(self, "_h", None)
+        if h:
+            lib().pkv_pool_destroy(h)
+            self._h = None
+
+    def __del__(self) -> None:
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def layer(self, l: int) -> "KvPool":
+        if not 0 <= l < self.n_layers:
+            raise IndexError(l)
+        return KvPool(self, l)
+
+    @property
+    def layer_bytes(self) -> int:
+        return int(lib().pkv_pool_layer_bytes(self._h))
+
+    @property
+    def block_bytes(self) -> int:
+        return self.layer_bytes // self.num_blocks
+
+    def fill_normal(self, seed: int, stream=None) -> None:
+        check(lib().pkv_pool_fill_normal(self._h, seed, _stream_ptr(stream)), self._h)
+
+    def copy_blocks(self, src, dst, stream=None) -> None:
+        """Copy-on-write: block dst[i] <- src[i] in every layer, K and V."""
+        s = _i32(src, self.device)
+        d = _i32(dst, self.device)
+        if s.numel() != d.numel():
+            raise ValueError("src/dst length mismatch")
+        check(lib().pkv_copy_blocks(self._h, _dev_ptr(s), _dev_ptr(d), s.numel(),
+                                    _stream_ptr(stream)), self._h)
+
+    def compact(self, src: Sequence[int], dst: Sequence[int], stream=None) -> None:
+        """In-place block moves src[i] -> dst[i] (sets may overlap)."""
+        import numpy as np
+        s = np.ascontiguousarray(src, dtype=np.int32)
+        d = np.ascontiguousarray(dst, dtype=np.int32)
+        if s.size != d.size:
+            raise ValueError("src/dst length mismatch")
+        P = ctypes.POINTER(ctypes.c_int32)
+        check(lib().pkv_compact(self._h, s.ctypes.data_as(P), d.ctypes.data_as(P), s.size,
+                                _stream_ptr(stream)), self._h)
+
+    def check(self) -> None:
+        """Raise if a kernel met an out-of-range id or length since last check."""
+        check(lib().pkv_pool_check(self._h), self._h)
+
+    def reserve_decode(self, batch: int, n_head: int, max_context_len: int) -> None:
+        check(lib().pkv_pool_reserve_decode(self._h, batch, n_head, max_context_len), self._h)
+
+    # raw byte access (synchronous), for tests and checkpoints
+    def read_bytes(self, layer: int, which: int, offset: int = 0, nbytes: int | None = None):
+        import numpy as np
+        if nbytes is None:
+            nbytes = self.layer_bytes - offset
+        buf = np.empty(nbytes, dtype=np.uint8)
+        check(lib().pkv_pool_read(self._h, layer, which, offset, nbytes, buf.ctypes.data), self._h)
+        return buf
+
+    def write_bytes(self, layer: int, which: int, data, offset: int = 0) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        check(lib().pkv_pool_write(self._h, layer, which, offset, a.ctypes.data, a.size), self._h)
+
+
+class KvPool:
+    """One layer of a PagedKvCache: the reference's KvPool (attention.rs:30-98)."""
+
+    def __init__(self, cache: PagedKvCache, layer: int) -> None:
+        self.cache = cache
+        self.layer_index = layer
+
+    @property
+    def _h(self):
+        return self.cache.handle
+
+    # -- KvPool::write (attention.rs:57-83) --------------------------------
+    def write(self, alloc: BlockAllocator, table: BlockTable, start_pos: int, k, v,
+              stream=None) -> None:
+        n_new = int(k.shape[0])
+        slots = [alloc.slot(table, start_pos + i) for i in range(n_new)]
+        self.append(k, v, slots, stream)
+
+    def append(self, k, v, slot_mapping, stream=None) -> None:
+        """Scatter k, v (n, n_kv, hd) to the given slots (int32, -1 = skip)."""
+        c = self.cache
+        self._check_rows(k, "k")
+        self._check_rows(v, "v")
+        sm = _i32(slot_mapping, c.device)
+        if sm.numel() != k.shape[0] or v.shape[0] != k.shape[0]:
+            raise ValueError("slot_mapping / k / v lengths differ")
+        check(lib().pkv_append(self._h, self.layer_index, _dev_ptr(k), _dev_ptr(v),
+                               _dev_ptr(sm), k.shape[0], _stream_ptr(stream)), self._h)
+
+    # -- KvPool::gather_seq (attention.rs:85-97) ----------------------------
+    def gather_seq(self, table, length: int, stream=None):
+        import torch
+        c = self.cache
+        blocks = table.blocks if isinstance(table, BlockTable) else list(table)
+        need = -(-length // c.block_size)
+        if need > len(blocks):
+            raise IndexError("length beyond the block table")
+        tb = _i32(blocks[:max(need, 1)] if blocks else [0], c.device)
+        ok = torch.empty((length, c.n_kv_head, c.head_dim), dtype=c.dtype, device=c.device)
+        ov = torch.empty_like(ok)
+        check(lib().pkv_gather_seq(self._h, self.layer_index, _dev_ptr(tb), length,
+                                   _dev_ptr(ok), _dev_ptr(ov), _stream_ptr(stream)), self._h)
+        return ok, ov
+
+    # -- decode attention ---------------------------------------------------
+    def decode_attention(self, q, block_tables, context_lens, max_context_len: int | None = None,
+                         k_new=None, v_new=None, scale: float | None = None, out_dtype=None,
+                         out=None, stream=None):
+        """q: (B, H, hd); block_tables: (B, max_nb) int32 device; context_lens:
+        (B,) int32 device = keys attended (seq_lens + 1).  With k_new/v_new
+        (B, n_kv, hd) the new token is stored at position context_lens-1 first.
+        Returns (B, H*hd)."""
+        import torch
+        c = self.cache
+        B, H, hd = q.shape
+        if hd != c.head_dim:
+            raise ValueError("head_dim mismatch")
+        if out_dtype is None:
+            out_dtype = q.dtype
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        bt = _i32(block_tables, c.device)
+        cl = _i32(context_lens, c.device)
+        if max_context_len is None:
+            max_context_len = int(cl.max().item()) if B else 1
+        if out is None:
+            out = torch.empty((B, H * hd), dtype=out_dtype, device=c.device)
+        if k_new is not None:
+            self._check_rows(k_new, "k_new")
+            self._check_rows(v_new, "v_new")
+        qq = q.contiguous()
+        if qq.dtype != c.dtype:
+            raise TypeError("q must have the pool dtype")
+        check(lib().pkv_decode_attention(
+            self._h, self.layer_index, _dev_ptr(qq), _dev_ptr(out), pkv_dtype(out.dtype),
+            _dev_ptr(bt), bt.shape[1], _dev_ptr(cl), int(max_context_len), B, H, float(scale),
+            _dev_ptr(k_new) if k_new is not None else None,
+            _dev_ptr(v_new) if v_new is not None else None, _stream_ptr(stream)), self._h)
+        return out
+
+    # -- chunked prefill attention -------------------------------------------
+    def prefill_attention(self, q, cu_q_lens, context_lens, block_tables, max_q_len: int,
+                          max_context_len: int, scale: float | None = None, out_dtype=None,
+                          out=None, stream=None):
+        import torch
+        c = self.cache
+        T, H, hd = q.shape
+        if out_dtype is None:
+            out_dtype = q.dtype
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        cu = _i32(cu_q_lens, c.device)
+        cl = _i32(context_lens, c.device)
+        bt = _i32(block_tables, c.device)
+        if out is None:
+            out = torch.empty((T, H * hd), dtype=out_dtype, device=c.device)
+        check(lib().pkv_prefill_attention(
+            self._h, self.layer_index, _dev_ptr(q.contiguous()), _dev_ptr(out),
+            pkv_dtype(out.dtype), _dev_ptr(cu), _dev_ptr(cl), _dev_ptr(bt), bt.shape[1],
+            cl.numel(), int(max_q_len), int(max_context_len), H, float(scale),
+            _stream_ptr(stream)), self._h)
+        return out
+
+    def _check_rows(self, t, name: str) -> None:
+        c = self.cache
+        if t.dtype != c.dtype:
+            raise TypeError(f"{name} must have the pool dtype {c.dtype}")
+        if t.dim() != 3 or t.shape[1] != c.n_kv_head or t.shape[2] != c.head_dim:
+            raise ValueError(f"{name} must be (n, {c.n_kv_head}, {c.head_dim})")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")

@@ -1,0 +1,250 @@
+"""Benchmark: paged decode attention + KV append on one MI355X.
+
+A step is one decode step of the BASELINE.json north-star workload
+(configs[2], Llama-3-8B shape): for each of the 32 layers, every one of the
+256 sequences appends its new K/V token and attends over its whole context
+(seq_len + 1 keys) -- one pkv_decode_attention launch per layer.  Inputs are
+resident in HBM before the timed region.
+
+Prints ONE JSON line (rank 0).  `value` = tokens/s = batch / step time;
+`roofline` = the decode kernel's algorithmic bytes per launch over its
+average launch duration (HIP events on the launch stream) against the 8 TB/s
+HBM peak; `cpu_baseline` = the oracle's CPU restatement of the reference
+decode math timed on this host on a bounded sample (see --cpu-layers).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "ai-engine_amd"), os.path.join(ROOT, "oracle")]
+
+METRIC = "decode attn+KV-append tokens/s and achieved HBM GB/s, Llama-3-8B shape, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (shape attr, batch, ctx_lo, ctx_hi, description)
+    "cfg1": ("CFG1", 8, 128, 1024, "Llama-3.2-1B decode: 16 layers, 32q/8kv heads, hd 64, bs 16, "
+             "f16 KV, B=8, ctx U[128,1024], 2048 blocks/layer"),
+    "cfg2d": ("CFG2", 56, 256, 2048, "TinyLlama-1.1B decode part: 22 layers, 32q/4kv heads, hd 64, "
+              "bs 16, f16 KV, B=56, ctx U[256,2048]"),
+    "cfg3": ("CFG3", 256, 512, 4096, "Llama-3-8B decode: 32 layers, 32q/8kv heads, hd 128, bs 16, "
+             "bf16 KV, B=256, ctx U[512,4096], pool 1.2x live tokens"),
+    "cfg4": ("CFG4", 128, 2048, 8192, "Llama-3-70B layers 0-39: 40 layers, 64q/8kv heads, hd 128, "
+             "bs 16, bf16 KV, B=128, ctx U[2048,8192], pool 1.2x live tokens"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-layers", type=int, default=2,
+                    help="layer passes of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the paged-KV path has no "
+                                   "inter-GPU exchange here (see DESIGN.md, sharding); "
+                                   "run with --gpus 1"}))
+        return 2
+
+    import numpy as np
+    import torch
+
+    import pagedkv
+    from pagedkv import workload as wl
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    dev = torch.device("cuda", 0)
+    shape_attr, B, lo, hi, desc = CONFIGS[args.config]
+    shape = getattr(wl, shape_attr)
+    L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
+    tdt = pagedkv.torch_dtype(shape.dtype)
+    num_blocks = 2048 if args.config == "cfg1" else None
+    batch = wl.decode_batch(shape, B, lo, hi, args.seed, num_blocks=num_blocks)
+    log(f"[bench] {args.config}: B={B} ctx mean {batch.ctx.mean():.0f} max {batch.ctx.max()} "
+        f"pool {batch.num_blocks} blocks x {L} layers")
+
+    cache = pagedkv.PagedKvCache(L, batch.num_blocks, bs, KVH, hd, tdt)
+    cache.fill_normal(args.seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    q = (torch.randn((L, B, H, hd), generator=g, device=dev, dtype=torch.float32)
+         / math.sqrt(hd)).to(tdt)
+    k_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(tdt)
+    v_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(tdt)
+    out = torch.empty((L, B, H * hd), dtype=tdt, device=dev)
+    tables = torch.from_numpy(np.where(batch.tables < 0, 0, batch.tables).astype(np.int32)).to(dev)
+    ctx_lens = torch.from_numpy(batch.context_lens).to(dev)
+    max_ctx = int(batch.context_lens.max())
+    cache.reserve_decode(B, H, max_ctx)
+    torch.cuda.synchronize()
+
+    lib = pagedkv.lib()
+    stream = torch.cuda.current_stream(dev)
+    sp = int(stream.cuda_stream) or None
+    h = cache.handle
+    odt = pagedkv.pkv_dtype(tdt)
+    scale = 1.0 / math.sqrt(hd)
+    ptrs = [(q[l].data_ptr(), out[l].data_ptr(), k_new[l].data_ptr(), v_new[l].data_ptr())
+            for l in range(L)]
+    tp, cp, mbps = tables.data_ptr(), ctx_lens.data_ptr(), tables.shape[1]
+
+    def launch(l: int) -> None:
+        qp, op, kp, vp = ptrs[l]
+        rc = lib.pkv_decode_attention(h, l, qp, op, odt, tp, mbps, cp, max_ctx, B, H, scale,
+                                      kp, vp, sp)
+        if rc:
+            pagedkv._lib.check(rc, h)
+
+    def step() -> None:
+        for l in range(L):
+            launch(l)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    cache.check()
+
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+
+    # Kernel duration: HIP events around each launch on the launch stream.
+    n_kt = max(1, min(args.steps, 5))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_kt * L)]
+    i = 0
+    for _ in range(n_kt):
+        for l in range(L):
+            evs[i][0].record(stream)
+            launch(l)
+            evs[i][1].record(stream)
+            i += 1
+    torch.cuda.synchronize()
+    kern_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    kern_avg_ms = sum(kern_ms) / len(kern_ms)
+    cache.check()
+
+    bytes_step = wl.decode_bytes(shape, batch.ctx)
+    bytes_launch = bytes_step / L
+    tok_s = B / (ms_step / 1e3)
+    gbps_step = bytes_step / (ms_step / 1e3) / 1e9
+    gbps_kernel = bytes_launch / (kern_avg_ms / 1e3) / 1e9
+    log(f"[bench] {ms_step:.3f} ms/step, {tok_s:.0f} tok/s, step {gbps_step:.0f} GB/s, "
+        f"kernel avg {kern_avg_ms * 1e3:.1f} us ({gbps_kernel:.0f} GB/s, "
+        f"p10 {kern_ms[len(kern_ms) // 10] * 1e3:.1f} p90 {kern_ms[9 * len(kern_ms) // 10] * 1e3:.1f} us)")
+
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", f"decode_{args.config}_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            tr = json.load(f)
+        if tr.get("seed") == args.seed and tr.get("config") == args.config:
+            traffic = tr.get("bytes_per_launch")
+
+    cpu = None
+    if args.cpu_layers > 0:
+        cpu = cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log)
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {wl.BF16: "bf16", wl.F16: "f16", wl.F32: "f32"}[shape.dtype],
+        "data": "synthetic (seeded N(0,1) K/V/Q, random block tables)",
+        "config": {"workload": f"{args.config}: {desc}", "batch": B, "layers": L,
+                   "mean_context": round(float(batch.ctx.mean()), 1), "seed": args.seed,
+                   "num_blocks": batch.num_blocks, "parallelism": "single GPU"},
+        "hbm_gbps": round(gbps_step, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbps_kernel, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps_kernel / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "kernel": "pkv::decode_kernel",
+                     "kernel_avg_us": round(kern_avg_ms * 1e3, 2),
+                     "algorithmic_bytes_per_launch": int(bytes_launch)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    cache.close()
+    return 0
+
+
+def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
+    """Times the oracle's CPU restatement of the reference decode math
+    (append + attention per layer, OpenMP over (sequence, kv head)) on layer
+    0's data copied to host, `cpu_layers` passes, scaled to a full step."""
+    import numpy as np
+    import oracle
+    import pagedkv
+    from pagedkv import workload as wl
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    nd = np.float32 if shape.dtype == wl.F32 else np.uint16
+    shp = (cache.num_blocks, cache.block_size, cache.n_kv_head, cache.head_dim)
+    t_copy = time.time()
+    kp = cache.read_bytes(0, pagedkv.K).view(nd).reshape(shp)
+    vp = cache.read_bytes(0, pagedkv.V).view(nd).reshape(shp)
+
+    def host(t):
+        t = t.contiguous().cpu()
+        if nd is np.uint16:
+            return t.view(__import__("torch").int16).numpy().view(np.uint16)
+        return t.numpy()
+
+    qh, knh, vnh = host(q[0]), host(k_new[0]), host(v_new[0])
+    tables = np.where(batch.tables < 0, 0, batch.tables).astype(np.int32)
+    cl = batch.context_lens
+    log(f"[bench] cpu baseline: host copy {time.time() - t_copy:.1f}s, {threads} threads")
+    scale = 1.0 / math.sqrt(shape.head_dim)
+    oracle.lib()
+    t = time.time()
+    res = None
+    for _ in range(args.cpu_layers):
+        res = oracle.decode_inplace(kp, vp, shape.dtype, shape.block_size, tables, cl, qh, knh, vnh,
+                                    scale, n_threads=threads)
+    dt = (time.time() - t) / args.cpu_layers
+    step_s = dt * shape.n_layers
+    # sanity: the CPU result agrees with the GPU's layer-0 output
+    gpu0 = out[0].float().cpu().numpy()
+    agree = bool(np.all(np.abs(gpu0 - res) <= 1e-3 + 2e-2 * np.abs(res)))
+    log(f"[bench] cpu baseline: {dt:.2f} s/layer -> {batch.batch / step_s:.1f} tok/s "
+        f"(gpu/cpu layer-0 agreement: {agree})")
+    return {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
+                       f"{args.cpu_layers} passes of {dt:.2f} s, scaled x{shape.n_layers} layers"),
+            "agrees_with_gpu": agree}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,222 @@
+/*
+ * pagedkv.h -- C ABI of the MI355X paged-KV engine (libpagedkv.so).
+ *
+ * This is the drop-in boundary under the candle provider's `engine = "paged"`
+ * path of einyx/ai-engine.  Every entry point is plain C: opaque handles,
+ * raw pointers, sizes and an int status.  No torch, HIP or Rust types cross
+ * it; HIP streams are passed as `void*` (a hipStream_t, NULL = default stream).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   KvPool::new            crates/ai-engine-candle/src/paged/attention.rs:39-55
+ *   KvPool::write          crates/ai-engine-candle/src/paged/attention.rs:57-83
+ *   KvPool::gather_seq     crates/ai-engine-candle/src/paged/attention.rs:85-97
+ *   build_mask + sdpa      crates/ai-engine-candle/src/paged/attention.rs:11-28,100-136
+ *   decode attention slice crates/ai-engine-candle/src/paged/transformer.rs:271-292
+ *   prefill attention      crates/ai-engine-candle/src/paged/transformer.rs:139-196
+ *   BlockAllocator/Table   crates/ai-engine-candle/src/paged/block_table.rs:5-58
+ *
+ * Conventions shared by every call:
+ *  - Status: 0 = PKV_OK, negative = error.  The message of the last error of a
+ *    pool is returned by pkv_last_error(pool); errors of calls that have no pool
+ *    (create, allocator) by pkv_last_error(NULL) on the calling thread.
+ *    No call unwinds, aborts or panics across the boundary.
+ *  - Threading: a pool handle is externally synchronised (one caller thread at a
+ *    time, like the reference's single engine thread, engine.rs:49).  Device
+ *    work is enqueued on the caller's stream and is stream-ordered; the library
+ *    starts no threads.
+ *  - Pool layout (per layer, K and V separately), identical to the reference's
+ *    KvPool tensors: [num_blocks][block_size][n_kv_head][head_dim], row-major,
+ *    element type `dtype`.  Slot s = block_id * block_size + pos % block_size
+ *    addresses the row [s][n_kv_head][head_dim] (attention.rs:88-91).
+ *  - Device arrays (q, k, v, out, slot mappings, block tables, lengths) are
+ *    device pointers unless the parameter name ends in `_host`.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define PKV_OK 0
+#define PKV_ERR_INVALID (-1)     /* invalid argument or shape               */
+#define PKV_ERR_OOM (-2)         /* device or host allocation failed        */
+#define PKV_ERR_HIP (-3)         /* HIP runtime error                       */
+#define PKV_ERR_UNSUPPORTED (-4) /* shape/dtype combination not provided    */
+#define PKV_ERR_CAPACITY (-5)    /* allocator: free list too short          */
+#define PKV_ERR_DEVICE_DATA (-6) /* kernel saw an out-of-range id/length    */
+
+/* ---- element types ----------------------------------------------------- */
+#define PKV_F32 0
+#define PKV_F16 1
+#define PKV_BF16 2
+
+/* ---- pool selectors ---------------------------------------------------- */
+#define PKV_K 0
+#define PKV_V 1
+
+typedef struct pkv_pool pkv_pool;
+
+/* Library version string, e.g. "pagedkv 0.1 gfx950". */
+const char* pkv_version(void);
+
+/* Message of the last failed call on `pool` (or of the calling thread when
+ * pool is NULL).  Never NULL; "" when there was no error. */
+const char* pkv_last_error(const pkv_pool* pool);
+
+/* Allocate K and V pools for `n_layers` layers on HIP device `device`, zero
+ * filled like Tensor::zeros in KvPool::new (attention.rs:39-55).  One handle
+ * stands for the reference's Vec<KvPool> (engine.rs:70-72): layer l of the
+ * handle is the reference's kv[l].  Block ids are shared by all layers.
+ * dtype: PKV_F32 (the reference's own dtype), PKV_F16 or PKV_BF16.
+ * head_dim must be 64, 128 or 256; block_size a power of two in [16, 256]
+ * (the reference's default is 16, app.rs:701). */
+int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
+                    int block_size, int n_kv_head, int head_dim, int dtype,
+                    int device);
+int pkv_pool_destroy(pkv_pool* pool);
+
+/* Shape and placement queries. */
+int pkv_pool_shape(const pkv_pool* pool, int* n_layers, int* num_blocks,
+                   int* block_size, int* n_kv_head, int* head_dim, int* dtype);
+size_t pkv_pool_layer_bytes(const pkv_pool* pool); /* bytes of one K (or V) */
+int pkv_pool_layer_ptrs(const pkv_pool* pool, int layer, void** k, void** v);
+
+/* Synchronous host<->pool byte copies (tests, debugging, checkpoints). */
+int pkv_pool_read(pkv_pool* pool, int layer, int which, size_t byte_offset,
+                  size_t nbytes, void* host_dst);
+int pkv_pool_write(pkv_pool* pool, int layer, int which, size_t byte_offset,
+                   const void* host_src, size_t nbytes);
+
+/* Fill every layer's K and V with N(0,1) samples rounded to the pool dtype,
+ * from a counter-based hash of (seed, layer, which, element index).
+ * A workload generator for benchmarks; no reference counterpart. */
+int pkv_pool_fill_normal(pkv_pool* pool, uint64_t seed, void* stream);
+
+/* ---- KV append / scatter (KvPool::write, attention.rs:57-83) -----------
+ * k, v: [n_tokens][n_kv_head][head_dim] in the pool dtype.
+ * slot_mapping: [n_tokens] int32, slot = block * block_size + offset
+ * (the host computes it with BlockAllocator::locate, block_table.rs:55-58).
+ * Token i is copied bit-exactly to row slot_mapping[i] of layer `layer`'s K
+ * and V pools; no other byte changes.  A negative slot skips the token
+ * (padding); a slot >= num_blocks*block_size is not written and makes the
+ * next pkv_pool_check() report PKV_ERR_DEVICE_DATA. */
+int pkv_append(pkv_pool* pool, int layer, const void* k, const void* v,
+               const int32_t* slot_mapping, int n_tokens, void* stream);
+
+/* ---- gather (KvPool::gather_seq, attention.rs:85-97) -------------------
+ * out_k, out_v: [len][n_kv_head][head_dim] pool dtype, bit-exact copies of
+ * the rows at slot blocks[p / bs] * bs + p % bs, p = 0..len-1.
+ * block_table: device int32 [ceil(len / block_size)]. */
+int pkv_gather_seq(pkv_pool* pool, int layer, const int32_t* block_table,
+                   int len, void* out_k, void* out_v, void* stream);
+
+/* ---- block copy (copy-on-write after fork; no reference counterpart) ----
+ * For every layer and both K and V: block dst[i] <- block src[i], i < n.
+ * src, dst: device int32 [n].  dst ids must be distinct and no dst may be a
+ * src of the same call (the CoW contract: dst blocks are fresh). */
+int pkv_copy_blocks(pkv_pool* pool, const int32_t* src, const int32_t* dst,
+                    int n, void* stream);
+
+/* ---- compaction (no reference counterpart) ------------------------------
+ * Moves block src_host[i] to dst_host[i] for every layer and K/V, in place:
+ * the dst set may overlap the src set (e.g. survivors gathered into a
+ * contiguous prefix).  src ids distinct, dst ids distinct.  The plan (chains
+ * and cycles of the move graph) is built on the host, so ids are host arrays.
+ * Each byte is read once and written once; no scratch pool is allocated. */
+int pkv_compact(pkv_pool* pool, const int32_t* src_host,
+                const int32_t* dst_host, int n, void* stream);
+
+/* ---- paged decode attention (sdpa + build_mask + the decode-step
+ * attention slice, attention.rs:100-136, transformer.rs:271-292) ----------
+ * One query token per sequence.
+ *  q:            [batch][n_head][head_dim], pool dtype (post-RoPE).
+ *  out:          [batch][n_head * head_dim], out_dtype (PKV_F32 or the pool
+ *                dtype); element [b][h*head_dim + d] as in attention.rs:124-125.
+ *  block_tables: [batch][max_blocks_per_seq] int32.
+ *  context_lens: [batch] int32 = number of keys attended = seq_lens[b] + 1
+ *                (the reference's valid_lens, transformer.rs:289).
+ *  max_context_len: host int >= every context_lens[b] (the reference's
+ *                kv_len, transformer.rs:241); sizes the partition grid.
+ *  scale:        multiplies q.k (the reference uses 1/sqrt(head_dim),
+ *                attention.rs:118-120).
+ *  k_new, v_new: NULL, or [batch][n_kv_head][head_dim]: then the call first
+ *                stores them at token position context_lens[b]-1 of sequence
+ *                b (KvPool::write at seq_lens[b], transformer.rs:276) and the
+ *                attention sees them -- append and attention in one launch.
+ * GQA: query head h reads kv head h / (n_head / n_kv_head) (attention.rs:128-136).
+ * fp32 accumulation; softmax in fp32 with an exp2 formulation.
+ * context_lens[b] == 0 yields a zero output row. */
+int pkv_decode_attention(pkv_pool* pool, int layer, const void* q, void* out,
+                         int out_dtype, const int32_t* block_tables,
+                         int max_blocks_per_seq, const int32_t* context_lens,
+                         int max_context_len, int batch, int n_head,
+                         float scale, const void* k_new, const void* v_new,
+                         void* stream);
+
+/* Workspace that pkv_decode_attention needs for a given batch/length; the
+ * pool grows its internal workspace on demand (hipMalloc + device sync).
+ * Callers that must not allocate later (stream capture, serving loops)
+ * reserve the largest shape they will use up front. */
+size_t pkv_decode_workspace_bytes(const pkv_pool* pool, int batch, int n_head,
+                                  int max_context_len);
+int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,
+                            int max_context_len);
+
+/* ---- chunked prefill attention (prefill_seq attention,
+ * transformer.rs:139-196, generalised to a prior context) -----------------
+ * Sequence s has q_len_s = cu_q_lens[s+1]-cu_q_lens[s] query tokens whose K/V
+ * are already in the pool (pkv_append); its context has context_lens[s] keys
+ * in total, so query i sits at position context_lens[s]-q_len_s+i and
+ * attends keys 0..that position (causal; the reference's mask j > i -> -inf
+ * when the prior context is empty).
+ *  q:   [total_q][n_head][head_dim] pool dtype;  out: [total_q][n_head*head_dim].
+ *  cu_q_lens: [n_seqs+1] int32; context_lens: [n_seqs] int32;
+ *  block_tables: [n_seqs][max_blocks_per_seq] int32.
+ *  max_q_len, max_context_len: host upper bounds. */
+int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
+                          int out_dtype, const int32_t* cu_q_lens,
+                          const int32_t* context_lens,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          int n_seqs, int max_q_len, int max_context_len,
+                          int n_head, float scale, void* stream);
+
+/* Synchronise the pool's device and report (then clear) any out-of-range
+ * slot/block id or length a kernel met since the last check:
+ * PKV_OK or PKV_ERR_DEVICE_DATA. */
+int pkv_pool_check(pkv_pool* pool);
+
+/* ---- host block bookkeeping (BlockAllocator / BlockTable,
+ * block_table.rs:5-58).  Pure host code, usable without a GPU. ------------ */
+typedef struct pkv_allocator pkv_allocator;
+typedef struct pkv_table pkv_table;
+
+/* BlockAllocator::new: free list [num_blocks-1, ..., 1, 0], pops from the end
+ * so the first blocks handed out are 0, 1, 2, ... (block_table.rs:17-21). */
+pkv_allocator* pkv_allocator_new(size_t num_blocks, size_t block_size);
+void pkv_allocator_free(pkv_allocator* a);
+size_t pkv_allocator_free_count(const pkv_allocator* a);       /* :23-25 */
+size_t pkv_allocator_blocks_for(const pkv_allocator* a, size_t n_tokens); /* :27-30 */
+/* :32-47  PKV_OK, or PKV_ERR_CAPACITY with nothing allocated. */
+int pkv_allocator_ensure_capacity(pkv_allocator* a, pkv_table* t,
+                                  size_t n_tokens);
+/* :49-52  appends the table's blocks to the free list in table order. */
+void pkv_allocator_release(pkv_allocator* a, pkv_table* t);
+/* :54-58  PKV_ERR_INVALID when pos is beyond the table (the reference panics). */
+int pkv_allocator_locate(const pkv_allocator* a, const pkv_table* t,
+                         size_t pos, uint32_t* block_id, size_t* slot);
+
+pkv_table* pkv_table_new(void);
+void pkv_table_free(pkv_table* t);
+size_t pkv_table_len(const pkv_table* t);
+const uint32_t* pkv_table_blocks(const pkv_table* t);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

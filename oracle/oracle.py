@@ -1,0 +1,262 @@
+"""CPU oracle for the paged-KV path (test infrastructure only).
+
+Numpy/ctypes front end of ``pagedkv_oracle.c``.  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg use this
+module, and only as the checker or as the timed CPU baseline; the product
+path (``libpagedkv.so``) never calls it.
+
+Each wrapper names the reference function it restates (paths relative to the
+reference repository).  How each one is pinned is listed at the top of
+``pagedkv_oracle.c`` and exercised by ``tests/test_oracle.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liborc.so")
+
+F32, F16, BF16 = 0, 1, 2
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle with gcc (make)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.orc_kv_write.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _P, _P, _SZ]
+    L.orc_kv_write.restype = ctypes.c_int
+    L.orc_gather_seq.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _P, _P]
+    L.orc_gather_seq.restype = ctypes.c_int
+    L.orc_build_mask.argtypes = [_P, _P, _SZ, _SZ, _P]
+    L.orc_build_mask.restype = None
+    L.orc_sdpa_f32.argtypes = [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]
+    L.orc_sdpa_f32.restype = None
+    L.orc_decode_step_f32.argtypes = [_P, _P, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P, _P, _P,
+                                      _SZ, _SZ, ctypes.c_float, _P]
+    L.orc_decode_step_f32.restype = ctypes.c_int
+    L.orc_paged_attention_f64.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P,
+                                          _SZ, _SZ, ctypes.c_double, _P]
+    L.orc_paged_attention_f64.restype = None
+    L.orc_prefill_attention_f64.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P,
+                                            _SZ, _P, _SZ, ctypes.c_double, _P]
+    L.orc_prefill_attention_f64.restype = None
+    L.orc_prefill_seq_f32.argtypes = [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]
+    L.orc_prefill_seq_f32.restype = None
+    L.orc_copy_blocks.argtypes = [_P, _SZ, _SZ, _SZ, _P, _P, _SZ]
+    L.orc_copy_blocks.restype = None
+    L.orc_compact.argtypes = [_P, _SZ, _SZ, _SZ, _P, _P, _SZ]
+    L.orc_compact.restype = ctypes.c_int
+    L.orc_decode_inplace.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P, _P,
+                                     _SZ, _SZ, ctypes.c_float, _P, ctypes.c_int]
+    L.orc_decode_inplace.restype = None
+    L.orc_threads.argtypes = [ctypes.c_int]
+    L.orc_threads.restype = ctypes.c_int
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def widen(a: np.ndarray, dtype: int) -> np.ndarray:
+    """Exact widening of stored f16/bf16 bits (uint16) or f32 to float32."""
+    if dtype == F32:
+        return np.ascontiguousarray(a, dtype=np.float32)
+    if dtype == F16:
+        return np.ascontiguousarray(a).view(np.float16).astype(np.float32)
+    u = np.ascontiguousarray(a).view(np.uint16).astype(np.uint32) << 16
+    return u.view(np.float32)
+
+
+# --------------------------------------------------------------------------
+# byte-moving functions (bit-exact)
+# --------------------------------------------------------------------------
+def kv_write(k_pool: np.ndarray, v_pool: np.ndarray, block_size: int,
+             blocks: np.ndarray, start_pos: int, k: np.ndarray, v: np.ndarray) -> None:
+    """KvPool::write (attention.rs:57-83) on pools shaped
+    (num_blocks, block_size, n_kv, hd); k, v: (n_new, n_kv, hd)."""
+    n_kv, hd = k_pool.shape[2], k_pool.shape[3]
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+    k = np.ascontiguousarray(k, dtype=k_pool.dtype)
+    v = np.ascontiguousarray(v, dtype=v_pool.dtype)
+    rc = lib().orc_kv_write(_p(k_pool), _p(v_pool), k_pool.itemsize, block_size, n_kv, hd,
+                            _p(blocks), blocks.size, start_pos, _p(k), _p(v), k.shape[0])
+    if rc != 0:
+        raise IndexError("position beyond block table (the reference panics here)")
+
+
+def gather_seq(k_pool: np.ndarray, v_pool: np.ndarray, block_size: int,
+               blocks: np.ndarray, length: int) -> tuple[np.ndarray, np.ndarray]:
+    """KvPool::gather_seq (attention.rs:85-97) -> (len, n_kv, hd) each."""
+    n_kv, hd = k_pool.shape[2], k_pool.shape[3]
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+    ok = np.empty((length, n_kv, hd), dtype=k_pool.dtype)
+    ov = np.empty((length, n_kv, hd), dtype=v_pool.dtype)
+    rc = lib().orc_gather_seq(_p(k_pool), _p(v_pool), k_pool.itemsize, block_size, n_kv, hd,
+                              _p(blocks), blocks.size, length, _p(ok), _p(ov))
+    if rc != 0:
+        raise IndexError("position beyond block table (the reference panics here)")
+    return ok, ov
+
+
+def build_mask(seq_lens, q_positions, kv_len: int) -> np.ndarray:
+    """build_mask (attention.rs:11-28) -> (batch, 1, 1, kv_len) float32."""
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int64)
+    qp = np.ascontiguousarray(q_positions, dtype=np.int64)
+    out = np.empty((sl.size, kv_len), dtype=np.float32)
+    lib().orc_build_mask(_p(sl), _p(qp), sl.size, kv_len, _p(out))
+    return out.reshape(sl.size, 1, 1, kv_len)
+
+
+def copy_blocks(pool: np.ndarray, n_layers: int, block_bytes: int, src, dst) -> None:
+    """Closed form of block copy over [n_layers][2][pool bytes] (uint8 array)."""
+    src = np.ascontiguousarray(src, dtype=np.int32)
+    dst = np.ascontiguousarray(dst, dtype=np.int32)
+    layer_bytes = pool.nbytes // (n_layers * 2)
+    lib().orc_copy_blocks(_p(pool), n_layers, layer_bytes, block_bytes, _p(src), _p(dst), src.size)
+
+
+def compact(pool: np.ndarray, n_layers: int, block_bytes: int, src, dst) -> None:
+    """Closed form of compaction: new[dst[i]] = old[src[i]], out of place."""
+    src = np.ascontiguousarray(src, dtype=np.int32)
+    dst = np.ascontiguousarray(dst, dtype=np.int32)
+    layer_bytes = pool.nbytes // (n_layers * 2)
+    if lib().orc_compact(_p(pool), n_layers, layer_bytes, block_bytes, _p(src), _p(dst), src.size):
+        raise MemoryError("oracle compact: host allocation failed")
+
+
+# --------------------------------------------------------------------------
+# attention
+# --------------------------------------------------------------------------
+def sdpa_f32(q, k, v, mask, n_head: int, n_kv_head: int, scale: float | None = None) -> np.ndarray:
+    """sdpa (attention.rs:100-136) in f32.  q: (B,H,Lq,hd); k,v: (B,KVH,kv,hd);
+    mask: (B,1,Lq,kv).  Returns (B, Lq, H*hd)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    mask = np.ascontiguousarray(mask, dtype=np.float32)
+    B, H, Lq, hd = q.shape
+    kv = k.shape[2]
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.empty((B, Lq, H * hd), dtype=np.float32)
+    lib().orc_sdpa_f32(_p(q), _p(k), _p(v), _p(mask), B, H, n_kv_head, Lq, kv, hd,
+                       float(scale), _p(out))
+    return out
+
+
+def decode_step_f32(k_pool, v_pool, block_size: int, tables, seq_lens, positions,
+                    q, k_new, v_new, scale: float | None = None) -> np.ndarray:
+    """Transformer::decode_step attention slice (transformer.rs:271-292) in f32.
+    Pools (num_blocks, bs, KVH, hd) float32 are modified (append).
+    tables: (B, max_nb); q: (B, H, hd); k_new/v_new: (B, KVH, hd).
+    Returns (B, H*hd)."""
+    assert k_pool.dtype == np.float32 and v_pool.dtype == np.float32
+    KVH, hd = k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.uint32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int64)
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k_new = np.ascontiguousarray(k_new, dtype=np.float32)
+    v_new = np.ascontiguousarray(v_new, dtype=np.float32)
+    B, H = q.shape[0], q.shape[1]
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.empty((B, H * hd), dtype=np.float32)
+    rc = lib().orc_decode_step_f32(_p(k_pool), _p(v_pool), block_size, KVH, hd, _p(tables),
+                                   tables.shape[1], _p(sl), _p(pos), _p(q), _p(k_new),
+                                   _p(v_new), B, H, float(scale), _p(out))
+    if rc:
+        raise IndexError("position beyond block table")
+    return out
+
+
+def paged_attention_f64(k_pool, v_pool, dtype: int, block_size: int, tables, ctx_lens,
+                        q, scale: float) -> np.ndarray:
+    """Closed-form fp64 paged decode attention.  Pools hold stored elements
+    (uint16 bits for f16/bf16); q: (B, H, hd) float32.  Returns (B, H*hd) f64."""
+    KVH, hd = k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.uint32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    B, H = q.shape[0], q.shape[1]
+    out = np.empty((B, H * hd), dtype=np.float64)
+    lib().orc_paged_attention_f64(_p(np.ascontiguousarray(k_pool)), _p(np.ascontiguousarray(v_pool)),
+                                  dtype, block_size, KVH, hd, _p(tables), tables.shape[1],
+                                  _p(cl), _p(q), B, H, float(scale), _p(out))
+    return out
+
+
+def prefill_attention_f64(k_pool, v_pool, dtype: int, block_size: int, tables, cu_q_lens,
+                          ctx_lens, q, scale: float) -> np.ndarray:
+    """Closed-form fp64 chunked-prefill attention.  q: (T, H, hd) float32.
+    Returns (T, H*hd) f64."""
+    KVH, hd = k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.uint32)
+    cu = np.ascontiguousarray(cu_q_lens, dtype=np.int64)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    T, H = q.shape[0], q.shape[1]
+    out = np.empty((T, H * hd), dtype=np.float64)
+    lib().orc_prefill_attention_f64(_p(np.ascontiguousarray(k_pool)), _p(np.ascontiguousarray(v_pool)),
+                                    dtype, block_size, KVH, hd, _p(tables), tables.shape[1],
+                                    _p(cu), _p(cl), cl.size, _p(q), H, float(scale), _p(out))
+    return out
+
+
+def prefill_seq_f32(q, k, v, n_kv_head: int, scale: float | None = None) -> np.ndarray:
+    """prefill_seq attention slice (transformer.rs:139-196) in f32.
+    q: (H, N, hd); k, v: (KVH, N, hd).  Returns (N, H*hd)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    H, N, hd = q.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.empty((N, H * hd), dtype=np.float32)
+    lib().orc_prefill_seq_f32(_p(q), _p(k), _p(v), H, n_kv_head, N, hd, float(scale), _p(out))
+    return out
+
+
+def decode_inplace(k_pool, v_pool, dtype: int, block_size: int, tables, ctx_lens, q,
+                   k_new, v_new, scale: float, n_threads: int = 0) -> np.ndarray:
+    """CPU baseline: reference decode math, in place, ragged, OpenMP.
+    Pools/q/k_new/v_new hold stored elements of `dtype`.  Returns (B, H*hd) f32."""
+    KVH, hd = k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    B, H = q.shape[0], q.shape[1]
+    out = np.empty((B, H * hd), dtype=np.float32)
+    kn = _p(k_new) if k_new is not None else None
+    vn = _p(v_new) if v_new is not None else None
+    lib().orc_decode_inplace(_p(k_pool), _p(v_pool), dtype, block_size, KVH, hd, _p(tables),
+                             tables.shape[1], _p(cl), _p(q), kn, vn, B, H, float(scale),
+                             _p(out), int(n_threads))
+    return out
+
+
+def threads(requested: int = 0) -> int:
+    return int(lib().orc_threads(int(requested)))

@@ -1,0 +1,502 @@
+/*
+ * pagedkv_oracle.c -- CPU oracle for the paged-KV hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file restates, in plain C, what the
+ * reference's candle `engine = "paged"` path computes, so that the HIP
+ * kernels of libpagedkv can be checked against it.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, and only
+ * as the checker or as the timed CPU baseline -- never as a product path.
+ *
+ * Reference files restated (paths relative to the reference repository):
+ *   crates/ai-engine-candle/src/paged/attention.rs   (KvPool, build_mask, sdpa)
+ *   crates/ai-engine-candle/src/paged/transformer.rs (decode/prefill slices)
+ * The reference's arithmetic runs inside candle-core/candle-nn 0.10.2 and
+ * gemm 0.19.0 (Cargo.lock:1220-1223,1276-1279,3037-3040), which are not in
+ * the reference tree; their published semantics are restated (row-major
+ * matmul in f32, softmax_last_dim = exp(x - max) / sum, affine scale).
+ * Summation order inside gemm is not reproducible here, so the f32
+ * restatements agree with the reference to rounding, and attention parity
+ * is a tolerance check (bit-exact only for the byte-moving functions).
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   orc_build_mask        - the reference's own KAT (attention.rs:142-156).
+ *   orc_kv_write/gather   - closed form (slot = blocks[p/bs]*bs + p%bs) and
+ *                           the "no other byte changes" invariant.
+ *   orc_sdpa_f32          - torch.nn.functional.scaled_dot_product_attention
+ *                           in float64 (independent library routine), special
+ *                           cases (one key -> that V row; equal keys -> mean V;
+ *                           dominant key -> its V row), mutation checks.
+ *   orc_decode_step_f32   - equals orc_paged_attention_f64 on ragged inputs
+ *                           (padding invariance) and orc_sdpa_f32 on the
+ *                           gathered inputs.
+ *   orc_prefill_*         - reduces to the reference prefill mask (P = 0), to
+ *                           decode (one query), chunk-split invariance, and
+ *                           brute-force torch float64 on tiny inputs.
+ *   orc_copy/compact      - closed-form out-of-place memcpy.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_BF16 2
+
+/* ------------------------------------------------------------------------ */
+/* dtype helpers: exact widening of f16/bf16 to f32                          */
+/* ------------------------------------------------------------------------ */
+static inline float orc_bf16_to_f32(uint16_t h) {
+    uint32_t u = ((uint32_t)h) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static inline float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t u;
+    if (exp == 0) {
+        if (man == 0) {
+            u = sign;
+        } else { /* subnormal: normalise */
+            int e = -1;
+            do {
+                e++;
+                man <<= 1;
+            } while ((man & 0x400) == 0);
+            man &= 0x3ff;
+            u = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 0x1f) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else {
+        u = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static inline float orc_load(const void* base, int dtype, size_t i) {
+    if (dtype == ORC_F32) return ((const float*)base)[i];
+    uint16_t h = ((const uint16_t*)base)[i];
+    return dtype == ORC_BF16 ? orc_bf16_to_f32(h) : orc_f16_to_f32(h);
+}
+
+static inline size_t orc_esize(int dtype) { return dtype == ORC_F32 ? 4 : 2; }
+
+/* Widen n elements of `dtype` to f32 (exact). */
+void orc_widen(const void* src, int dtype, size_t n, float* dst) {
+    for (size_t i = 0; i < n; i++) dst[i] = orc_load(src, dtype, i);
+}
+
+/* ------------------------------------------------------------------------ */
+/* KvPool::write (attention.rs:57-83): per new token i, locate(start_pos+i)  */
+/* -> (blocks[pos/bs], pos%bs) (block_table.rs:55-58), then the row          */
+/* [block, slot, :, :] of K and V is replaced by k[i], v[i].  The reference  */
+/* does it with a functional slice_assign; the stored values are the same.   */
+/* Returns -1 if a position is beyond the table (the reference panics).      */
+/* ------------------------------------------------------------------------ */
+int orc_kv_write(void* k_pool, void* v_pool, size_t elem_bytes, size_t bs,
+                 size_t n_kv, size_t hd, const uint32_t* blocks,
+                 size_t n_table_blocks, size_t start_pos, const void* k,
+                 const void* v, size_t n_new) {
+    const size_t row = n_kv * hd * elem_bytes;
+    for (size_t i = 0; i < n_new; i++) {
+        size_t pos = start_pos + i;
+        size_t bi = pos / bs;
+        if (bi >= n_table_blocks) return -1;
+        size_t slot = (size_t)blocks[bi] * bs + pos % bs;
+        memcpy((char*)k_pool + slot * row, (const char*)k + i * row, row);
+        memcpy((char*)v_pool + slot * row, (const char*)v + i * row, row);
+    }
+    return 0;
+}
+
+/* KvPool::gather_seq (attention.rs:85-97): idx[p] = blocks[p/bs]*bs + p%bs,
+ * index_select on the pool flattened to (N*bs, n_kv, hd). */
+int orc_gather_seq(const void* k_pool, const void* v_pool, size_t elem_bytes,
+                   size_t bs, size_t n_kv, size_t hd, const uint32_t* blocks,
+                   size_t n_table_blocks, size_t len, void* out_k,
+                   void* out_v) {
+    const size_t row = n_kv * hd * elem_bytes;
+    for (size_t p = 0; p < len; p++) {
+        size_t bi = p / bs;
+        if (bi >= n_table_blocks) return -1;
+        size_t idx = (size_t)blocks[bi] * bs + p % bs;
+        memcpy((char*)out_k + p * row, (const char*)k_pool + idx * row, row);
+        memcpy((char*)out_v + p * row, (const char*)v_pool + idx * row, row);
+    }
+    return 0;
+}
+
+/* build_mask (attention.rs:11-28): (batch, 1, 1, kv_len) additive mask,
+ * -inf where k >= seq_lens[b] or k > q_positions[b], else 0. */
+void orc_build_mask(const int64_t* seq_lens, const int64_t* q_positions,
+                    size_t batch, size_t kv_len, float* out) {
+    for (size_t b = 0; b < batch; b++)
+        for (size_t k = 0; k < kv_len; k++)
+            out[b * kv_len + k] =
+                ((int64_t)k >= seq_lens[b] || (int64_t)k > q_positions[b])
+                    ? -INFINITY
+                    : 0.0f;
+}
+
+/* candle_nn::ops::softmax_last_dim on one row: max, exp(x - max), sum,
+ * divide (published candle-nn 0.10.2 CPU semantics). */
+static void orc_softmax_row_f32(float* x, size_t n) {
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; i++) mx = x[i] > mx ? x[i] : mx;
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        x[i] = expf(x[i] - mx);
+        sum += x[i];
+    }
+    for (size_t i = 0; i < n; i++) x[i] /= sum;
+}
+
+/* sdpa (attention.rs:100-126) with repeat_kv (:128-136), all in f32:
+ *   q: (B, H, Lq, hd); k, v: (B, KVH, kv, hd); mask: (B, 1, Lq, kv)
+ *   query head h reads kv head h / (H / KVH) (consecutive repeat);
+ *   att = (q @ k^T) * scale; att += mask; softmax over kv; out = att @ v;
+ *   result (B, Lq, H*hd), element [b, i, h*hd + d] (:124-125). */
+void orc_sdpa_f32(const float* q, const float* k, const float* v,
+                  const float* mask, size_t B, size_t H, size_t KVH,
+                  size_t Lq, size_t kv, size_t hd, float scale, float* out) {
+    size_t rep = H / KVH;
+    float* att = (float*)malloc(sizeof(float) * (kv ? kv : 1));
+    for (size_t b = 0; b < B; b++)
+        for (size_t h = 0; h < H; h++) {
+            size_t g = h / rep;
+            const float* kb = k + (b * KVH + g) * kv * hd;
+            const float* vb = v + (b * KVH + g) * kv * hd;
+            for (size_t i = 0; i < Lq; i++) {
+                const float* qi = q + ((b * H + h) * Lq + i) * hd;
+                const float* mi = mask + (b * Lq + i) * kv;
+                for (size_t j = 0; j < kv; j++) {
+                    float s = 0.0f;
+                    for (size_t d = 0; d < hd; d++) s += qi[d] * kb[j * hd + d];
+                    att[j] = s * scale + mi[j];
+                }
+                orc_softmax_row_f32(att, kv);
+                float* o = out + (b * Lq + i) * H * hd + h * hd;
+                for (size_t d = 0; d < hd; d++) {
+                    float acc = 0.0f;
+                    for (size_t j = 0; j < kv; j++) acc += att[j] * vb[j * hd + d];
+                    o[d] = acc;
+                }
+            }
+        }
+    free(att);
+}
+
+/* Transformer::decode_step, attention slice (transformer.rs:271-292), in f32
+ * on f32 pools (the reference's KvPool dtype):
+ *   for each row b: write k_new[b], v_new[b] at pos seq_lens[b] (:276), then
+ *   gather seq_lens[b]+1 rows (:277), zero-pad to kv_len = max(seq_lens)+1
+ *   (:241,:278-281); stack to (B, KVH, kv_len, hd) (:285-286); mask with
+ *   valid_lens = seq_lens+1 and positions (:289-290); sdpa (:292).
+ * k_pool/v_pool are modified (the append).  tables: [B][max_nb] uint32.
+ * Returns -1 on a position beyond a table. */
+int orc_decode_step_f32(float* k_pool, float* v_pool, size_t bs, size_t KVH,
+                        size_t hd, const uint32_t* tables, size_t max_nb,
+                        const int64_t* seq_lens, const int64_t* positions,
+                        const float* q, const float* k_new,
+                        const float* v_new, size_t B, size_t H, float scale,
+                        float* out) {
+    size_t kv_len = 0;
+    for (size_t b = 0; b < B; b++)
+        if ((size_t)seq_lens[b] + 1 > kv_len) kv_len = (size_t)seq_lens[b] + 1;
+    const size_t row = KVH * hd;
+    float* k_all = (float*)calloc(B * KVH * kv_len * hd, sizeof(float));
+    float* v_all = (float*)calloc(B * KVH * kv_len * hd, sizeof(float));
+    float* gk = (float*)malloc(sizeof(float) * kv_len * row);
+    float* gv = (float*)malloc(sizeof(float) * kv_len * row);
+    int rc = 0;
+    for (size_t b = 0; b < B && rc == 0; b++) {
+        const uint32_t* tb = tables + b * max_nb;
+        rc = orc_kv_write(k_pool, v_pool, 4, bs, KVH, hd, tb, max_nb,
+                          (size_t)seq_lens[b], k_new + b * row,
+                          v_new + b * row, 1);
+        if (rc) break;
+        size_t len = (size_t)seq_lens[b] + 1;
+        rc = orc_gather_seq(k_pool, v_pool, 4, bs, KVH, hd, tb, max_nb, len,
+                            gk, gv);
+        /* pad_with_zeros + cat + transpose(1,2): (len, KVH, hd) -> (KVH, kv_len, hd) */
+        for (size_t p = 0; p < len; p++)
+            for (size_t g = 0; g < KVH; g++)
+                for (size_t d = 0; d < hd; d++) {
+                    size_t dst = ((b * KVH + g) * kv_len + p) * hd + d;
+                    k_all[dst] = gk[(p * KVH + g) * hd + d];
+                    v_all[dst] = gv[(p * KVH + g) * hd + d];
+                }
+    }
+    if (rc == 0) {
+        int64_t* valid = (int64_t*)malloc(sizeof(int64_t) * B);
+        for (size_t b = 0; b < B; b++) valid[b] = seq_lens[b] + 1;
+        float* mask = (float*)malloc(sizeof(float) * B * kv_len);
+        orc_build_mask(valid, positions, B, kv_len, mask);
+        orc_sdpa_f32(q, k_all, v_all, mask, B, H, KVH, 1, kv_len, hd, scale,
+                     out);
+        free(mask);
+        free(valid);
+    }
+    free(k_all);
+    free(v_all);
+    free(gk);
+    free(gv);
+    return rc;
+}
+
+/* Closed form in fp64: paged decode attention straight off the block tables,
+ * ragged (no padding).  For every (b, h): keys p = 0..ctx_lens[b]-1 at slot
+ * tables[b][p/bs]*bs + p%bs, kv head h / (H/KVH), s_p = scale * q.k_p,
+ * out = sum_p softmax(s)_p v_p.  Pools are element type `dtype` (widened
+ * exactly).  ctx_lens[b] == 0 gives a zero row. */
+void orc_paged_attention_f64(const void* k_pool, const void* v_pool,
+                             int dtype, size_t bs, size_t KVH, size_t hd,
+                             const uint32_t* tables, size_t max_nb,
+                             const int64_t* ctx_lens, const float* q,
+                             size_t B, size_t H, double scale, double* out) {
+    size_t rep = H / KVH;
+    for (size_t b = 0; b < B; b++) {
+        size_t n = (size_t)ctx_lens[b];
+        double* s = (double*)malloc(sizeof(double) * (n ? n : 1));
+        for (size_t h = 0; h < H; h++) {
+            size_t g = h / rep;
+            const float* qh = q + (b * H + h) * hd;
+            double* o = out + (b * H + h) * hd;
+            for (size_t d = 0; d < hd; d++) o[d] = 0.0;
+            if (n == 0) continue;
+            double mx = -INFINITY;
+            for (size_t p = 0; p < n; p++) {
+                size_t slot = (size_t)tables[b * max_nb + p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                double acc = 0.0;
+                for (size_t d = 0; d < hd; d++)
+                    acc += (double)qh[d] * (double)orc_load(k_pool, dtype, base + d);
+                s[p] = acc * scale;
+                if (s[p] > mx) mx = s[p];
+            }
+            double sum = 0.0;
+            for (size_t p = 0; p < n; p++) {
+                s[p] = exp(s[p] - mx);
+                sum += s[p];
+            }
+            for (size_t p = 0; p < n; p++) {
+                size_t slot = (size_t)tables[b * max_nb + p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                double w = s[p] / sum;
+                for (size_t d = 0; d < hd; d++)
+                    o[d] += w * (double)orc_load(v_pool, dtype, base + d);
+            }
+        }
+        free(s);
+    }
+}
+
+/* Closed form in fp64 for chunked prefill with a prior context: sequence s
+ * has ql = cu_q[s+1]-cu_q[s] queries whose K/V are already stored; query i
+ * is at position ctx_lens[s]-ql+i and attends keys 0..that position.  With
+ * an empty prior context this is prefill_seq's causal attention
+ * (transformer.rs:139-148,191-196: mask j > i -> -inf). */
+void orc_prefill_attention_f64(const void* k_pool, const void* v_pool,
+                               int dtype, size_t bs, size_t KVH, size_t hd,
+                               const uint32_t* tables, size_t max_nb,
+                               const int64_t* cu_q, const int64_t* ctx_lens,
+                               size_t n_seqs, const float* q, size_t H,
+                               double scale, double* out) {
+    size_t rep = H / KVH;
+    for (size_t sq = 0; sq < n_seqs; sq++) {
+        size_t q0 = (size_t)cu_q[sq], ql = (size_t)(cu_q[sq + 1] - cu_q[sq]);
+        size_t n = (size_t)ctx_lens[sq];
+        const uint32_t* tb = tables + sq * max_nb;
+        double* s = (double*)malloc(sizeof(double) * (n ? n : 1));
+        for (size_t i = 0; i < ql; i++) {
+            long long posi = (long long)n - (long long)ql + (long long)i;
+            for (size_t h = 0; h < H; h++) {
+                size_t g = h / rep;
+                const float* qh = q + ((q0 + i) * H + h) * hd;
+                double* o = out + ((q0 + i) * H + h) * hd;
+                for (size_t d = 0; d < hd; d++) o[d] = 0.0;
+                if (posi < 0) continue;
+                size_t nk = (size_t)posi + 1;
+                double mx = -INFINITY;
+                for (size_t p = 0; p < nk; p++) {
+                    size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                    size_t base = (slot * KVH + g) * hd;
+                    double acc = 0.0;
+                    for (size_t d = 0; d < hd; d++)
+                        acc += (double)qh[d] * (double)orc_load(k_pool, dtype, base + d);
+                    s[p] = acc * scale;
+                    if (s[p] > mx) mx = s[p];
+                }
+                double sum = 0.0;
+                for (size_t p = 0; p < nk; p++) {
+                    s[p] = exp(s[p] - mx);
+                    sum += s[p];
+                }
+                for (size_t p = 0; p < nk; p++) {
+                    size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                    size_t base = (slot * KVH + g) * hd;
+                    double w = s[p] / sum;
+                    for (size_t d = 0; d < hd; d++)
+                        o[d] += w * (double)orc_load(v_pool, dtype, base + d);
+                }
+            }
+        }
+        free(s);
+    }
+}
+
+/* prefill_seq attention slice (transformer.rs:139-148,179-196) in f32 for
+ * one sequence of N tokens with in-register K/V:
+ *   q: (H, N, hd); k, v: (KVH, N, hd); causal mask j > i -> -inf;
+ *   GQA expand; att = (q @ k^T) * scale + mask; softmax; att @ v;
+ *   out (N, H*hd) (:196). */
+void orc_prefill_seq_f32(const float* q, const float* k, const float* v,
+                         size_t H, size_t KVH, size_t N, size_t hd,
+                         float scale, float* out) {
+    float* mask = (float*)malloc(sizeof(float) * N * N);
+    for (size_t i = 0; i < N; i++)
+        for (size_t j = 0; j < N; j++) mask[i * N + j] = j > i ? -INFINITY : 0.0f;
+    orc_sdpa_f32(q, k, v, mask, 1, H, KVH, N, N, hd, scale, out);
+    free(mask);
+}
+
+/* Block copy over every layer and K/V: block dst[i] <- block src[i].
+ * layer_bytes = one layer's K (or V) pool size; block_bytes = one block.
+ * The pool buffer holds [n_layers][2][num_blocks * block_bytes]. */
+void orc_copy_blocks(void* pool, size_t n_layers, size_t layer_bytes,
+                     size_t block_bytes, const int32_t* src,
+                     const int32_t* dst, size_t n) {
+    for (size_t l = 0; l < n_layers * 2; l++) {
+        char* base = (char*)pool + l * layer_bytes;
+        for (size_t i = 0; i < n; i++)
+            memmove(base + (size_t)dst[i] * block_bytes,
+                    base + (size_t)src[i] * block_bytes, block_bytes);
+    }
+}
+
+/* Compaction closed form: new[dst[i]] = old[src[i]] for all i, computed out
+ * of place (a full copy of the old pool), every other block unchanged. */
+int orc_compact(void* pool, size_t n_layers, size_t layer_bytes,
+                size_t block_bytes, const int32_t* src, const int32_t* dst,
+                size_t n) {
+    char* old = (char*)malloc(layer_bytes);
+    if (!old) return -1;
+    for (size_t l = 0; l < n_layers * 2; l++) {
+        char* base = (char*)pool + l * layer_bytes;
+        memcpy(old, base, layer_bytes);
+        for (size_t i = 0; i < n; i++)
+            memcpy(base + (size_t)dst[i] * block_bytes,
+                   old + (size_t)src[i] * block_bytes, block_bytes);
+    }
+    free(old);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* CPU baseline: the reference's decode attention math (write at seq_lens,   */
+/* attend seq_lens+1 keys, scale after the dot product, max/exp/sum/divide   */
+/* softmax, P.V) done in place on the pool in its storage dtype, ragged      */
+/* lengths, OpenMP over (sequence, kv head).  This is the reference-math     */
+/* in-place variant timed by bench.py; it is not the faithful per-append     */
+/* full-pool copy of slice_assign (attention.rs:73-80), which is infeasible  */
+/* at the benchmark sizes.                                                   */
+/* ------------------------------------------------------------------------ */
+void orc_decode_inplace(void* k_pool, void* v_pool, int dtype, size_t bs,
+                        size_t KVH, size_t hd, const int32_t* tables,
+                        size_t max_nb, const int32_t* ctx_lens,
+                        const void* q, const void* k_new, const void* v_new,
+                        size_t B, size_t H, float scale, float* out,
+                        int n_threads) {
+    const size_t es = orc_esize(dtype);
+    const size_t rep = H / KVH;
+    /* append first (transformer.rs:276), bit-exact row copy */
+    for (size_t b = 0; b < B; b++) {
+        if (ctx_lens[b] <= 0 || !k_new) continue;
+        size_t pos = (size_t)ctx_lens[b] - 1;
+        size_t slot = (size_t)tables[b * max_nb + pos / bs] * bs + pos % bs;
+        memcpy((char*)k_pool + slot * KVH * hd * es,
+               (const char*)k_new + b * KVH * hd * es, KVH * hd * es);
+        memcpy((char*)v_pool + slot * KVH * hd * es,
+               (const char*)v_new + b * KVH * hd * es, KVH * hd * es);
+    }
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#pragma omp parallel
+#endif
+    {
+        size_t maxn = 0;
+        for (size_t b = 0; b < B; b++)
+            if ((size_t)ctx_lens[b] > maxn) maxn = (size_t)ctx_lens[b];
+        float* s = (float*)malloc(sizeof(float) * rep * (maxn ? maxn : 1));
+        float* qf = (float*)malloc(sizeof(float) * rep * hd);
+        float* kf = (float*)malloc(sizeof(float) * hd);
+        float* acc = (float*)malloc(sizeof(float) * rep * hd);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long long w = 0; w < (long long)(B * KVH); w++) {
+            size_t b = (size_t)w / KVH, g = (size_t)w % KVH;
+            size_t n = (size_t)ctx_lens[b];
+            const int32_t* tb = tables + b * max_nb;
+            for (size_t r = 0; r < rep; r++)
+                for (size_t d = 0; d < hd; d++)
+                    qf[r * hd + d] = orc_load(q, dtype, (b * H + g * rep + r) * hd + d);
+            for (size_t p = 0; p < n; p++) {
+                size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                for (size_t d = 0; d < hd; d++) kf[d] = orc_load(k_pool, dtype, base + d);
+                for (size_t r = 0; r < rep; r++) {
+                    float dot = 0.0f;
+                    for (size_t d = 0; d < hd; d++) dot += qf[r * hd + d] * kf[d];
+                    s[r * n + p] = dot * scale;
+                }
+            }
+            for (size_t r = 0; r < rep; r++) {
+                float mx = -INFINITY, sum = 0.0f;
+                for (size_t p = 0; p < n; p++) mx = s[r * n + p] > mx ? s[r * n + p] : mx;
+                for (size_t p = 0; p < n; p++) {
+                    s[r * n + p] = expf(s[r * n + p] - mx);
+                    sum += s[r * n + p];
+                }
+                for (size_t p = 0; p < n; p++) s[r * n + p] /= sum;
+            }
+            for (size_t i = 0; i < rep * hd; i++) acc[i] = 0.0f;
+            for (size_t p = 0; p < n; p++) {
+                size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                for (size_t d = 0; d < hd; d++) kf[d] = orc_load(v_pool, dtype, base + d);
+                for (size_t r = 0; r < rep; r++) {
+                    float w = s[r * n + p];
+                    for (size_t d = 0; d < hd; d++) acc[r * hd + d] += w * kf[d];
+                }
+            }
+            for (size_t r = 0; r < rep; r++)
+                memcpy(out + (b * H + g * rep + r) * hd, acc + r * hd, sizeof(float) * hd);
+        }
+        free(s);
+        free(qf);
+        free(kf);
+        free(acc);
+    }
+}
+
+/* Number of OpenMP threads the baseline uses for a requested count. */
+int orc_threads(int requested) {
+#ifdef _OPENMP
+    if (requested > 0) return requested;
+    return omp_get_max_threads();
+#else
+    (void)requested;
+    return 1;
+#endif
+}

@@ -1,0 +1,241 @@
+"""GPU parity of paged decode attention (+ fused KV append) against the CPU
+oracle.  Tolerance: |gpu - ref| <= 1e-3 + 2e-3 |ref|,
+fp32 accumulation; the reference output is the fp64 closed form over the
+same stored (dtype-rounded) inputs."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pagedkv
+from pagedkv import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+TD = {wl.F32: torch.float32, wl.F16: torch.float16, wl.BF16: torch.bfloat16}
+ND = {wl.F32: np.float32, wl.F16: np.uint16, wl.BF16: np.uint16}
+RTOL, ATOL = 2e-3, 1e-3
+
+
+def _to_dev(a, dt, device):
+    a = np.ascontiguousarray(a)
+    if dt == wl.F32:
+        return torch.from_numpy(a).to(device)
+    return torch.from_numpy(a.view(np.int16)).view(TD[dt]).to(device)
+
+
+def _host_pool(cache, layer):
+    nd = ND[pagedkv.pkv_dtype(cache.dtype)]
+    shp = (cache.num_blocks, cache.block_size, cache.n_kv_head, cache.head_dim)
+    return (cache.read_bytes(layer, pagedkv.K).view(nd).reshape(shp),
+            cache.read_bytes(layer, pagedkv.V).view(nd).reshape(shp))
+
+
+def _close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref)
+    bound = ATOL + RTOL * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance; "
+                           f"max err {err.max():.3g}, worst excess {(err - bound).max():.3g}")
+
+
+class Case:
+    """A one-layer pool with a random decode batch on it."""
+
+    def __init__(self, gpu, dt, H, KVH, hd, bs, ctx, seed, fused=False, pool_factor=1.3):
+        self.dt, self.H, self.KVH, self.hd, self.bs = dt, H, KVH, hd, bs
+        B = len(ctx)
+        self.ctx = np.asarray(ctx, np.int64)
+        need = -(-(self.ctx + 1) // bs)
+        nb = max(int(math.ceil(pool_factor * need.sum())), int(need.sum()) + 1)
+        perm = wl.permutation(seed, nb)
+        tables = np.zeros((B, max(int(need.max()), 1)), np.int32)
+        o = 0
+        for b in range(B):
+            tables[b, :need[b]] = perm[o:o + need[b]]
+            o += need[b]
+        self.tables = tables
+        self.cache = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, TD[dt])
+        shp = (nb, bs, KVH, hd)
+        self.kp = wl.normal_storage(seed + 1, shp, dt)
+        self.vp = wl.normal_storage(seed + 2, shp, dt)
+        self.cache.write_bytes(0, pagedkv.K, self.kp)
+        self.cache.write_bytes(0, pagedkv.V, self.vp)
+        self.q = wl.normal_storage(seed + 3, (B, H, hd), dt, scale=1 / math.sqrt(hd))
+        self.kn = wl.normal_storage(seed + 4, (B, KVH, hd), dt)
+        self.vn = wl.normal_storage(seed + 5, (B, KVH, hd), dt)
+        self.scale = 1 / math.sqrt(hd)
+        self.gpu = gpu
+        self.fused = fused
+
+    @property
+    def context_lens(self):
+        return (self.ctx + 1).astype(np.int32)
+
+    def run(self, out_dtype=None, max_context_len=None):
+        pool = self.cache.layer(0)
+        kn = _to_dev(self.kn, self.dt, self.gpu) if self.fused else None
+        vn = _to_dev(self.vn, self.dt, self.gpu) if self.fused else None
+        out = pool.decode_attention(_to_dev(self.q, self.dt, self.gpu),
+                                    torch.from_numpy(self.tables).to(self.gpu),
+                                    torch.from_numpy(self.context_lens).to(self.gpu),
+                                    max_context_len=max_context_len or int(self.context_lens.max()),
+                                    k_new=kn, v_new=vn, scale=self.scale,
+                                    out_dtype=out_dtype or torch.float32)
+        torch.cuda.synchronize()
+        self.cache.check()
+        return out.float().cpu().numpy()
+
+    def reference(self):
+        kp, vp = self.kp.copy(), self.vp.copy()
+        if self.fused:
+            for b in range(len(self.ctx)):
+                oracle.kv_write(kp, vp, self.bs, self.tables[b].astype(np.uint32), int(self.ctx[b]),
+                                self.kn[b:b + 1], self.vn[b:b + 1])
+        ref = oracle.paged_attention_f64(kp, vp, self.dt, self.bs, self.tables.astype(np.uint32),
+                                         self.context_lens, wl.widen(self.q, self.dt), self.scale)
+        return ref, kp, vp
+
+    def close(self):
+        self.cache.close()
+
+
+# ---------------------------------------------------------------------------
+def test_golden_fixtures(gpu):
+    import glob
+    import os
+    files = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "decode_*.npz")))
+    assert files
+    for f in files:
+        z = np.load(f, allow_pickle=False)
+        dt = int(z["dtype"])
+        kp, vp = z["k_pool"], z["v_pool"]
+        nb, bs, kvh, hd = kp.shape
+        H = int(z["n_head"])
+        cache = pagedkv.PagedKvCache(1, nb, bs, kvh, hd, TD[dt])
+        cache.write_bytes(0, pagedkv.K, kp)
+        cache.write_bytes(0, pagedkv.V, vp)
+        for od in ([torch.float32] + ([TD[dt]] if dt != wl.F32 else [])):
+            out = cache.layer(0).decode_attention(
+                _to_dev(z["q"], dt, gpu), torch.from_numpy(z["tables"]).to(gpu),
+                torch.from_numpy(z["context_lens"]).to(gpu), scale=float(z["scale"]),
+                out_dtype=od)
+            torch.cuda.synchronize()
+            _close(out.float().cpu().numpy(), z["out"], f"{os.path.basename(f)} out={od}")
+        cache.check()
+        cache.close()
+
+
+@pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
+@pytest.mark.parametrize("hd", [64, 128, 256])
+@pytest.mark.parametrize("R", [1, 2, 4, 8])
+def test_decode_matches_oracle(gpu, dt, hd, R):
+    KVH = 2
+    ctx = [0, 1, 14, 15, 16, 63, 64, 200, 257, 700]
+    c = Case(gpu, dt, R * KVH, KVH, hd, 16, ctx, seed=hd * 10 + R + dt)
+    got = c.run()
+    ref, _, _ = c.reference()
+    _close(got, ref, f"dt={dt} hd={hd} R={R}")
+    c.close()
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64, 256])
+def test_decode_block_sizes(gpu, bs):
+    c = Case(gpu, wl.BF16, 8, 2, 128, bs, [0, bs - 2, bs - 1, bs, 3 * bs + 5, 1000], seed=bs)
+    _close(c.run(), c.reference()[0], f"bs={bs}")
+    c.close()
+
+
+@pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
+def test_fused_append_writes_pool_and_attends(gpu, dt):
+    c = Case(gpu, dt, 16, 4, 128, 16, [0, 5, 15, 16, 31, 255, 256, 300, 1023, 2047], seed=77 + dt,
+             fused=True)
+    got = c.run()
+    ref, kp, vp = c.reference()
+    _close(got, ref, "fused")
+    k1, v1 = _host_pool(c.cache, 0)  # the append is bit-exact, nothing else changed
+    assert np.array_equal(k1.view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(v1.view(np.uint8), vp.view(np.uint8))
+    c.close()
+
+
+def test_fused_equals_separate_append(gpu):
+    # write-then-attend in one launch == KvPool::write then attention
+    dt = wl.BF16
+    ctx = list(wl.randint(5, 24, 0, 1500))
+    c = Case(gpu, dt, 32, 8, 128, 16, ctx, seed=5, fused=True)
+    fused = c.run()
+    d = Case(gpu, dt, 32, 8, 128, 16, ctx, seed=5, fused=False)
+    slots = d.tables[np.arange(len(ctx)), d.ctx // 16].astype(np.int64) * 16 + d.ctx % 16
+    d.cache.layer(0).append(_to_dev(d.kn, dt, gpu), _to_dev(d.vn, dt, gpu), slots.astype(np.int32))
+    sep = d.run()
+    assert np.array_equal(fused, sep)
+    c.close()
+    d.close()
+
+
+def test_zero_context_gives_zero_row(gpu):
+    c = Case(gpu, wl.BF16, 8, 2, 128, 16, [10, 0, 3], seed=9)
+    c.context_lens_override = None
+    pool = c.cache.layer(0)
+    cl = torch.tensor([11, 0, 4], dtype=torch.int32, device=gpu)
+    out = pool.decode_attention(_to_dev(c.q, wl.BF16, gpu), torch.from_numpy(c.tables).to(gpu), cl,
+                                max_context_len=11, out_dtype=torch.float32)
+    o = out.cpu().numpy()
+    assert np.all(o[1] == 0) and np.abs(o[0]).sum() > 0
+    c.close()
+
+
+def test_reference_f32_op_order(gpu):
+    # f32 pool: compare with the restatement of the reference's own op order
+    # (write -> gather -> pad -> build_mask -> sdpa, transformer.rs:271-292)
+    B, H, KVH, hd, bs = 6, 16, 4, 64, 16
+    ctx = [3, 40, 17, 100, 0, 64]
+    c = Case(gpu, wl.F32, H, KVH, hd, bs, ctx, seed=3, fused=True)
+    got = c.run()
+    kp, vp = c.kp.copy(), c.vp.copy()
+    ref = oracle.decode_step_f32(kp, vp, bs, c.tables.astype(np.uint32), c.ctx, c.ctx,
+                                 c.q, c.kn, c.vn, c.scale)
+    _close(got, ref.astype(np.float64), "reference op order")
+    c.close()
+
+
+def test_out_of_range_block_id_reported(gpu):
+    c = Case(gpu, wl.BF16, 8, 2, 128, 16, [40, 20], seed=4)
+    c.tables[0, 1] = c.cache.num_blocks + 7
+    c.run_ok = False
+    with pytest.raises(pagedkv.PagedKvError):
+        c.run()
+    c.close()
+
+
+@pytest.mark.parametrize("cfg,B,lo,hi", [(wl.CFG1, 8, 128, 1024), (wl.CFG2, 56, 256, 2048),
+                                         (wl.CFG3, 32, 512, 4096), (wl.CFG4, 6, 2048, 8192)])
+def test_config_shapes(gpu, cfg, B, lo, hi):
+    ctx = wl.randint(cfg.n_layers * 7 + B, B, lo, hi)
+    c = Case(gpu, cfg.dtype, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.block_size, ctx,
+             seed=cfg.n_head + B, fused=True)
+    got = c.run(out_dtype=TD[cfg.dtype])
+    ref, _, _ = c.reference()
+    _close(got, ref, cfg.name)
+    c.close()
+
+
+def test_batched_equals_solo(gpu):
+    # the reference's batched_matches_solo (paged_batching.rs:40-51) at the
+    # attention level: a row's result does not depend on its batch mates
+    ctx = list(wl.randint(12, 10, 1, 3000))
+    c = Case(gpu, wl.BF16, 32, 8, 128, 16, ctx, seed=12)
+    full = c.run()
+    pool = c.cache.layer(0)
+    for b in (0, 3, 9):
+        out = pool.decode_attention(_to_dev(c.q[b:b + 1], wl.BF16, gpu),
+                                    torch.from_numpy(c.tables[b:b + 1]).to(gpu),
+                                    torch.from_numpy(c.context_lens[b:b + 1]).to(gpu),
+                                    max_context_len=int(c.context_lens.max()), scale=c.scale,
+                                    out_dtype=torch.float32)
+        np.testing.assert_allclose(out.cpu().numpy()[0], full[b], rtol=1e-5, atol=1e-6)
+    c.close()

@@ -1,0 +1,190 @@
+"""GPU parity of the byte-moving kernels (append/scatter, gather, block copy,
+compaction) against the CPU oracle: bit-exact, and no other byte changes."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pagedkv
+from pagedkv import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+TD = {wl.F32: torch.float32, wl.F16: torch.float16, wl.BF16: torch.bfloat16}
+ND = {wl.F32: np.float32, wl.F16: np.uint16, wl.BF16: np.uint16}
+
+
+def _host_pool(cache, layer):
+    """Layer's K and V as (num_blocks, bs, kvh, hd) storage arrays."""
+    nd = ND[pagedkv.pkv_dtype(cache.dtype)]
+    shp = (cache.num_blocks, cache.block_size, cache.n_kv_head, cache.head_dim)
+    k = cache.read_bytes(layer, pagedkv.K).view(nd).reshape(shp)
+    v = cache.read_bytes(layer, pagedkv.V).view(nd).reshape(shp)
+    return k, v
+
+
+def _to_dev(a, dt, device):
+    """Storage array (float32 or uint16 bits) -> device tensor of dtype dt."""
+    a = np.ascontiguousarray(a)
+    if dt == wl.F32:
+        return torch.from_numpy(a).to(device)
+    return torch.from_numpy(a.view(np.int16)).view(TD[dt]).to(device)
+
+
+def _fill(cache, seed):
+    dt = pagedkv.pkv_dtype(cache.dtype)
+    shp = (cache.num_blocks, cache.block_size, cache.n_kv_head, cache.head_dim)
+    for l in range(cache.n_layers):
+        cache.write_bytes(l, pagedkv.K, wl.normal_storage(seed + 2 * l, shp, dt))
+        cache.write_bytes(l, pagedkv.V, wl.normal_storage(seed + 2 * l + 1, shp, dt))
+
+
+@pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
+@pytest.mark.parametrize("hd,kvh,bs", [(128, 8, 16), (64, 4, 32), (256, 2, 16)])
+def test_append_bit_exact_and_untouched(gpu, dt, hd, kvh, bs):
+    cache = pagedkv.PagedKvCache(2, 40, bs, kvh, hd, TD[dt])
+    _fill(cache, 100)
+    k0, v0 = _host_pool(cache, 1)
+    n = 37
+    rng = np.random.default_rng(hd + bs)
+    slots = rng.choice(40 * bs, size=n, replace=False).astype(np.int32)
+    slots[[3, 11]] = -1  # padding tokens are skipped
+    k = wl.normal_storage(7, (n, kvh, hd), dt)
+    v = wl.normal_storage(8, (n, kvh, hd), dt)
+    cache.layer(1).append(_to_dev(k, dt, gpu), _to_dev(v, dt, gpu), slots)
+    cache.check()
+    k1, v1 = _host_pool(cache, 1)
+    ek = k0.reshape(-1, kvh, hd).copy()
+    ev = v0.reshape(-1, kvh, hd).copy()
+    keep = slots >= 0
+    ek[slots[keep]] = k[keep]
+    ev[slots[keep]] = v[keep]
+    assert np.array_equal(k1.reshape(-1, kvh, hd).view(np.uint8), ek.view(np.uint8))
+    assert np.array_equal(v1.reshape(-1, kvh, hd).view(np.uint8), ev.view(np.uint8))
+    # layer 0 untouched
+    a0, b0 = _host_pool(cache, 0)
+    assert np.array_equal(a0, wl.normal_storage(100, a0.shape, dt))
+    cache.close()
+
+
+def test_append_out_of_range_slot_is_reported_not_written(gpu):
+    cache = pagedkv.PagedKvCache(1, 8, 16, 2, 64, torch.bfloat16)
+    k0, _ = _host_pool(cache, 0)
+    k = torch.ones((2, 2, 64), dtype=torch.bfloat16, device=gpu)
+    cache.layer(0).append(k, k, [5, 8 * 16])  # second slot is one past the pool
+    with pytest.raises(pagedkv.PagedKvError) as e:
+        cache.check()
+    assert e.value.code == pagedkv._lib.PKV_ERR_DEVICE_DATA
+    k1, _ = _host_pool(cache, 0)
+    diff = np.nonzero((k1 != k0).reshape(8 * 16, -1).any(1))[0]
+    assert diff.tolist() == [5]
+    cache.check()  # cleared
+    cache.close()
+
+
+def test_kvpool_write_matches_reference_write(gpu):
+    # KvPool::write(alloc, table, start_pos, k, v) -- attention.rs:57-83
+    dt, bs, kvh, hd = wl.BF16, 16, 4, 128
+    cache = pagedkv.PagedKvCache(1, 12, bs, kvh, hd, TD[dt])
+    alloc = pagedkv.BlockAllocator(12, bs)
+    t = pagedkv.BlockTable()
+    alloc.ensure_capacity(t, 50)
+    kp, vp = _host_pool(cache, 0)
+    kp, vp = kp.copy(), vp.copy()
+    k = wl.normal_storage(1, (20, kvh, hd), dt)
+    v = wl.normal_storage(2, (20, kvh, hd), dt)
+    cache.layer(0).write(alloc, t, 30, _to_dev(k, dt, gpu), _to_dev(v, dt, gpu))
+    oracle.kv_write(kp, vp, bs, np.array(t.blocks, np.uint32), 30, k, v)
+    k1, v1 = _host_pool(cache, 0)
+    assert np.array_equal(k1, kp) and np.array_equal(v1, vp)
+    gk, gv = cache.layer(0).gather_seq(t, 50)
+    ok, ov = oracle.gather_seq(kp, vp, bs, np.array(t.blocks, np.uint32), 50)
+    gkn = gk.cpu().view(torch.int16).numpy().view(np.uint16)
+    gvn = gv.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(gkn, ok) and np.array_equal(gvn, ov)
+    cache.close()
+
+
+@pytest.mark.parametrize("dt", [wl.F16, wl.F32])
+def test_gather_bit_exact(gpu, dt):
+    bs, kvh, hd = 32, 2, 64
+    cache = pagedkv.PagedKvCache(1, 30, bs, kvh, hd, TD[dt])
+    _fill(cache, 5)
+    kp, vp = _host_pool(cache, 0)
+    table = wl.permutation(3, 30)[:9].astype(np.uint32)
+    for length in (1, 31, 32, 33, 9 * 32):
+        gk, gv = cache.layer(0).gather_seq(table.tolist(), length)
+        ok, ov = oracle.gather_seq(kp, vp, bs, table, length)
+        if dt == wl.F32:
+            assert np.array_equal(gk.cpu().numpy(), ok) and np.array_equal(gv.cpu().numpy(), ov)
+        else:
+            assert np.array_equal(gk.cpu().view(torch.int16).numpy().view(np.uint16), ok)
+            assert np.array_equal(gv.cpu().view(torch.int16).numpy().view(np.uint16), ov)
+    cache.close()
+
+
+def _all_bytes(cache):
+    return np.concatenate([np.concatenate([cache.read_bytes(l, pagedkv.K), cache.read_bytes(l, pagedkv.V)])
+                           for l in range(cache.n_layers)])
+
+
+def test_copy_blocks_bit_exact(gpu):
+    cache = pagedkv.PagedKvCache(3, 50, 16, 8, 128, torch.bfloat16)
+    _fill(cache, 9)
+    before = _all_bytes(cache)
+    src = [3, 3, 17, 40, 0]
+    dst = [10, 11, 49, 2, 1]
+    cache.copy_blocks(src, dst)
+    cache.check()
+    after = _all_bytes(cache)
+    exp = before.copy()
+    oracle.copy_blocks(exp, 3, cache.block_bytes, src, dst)
+    assert np.array_equal(after, exp)
+    cache.close()
+
+
+@pytest.mark.parametrize("case", ["prefix", "cycles", "mixed"])
+def test_compact_in_place_bit_exact(gpu, case):
+    N = 96
+    cache = pagedkv.PagedKvCache(2, N, 16, 4, 128, torch.bfloat16)
+    _fill(cache, 77)
+    rng = np.random.default_rng({"prefix": 1, "cycles": 2, "mixed": 3}[case])
+    if case == "prefix":  # survivors -> contiguous prefix under a random remap
+        surv = np.sort(rng.choice(N, size=40, replace=False))
+        dst = rng.permutation(40)
+        src = surv
+    elif case == "cycles":  # a pure permutation of a subset (cycles only)
+        src = rng.choice(N, size=30, replace=False)
+        dst = rng.permutation(src)
+    else:  # chains + cycles + identity moves
+        src = np.array([5, 6, 7, 20, 21, 30, 31, 32, 50, 60], np.int32)
+        dst = np.array([6, 7, 8, 21, 20, 31, 32, 30, 50, 0], np.int32)
+    before = _all_bytes(cache)
+    cache.compact(src, dst)
+    cache.check()
+    after = _all_bytes(cache)
+    exp = before.copy()
+    oracle.compact(exp, 2, cache.block_bytes, src, dst)
+    assert np.array_equal(after, exp)
+    cache.close()
+
+
+def test_compact_rejects_duplicates(gpu):
+    cache = pagedkv.PagedKvCache(1, 8, 16, 2, 64, torch.float16)
+    with pytest.raises(pagedkv.PagedKvError):
+        cache.compact([1, 2], [3, 3])
+    with pytest.raises(pagedkv.PagedKvError):
+        cache.compact([1, 1], [3, 4])
+    cache.close()
+
+
+def test_fill_normal_deterministic_and_standard(gpu):
+    cache = pagedkv.PagedKvCache(1, 64, 16, 8, 128, torch.bfloat16)
+    cache.fill_normal(123)
+    a = cache.read_bytes(0, pagedkv.K).view(np.uint16)
+    cache.fill_normal(123)
+    b = cache.read_bytes(0, pagedkv.K).view(np.uint16)
+    assert np.array_equal(a, b)
+    x = wl.widen(a, wl.BF16)
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1) < 0.01
+    cache.close()
