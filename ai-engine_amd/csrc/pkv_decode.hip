@@ -26,15 +26,20 @@
 //     row) and P.V is accumulated in fp32 FMAs, so the softmax weights never
 //     lose precision.
 // Split-context: a sequence with n_parts > 1 partitions writes (m, l, O)
-// partials; the last wave of (b, g) to finish (agent-scope atomic counter)
-// merges them with log-sum-exp weights and resets the counter, so a whole
-// layer is one launch and no second pass is needed.
+// partials; a second, small kernel merges them with log-sum-exp weights.
+// (A last-arriver merge inside the main kernel needs agent-scope release/
+// acquire fences per wave, i.e. an L2 writeback + invalidate on every XCD;
+// measured on MI355X that cost more than half the kernel's throughput.  The
+// kernel boundary provides the same visibility once per launch.)
 //
 // Fused append: with k_new/v_new given, the wave owning the last partition
-// of (b, g) stores the new token's K/V row at position context_len-1
-// (slot = table[pos / bs] * bs + pos % bs, block_table.rs:55-58) and uses
-// the new row from the input for that token, i.e. write-then-attend exactly
-// as transformer.rs:276-277.
+// of (b, g) first stores the new token's K/V row at position context_len-1
+// (slot = table[pos / bs] * bs + pos % bs, block_table.rs:55-58), makes it
+// visible to itself with a workgroup-scope fence, and then reads it back
+// like every other row -- write-then-attend exactly as transformer.rs:276-277,
+// with no data-dependent loads in the main loop.
+#include <type_traits>
+
 #include "pkv_device.h"
 #include "pkv_internal.h"
 
@@ -89,7 +94,6 @@ struct DecodeKArgs {
   const char* v_new;
   float* part_ml;
   float* part_o;
-  uint32_t* counters;
   uint32_t* err;
 };
 
@@ -193,6 +197,9 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       st16(a.k_pool + off + lane * 16, ld16(knew_row + lane * 16));
       st16(a.v_pool + off + lane * 16, ld16(vnew_row + lane * 16));
     }
+    // Release/acquire at workgroup scope: the stores are complete and
+    // visible to this wave's loads of the same rows below.
+    __threadfence_block();
   }
 
   // Loads address a row as a wave-uniform base (pool + head + physical
@@ -217,7 +224,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 
   // K fragments of one tile: sub-tile st, token lane % 16, k-slice lane / 16.
   // Tokens past t_end are clamped to t_end - 1 (a valid row; their scores are
-  // masked).  The new token's row comes from k_new, not from the pool.
+  // masked).
   auto load_k = [&](u32x4 (&kf)[C::NST][C::NF], int tile_base) {
 #pragma unroll
     for (int st = 0; st < C::NST; ++st) {
@@ -228,16 +235,6 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       const char* base = kh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
 #pragma unroll
       for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(base + off + 64 * f);
-    }
-    if (new_pos >= tile_base && new_pos < tile_base + C::TILE) {
-#pragma unroll
-      for (int st = 0; st < C::NST; ++st) {
-        const int tok = min(tile_base + 16 * st + col, t_end - 1);
-        if (tok == new_pos) {
-#pragma unroll
-          for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(knew_row + 64 * f + 16 * G);
-        }
-      }
     }
   };
   // V chunks of one tile: load i covers TPL consecutive tokens (one block),
@@ -250,13 +247,6 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
       const char* base = vh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
       vf[i] = ld16(base + (uint32_t)((tok & tmask) * slot_stride) + 16 * c);
-    }
-    if (new_pos >= tile_base && new_pos < tile_base + C::TILE) {
-#pragma unroll
-      for (int i = 0; i < C::NV; ++i) {
-        const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
-        if (tok == new_pos) vf[i] = ld16(vnew_row + 16 * c);
-      }
     }
   };
 
@@ -276,8 +266,11 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   u32x4 kf[C::NST][C::NF];
   load_k(kf, t_begin);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int tile_base = t_begin + t * C::TILE;
+  // One tile: V loads issued first, QK^T on the K already in registers,
+  // then (PREFETCH) the next tile's K loads, softmax, P.V.  The last tile is
+  // instantiated without the prefetch so that every load count in the loop
+  // is static and the compiler can wait for exactly the loads it needs.
+  auto tile_body = [&](const int tile_base, auto prefetch) {
     u32x4 vf[C::NV];
     load_v(vf, tile_base);
 
@@ -288,7 +281,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 #pragma unroll
       for (int f = 0; f < C::NF; ++f) mfma_frag<DT>(qf[f], kf[st][f], acc[st]);
     }
-    if (t + 1 < ntiles) load_k(kf, tile_base + C::TILE);
+    if constexpr (decltype(prefetch)::value) load_k(kf, tile_base + C::TILE);
 
     // ---- online softmax (exp2 domain) ----
     float sc[C::NST][4];
@@ -356,7 +349,10 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
         for (int e = 0; e < C::EPL; ++e) o[h][e] = fmaf(ph[h], x[e], o[h][e]);
     }
     __builtin_amdgcn_wave_barrier();
-  }
+  };
+  for (int t = 0; t + 1 < ntiles; ++t)
+    tile_body(t_begin + t * C::TILE, std::true_type{});
+  tile_body(t_begin + (ntiles - 1) * C::TILE, std::false_type{});
 
   // ---- partition epilogue ----
 #pragma unroll
@@ -408,20 +404,28 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       ml[2 * h + 1] = lh[h];
     }
   }
-  __threadfence();
-  uint32_t prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(a.counters + pair, 1u, __ATOMIC_ACQ_REL,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  prev = (uint32_t)readlane_i((int)prev, 0);
-  if (prev != (uint32_t)(n_parts - 1)) return;
-  __threadfence();
-  if (lane == 0)
-    __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-  // ---- merge the partitions of (b, g) ----
-  const float* mlb = a.part_ml + pair * a.max_parts * R * 2;
-  const float* pob = a.part_o + pair * a.max_parts * R * HD;
+// Merge of the partitions of (b, g) for sequences with more than one
+// partition: M = max_p m_p, L = sum_p l_p 2^(m_p - M),
+// O = sum_p O_p 2^(m_p - M) / L (all in the exp2 domain of the main kernel).
+// One wave per (b, g); context clamping identical to the main kernel.
+__global__ void __launch_bounds__(kWavesPerBlock * kWave)
+    decode_merge_kernel(DecodeKArgs a, int R, int HD, int dt) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const long long pair = (long long)blockIdx.x * kWavesPerBlock + wave;
+  if (pair >= (long long)a.batch * a.kvh) return;
+  const int b = (int)(pair / a.kvh);
+  const int g = (int)(pair % a.kvh);
+  const int BS = 1 << a.bs_log2;
+  int ctx = a.context_lens[b];
+  ctx = ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
+  const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  if (n_parts <= 1) return;
+  const int H = a.kvh * R;
+  const float* mlb = a.part_ml + (size_t)pair * a.max_parts * R * 2;
+  const float* pob = a.part_o + (size_t)pair * a.max_parts * R * HD;
   for (int idx = lane * 4; idx < R * HD; idx += 4 * kWave) {
     const int h = idx / HD;
     const int d = idx - h * HD;
@@ -432,7 +436,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     for (int pp = 0; pp < n_parts; ++pp) {
       float w = fast_exp2(mlb[(pp * R + h) * 2] - M);
       L += w * mlb[(pp * R + h) * 2 + 1];
-      f32x4 v4 = *reinterpret_cast<const f32x4*>(pob + (pp * R + h) * HD + d);
+      f32x4 v4 = *reinterpret_cast<const f32x4*>(pob + ((size_t)pp * R + h) * HD + d);
       acc4 += w * v4;
     }
     float inv = 1.0f / L;
@@ -441,7 +445,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) = acc4 * inv;
     } else {
       uint32_t w0, w1;
-      if (DT == PKV_BF16) {
+      if (dt == PKV_BF16) {
         w0 = f32_to_bf16_bits(acc4[0] * inv) | (f32_to_bf16_bits(acc4[1] * inv) << 16);
         w1 = f32_to_bf16_bits(acc4[2] * inv) | (f32_to_bf16_bits(acc4[3] * inv) << 16);
       } else {
@@ -503,10 +507,12 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   (void)n_head;
   long long pairs = (long long)batch * p->n_kv_head;
   int mc = max_context_len > 0 ? max_context_len : 1;
-  // Partition length: 256 tokens (64 KB of K+V per bf16 head of 128) keeps
-  // partial traffic ~3% of the K/V stream; shorter partitions are used when
-  // the batch is too small to give every CU several waves.
-  int pt = 256;
+  // Partition length: 512 tokens (256 KB of K+V per bf16 head of 128) keeps
+  // the partial (m, l, O) traffic of the split-context merge near 1.5% of
+  // the K/V stream (measured: 512 beats 256 by ~7% on the Llama-3-8B
+  // decode); shorter partitions are used when the batch is too small to
+  // give every CU several waves.
+  int pt = 512;
   while (pt > 64 && pairs * ((mc + pt - 1) / pt) < 4096) pt >>= 1;
   // The per-partition table slice must fit one wave (<= 64 block ids).
   while (pt > 64 && (pt >> ilog2i(p->block_size)) + 1 > 64) pt >>= 1;
@@ -520,9 +526,9 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
   decode_plan(p, batch, n_head, max_context_len, &pt, &mp);
   size_t pairs = (size_t)batch * p->n_kv_head;
   size_t R = (size_t)(n_head / p->n_kv_head);
-  size_t cb = ((pairs * 4 + 255) / 256) * 256;
+  size_t cb = 0;  // no counters: the merge is a separate kernel
   if (counter_bytes) *counter_bytes = cb;
-  if (mp <= 1) return cb;
+  if (mp <= 1) return 256;
   size_t ml = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   size_t po = pairs * mp * R * (size_t)p->head_dim * 4;
   return cb + ml + po;
@@ -553,18 +559,22 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.k_new = reinterpret_cast<const char*>(a.k_new);
   k.v_new = reinterpret_cast<const char*>(a.v_new);
-  k.counters = reinterpret_cast<uint32_t*>(p->ws);
   size_t cb = p->ws_counter_bytes;
   size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   k.part_ml = reinterpret_cast<float*>(p->ws + cb);
   k.part_o = reinterpret_cast<float*>(p->ws + cb + ml_bytes);
   k.err = p->err;
   long long items = (long long)pairs * mp;
+  hipError_t e;
   switch (p->dtype) {
-    case PKV_F32: return launch_hd<PKV_F32>(p->head_dim, R, k, items, stream);
-    case PKV_F16: return launch_hd<PKV_F16>(p->head_dim, R, k, items, stream);
-    default: return launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream);
+    case PKV_F32: e = launch_hd<PKV_F32>(p->head_dim, R, k, items, stream); break;
+    case PKV_F16: e = launch_hd<PKV_F16>(p->head_dim, R, k, items, stream); break;
+    default: e = launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream); break;
   }
+  if (e != hipSuccess || mp <= 1) return e;
+  unsigned grid = (unsigned)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
+  decode_merge_kernel<<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->head_dim, p->dtype);
+  return hipGetLastError();
 }
 
 }  // namespace pkv
