@@ -120,6 +120,59 @@ __device__ __forceinline__ void store_out(void* out, size_t elem_off, int out_f3
   }
 }
 
+__device__ __forceinline__ int clamp_ctx(const DecodeKArgs& a, int ctx, int BS) {
+  return ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int y = __builtin_amdgcn_ds_bpermute((lane - off) << 2, x);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Work list of one launch, in dispatch order: first every full partition
+// (p < n_parts(b) - 1, PT tokens each) in sequence order, then the last,
+// shorter partition of every sequence (p = n_parts(b) - 1; p = 0 with an
+// empty context).  Hardware dispatch in grid order then approximates
+// longest-first scheduling, and the grid's surplus waves (the host sizes it
+// for the longest context) all sit past the end of the list.  Each wave
+// finds its (b, p) from the context lengths: 64 sequences per step, wave
+// prefix sum of full-partition counts, ballot for the owning lane.
+__device__ bool locate_pair(const DecodeKArgs& a, long long kpair, int lane, int BS,
+                            int& b, int& p) {
+  long long base = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int bb = b0 + lane;
+    int f = 0;
+    if (bb < a.batch) {
+      const int ctx = clamp_ctx(a, a.context_lens[bb], BS);
+      const int np = (ctx + a.part_tokens - 1) / a.part_tokens;
+      f = np > 1 ? np - 1 : 0;
+    }
+    const int incl = wave_incl_scan(f, lane);
+    const int excl = incl - f;
+    const unsigned long long hit = __ballot(kpair >= base + excl && kpair < base + incl);
+    if (hit) {
+      const int hl = __ffsll((long long)hit) - 1;
+      b = b0 + hl;
+      p = (int)(kpair - base - readlane_i(excl, hl));
+      return true;
+    }
+    base += readlane_i(incl, 63);
+  }
+  const long long k2 = kpair - base;
+  if (k2 >= a.batch) return false;
+  b = (int)k2;
+  const int ctx = clamp_ctx(a, a.context_lens[b], BS);
+  const int np = (ctx + a.part_tokens - 1) / a.part_tokens;
+  p = np > 0 ? np - 1 : 0;
+  return true;
+}
+
 template <int DT, int HD, int R>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
@@ -132,22 +185,17 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int lane = threadIdx.x & 63;
   float* p_lds = p_lds_all[wave];
 
-  const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
-  const int g = (int)(item % a.kvh);
-  const long long bp = item / a.kvh;
-  const int p = (int)(bp % a.max_parts);
-  const int b = (int)(bp / a.max_parts);
-  if (b >= a.batch) return;
-
   const int H = a.kvh * R;
   const int BS = 1 << a.bs_log2;
-  int ctx = a.context_lens[b];
-  bool clamped = false;
-  if (ctx > a.max_context_len || ctx > a.mbps * BS || ctx < 0) {
-    if (lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
-    ctx = ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
-    clamped = true;
-  }
+  const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
+  const int g = (int)(item % a.kvh);
+  int b = 0, p = 0;
+  if (!locate_pair(a, item / a.kvh, lane, BS, b, p)) return;
+
+  const int ctx_raw = a.context_lens[b];
+  const int ctx = clamp_ctx(a, ctx_raw, BS);
+  const bool clamped = ctx != ctx_raw;
+  if (clamped && lane == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
   const int PT = a.part_tokens;
   const int n_parts = (ctx + PT - 1) / PT;
   const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
@@ -173,24 +221,33 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= 64 (plan)
   const int new_pos = (a.k_new != nullptr && !clamped) ? ctx - 1 : -1;
 
-  // Block-table slice of this partition: lane i holds entry blk_begin + i.
+  const int G = lane >> 4;
+  const int col = lane & 15;
+
+  // Prologue loads are issued together: the block-table slice of this
+  // partition (lane i holds entry blk_begin + i) and the Q group as the MFMA
+  // A operand (row = head lane % 16, k-slice lane / 16).
   int tbl = 0;
-  if (lane < nblk) {
-    int e = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
-    if (e < 0 || e >= a.num_blocks) {
-      atomicOr(a.err, PKV_EBIT_BLOCK);
-      e = 0;
-    }
-    tbl = e;
+  if (lane < nblk) tbl = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
+  u32x4 qf[C::NF];
+  {
+    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * C::RB;
+#pragma unroll
+    for (int f = 0; f < C::NF; ++f)
+      qf[f] = col < R ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
+  }
+  if (lane < nblk && (tbl < 0 || tbl >= a.num_blocks)) {
+    atomicOr(a.err, PKV_EBIT_BLOCK);
+    tbl = 0;
   }
 
   const size_t head_off = (size_t)g * C::RB;
   const size_t slot_stride = (size_t)a.kvh * C::RB;
-  const char* knew_row = a.k_new ? a.k_new + ((size_t)b * a.kvh + g) * C::RB : nullptr;
-  const char* vnew_row = a.v_new ? a.v_new + ((size_t)b * a.kvh + g) * C::RB : nullptr;
 
   // Fused append: store the new token's row (write before attend).
   if (new_pos >= 0 && p == n_parts - 1) {
+    const char* knew_row = a.k_new + ((size_t)b * a.kvh + g) * C::RB;
+    const char* vnew_row = a.v_new + ((size_t)b * a.kvh + g) * C::RB;
     int blk = readlane_i(tbl, (new_pos >> a.bs_log2) - blk_begin);
     size_t off = ((size_t)blk * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
     if (lane < C::CH) {
@@ -202,52 +259,32 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     __threadfence_block();
   }
 
-  // Loads address a row as a wave-uniform base (pool + head + physical
-  // block, an SGPR pair) plus a 32-bit per-lane offset (slot in block,
-  // 16-byte fragment), which keeps the address math scalar.
+  // A row is addressed as a wave-uniform base (pool + head + physical block)
+  // plus a 32-bit per-lane offset (slot in block, 16-byte fragment).
+  // Tokens past t_end are clamped to t_end - 1: a valid row whose score is
+  // masked (K) or whose weight is exactly 0 (V).
   const char* kh = a.k_pool + head_off;
   const char* vh = a.v_pool + head_off;
   const size_t blk_stride = (size_t)BS * slot_stride;
   const int tmask = BS - 1;
   const int lg = a.bs_log2;
 
-  // ---- Q group as MFMA A operand: row = head (lane % 16), k-slice lane / 16
-  const int G = lane >> 4;
-  const int col = lane & 15;
-  u32x4 qf[C::NF];
-  {
-    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * C::RB;
-#pragma unroll
-    for (int f = 0; f < C::NF; ++f)
-      qf[f] = col < R ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
-  }
-
-  // K fragments of one tile: sub-tile st, token lane % 16, k-slice lane / 16.
-  // Tokens past t_end are clamped to t_end - 1 (a valid row; their scores are
-  // masked).
-  auto load_k = [&](u32x4 (&kf)[C::NST][C::NF], int tile_base) {
-#pragma unroll
-    for (int st = 0; st < C::NST; ++st) {
-      const int t0 = min(tile_base + 16 * st, t_end - 1);
-      const int tok = min(tile_base + 16 * st + col, t_end - 1);
-      const uint32_t off = (uint32_t)((tok & tmask) * slot_stride) + 16 * G;
-      // block_size >= 16: the 16 tokens of a sub-tile share one block
-      const char* base = kh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
-#pragma unroll
-      for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(base + off + 64 * f);
-    }
+  // K fragment f of sub-tile st: token lane % 16, k-slice lane / 16; the four
+  // lanes of a token read 64 contiguous bytes.  block_size >= 16, so the 16
+  // tokens of a sub-tile share one block.
+  auto k_row = [&](int tile_base, int st) {
+    const int t0 = min(tile_base + 16 * st, t_end - 1);
+    const int tok = min(tile_base + 16 * st + col, t_end - 1);
+    const char* base = kh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
+    return base + ((uint32_t)((tok & tmask) * slot_stride) + 16 * G);
   };
-  // V chunks of one tile: load i covers TPL consecutive tokens (one block),
-  // lane = (token group tg, 16-byte chunk c): consecutive lanes read
-  // consecutive 16 bytes of a row.
-  auto load_v = [&](u32x4 (&vf)[C::NV], int tile_base) {
-#pragma unroll
-    for (int i = 0; i < C::NV; ++i) {
-      const int t0 = min(tile_base + i * C::TPL, t_end - 1);
-      const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
-      const char* base = vh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
-      vf[i] = ld16(base + (uint32_t)((tok & tmask) * slot_stride) + 16 * c);
-    }
+  // V load i of a tile: TPL consecutive tokens (one block), lane = (token
+  // group tg, 16-byte chunk c): consecutive lanes read consecutive bytes.
+  auto v_chunk = [&](int tile_base, int i) {
+    const int t0 = min(tile_base + i * C::TPL, t_end - 1);
+    const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
+    const char* base = vh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
+    return base + ((uint32_t)((tok & tmask) * slot_stride) + 16 * c);
   };
 
   float m[4], lsum[4];
@@ -264,24 +301,37 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 
   const int ntiles = (t_end - t_begin + C::TILE - 1) / C::TILE;
   u32x4 kf[C::NST][C::NF];
-  load_k(kf, t_begin);
+  u32x4 vf[C::NV];
+#pragma unroll
+  for (int st = 0; st < C::NST; ++st) {
+    const char* r = k_row(t_begin, st);
+#pragma unroll
+    for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(r + 64 * f);
+  }
+#pragma unroll
+  for (int i = 0; i < C::NV; ++i) vf[i] = ld16(v_chunk(t_begin, i));
 
-  // One tile: V loads issued first, QK^T on the K already in registers,
-  // then (PREFETCH) the next tile's K loads, softmax, P.V.  The last tile is
-  // instantiated without the prefetch so that every load count in the loop
-  // is static and the compiler can wait for exactly the loads it needs.
+  // One tile, software-pipelined at distance one tile: every K fragment is
+  // reloaded with the next tile's fragment right after its MFMA has read
+  // it, and every V chunk right after its P.V, so a whole tile of loads is
+  // always in flight and the registers are reused in place.  The last tile
+  // is instantiated without the reloads, which keeps all load counts static
+  // for the compiler's wait insertion.
   auto tile_body = [&](const int tile_base, auto prefetch) {
-    u32x4 vf[C::NV];
-    load_v(vf, tile_base);
-
+    constexpr bool PF = decltype(prefetch)::value;
+    const int next = tile_base + C::TILE;
     f32x4 acc[C::NST];
 #pragma unroll
     for (int st = 0; st < C::NST; ++st) {
       acc[st] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int f = 0; f < C::NF; ++f) mfma_frag<DT>(qf[f], kf[st][f], acc[st]);
+      if constexpr (PF) {
+        const char* r = k_row(next, st);
+#pragma unroll
+        for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(r + 64 * f);
+      }
     }
-    if constexpr (decltype(prefetch)::value) load_k(kf, tile_base + C::TILE);
 
     // ---- online softmax (exp2 domain) ----
     float sc[C::NST][4];
@@ -301,13 +351,13 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       float mnew = fmaxf(m[j], tmax);
       alpha[j] = fast_exp2(m[j] - mnew);
       m[j] = mnew;
-      float s = 0.0f;
+      float ssum = 0.0f;
 #pragma unroll
       for (int st = 0; st < C::NST; ++st) {
         sc[st][j] = fast_exp2(sc[st][j] - mnew);
-        s += sc[st][j];
+        ssum += sc[st][j];
       }
-      lsum[j] = lsum[j] * alpha[j] + s;
+      lsum[j] = lsum[j] * alpha[j] + ssum;
     }
     if (G < C::RG) {
 #pragma unroll
@@ -343,6 +393,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       }
       float x[C::EPL];
       widen16<DT, C::EPL>(vf[i], x);
+      if constexpr (PF) vf[i] = ld16(v_chunk(next, i));
 #pragma unroll
       for (int h = 0; h < R; ++h)
 #pragma unroll
@@ -419,8 +470,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int b = (int)(pair / a.kvh);
   const int g = (int)(pair % a.kvh);
   const int BS = 1 << a.bs_log2;
-  int ctx = a.context_lens[b];
-  ctx = ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
+  const int ctx = clamp_ctx(a, a.context_lens[b], BS);
   const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
   if (n_parts <= 1) return;
   const int H = a.kvh * R;
