@@ -460,12 +460,18 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 // Merge of the partitions of (b, g) for sequences with more than one
 // partition: M = max_p m_p, L = sum_p l_p 2^(m_p - M),
 // O = sum_p O_p 2^(m_p - M) / L (all in the exp2 domain of the main kernel).
-// One wave per (b, g); context clamping identical to the main kernel.
+// One wave per query head (b, g, h): lane d covers HD / 64 consecutive
+// dimensions; the per-partition (m, l) pairs are wave-uniform.  Context
+// clamping is identical to the main kernel.
+template <int HD>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
-    decode_merge_kernel(DecodeKArgs a, int R, int HD, int dt) {
+    decode_merge_kernel(DecodeKArgs a, int R, int dt) {
+  constexpr int DPL = HD / kWave;  // dims per lane: 1, 2 or 4
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const long long pair = (long long)blockIdx.x * kWavesPerBlock + wave;
+  const long long qh = (long long)blockIdx.x * kWavesPerBlock + wave;  // (b, g, h)
+  const long long pair = qh / R;
+  const int h = (int)(qh - pair * R);
   if (pair >= (long long)a.batch * a.kvh) return;
   const int b = (int)(pair / a.kvh);
   const int g = (int)(pair % a.kvh);
@@ -473,39 +479,32 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int ctx = clamp_ctx(a, a.context_lens[b], BS);
   const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
   if (n_parts <= 1) return;
-  const int H = a.kvh * R;
-  const float* mlb = a.part_ml + (size_t)pair * a.max_parts * R * 2;
-  const float* pob = a.part_o + (size_t)pair * a.max_parts * R * HD;
-  for (int idx = lane * 4; idx < R * HD; idx += 4 * kWave) {
-    const int h = idx / HD;
-    const int d = idx - h * HD;
-    float M = -INFINITY;
-    for (int pp = 0; pp < n_parts; ++pp) M = fmaxf(M, mlb[(pp * R + h) * 2]);
-    float L = 0.0f;
-    f32x4 acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int pp = 0; pp < n_parts; ++pp) {
-      float w = fast_exp2(mlb[(pp * R + h) * 2] - M);
-      L += w * mlb[(pp * R + h) * 2 + 1];
-      f32x4 v4 = *reinterpret_cast<const f32x4*>(pob + ((size_t)pp * R + h) * HD + d);
-      acc4 += w * v4;
-    }
-    float inv = 1.0f / L;
-    size_t eo = ((size_t)b * H + g * R + h) * HD + d;
-    if (a.out_f32) {
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) = acc4 * inv;
-    } else {
-      uint32_t w0, w1;
-      if (dt == PKV_BF16) {
-        w0 = f32_to_bf16_bits(acc4[0] * inv) | (f32_to_bf16_bits(acc4[1] * inv) << 16);
-        w1 = f32_to_bf16_bits(acc4[2] * inv) | (f32_to_bf16_bits(acc4[3] * inv) << 16);
-      } else {
-        w0 = f32_to_f16_bits(acc4[0] * inv) | (f32_to_f16_bits(acc4[1] * inv) << 16);
-        w1 = f32_to_f16_bits(acc4[2] * inv) | (f32_to_f16_bits(acc4[3] * inv) << 16);
-      }
-      uint32_t* o32 = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + eo);
-      o32[0] = w0;
-      o32[1] = w1;
-    }
+  const float* mlb = a.part_ml + (size_t)pair * a.max_parts * R * 2 + 2 * h;
+  const float* pob = a.part_o + ((size_t)pair * a.max_parts * R + h) * HD + lane * DPL;
+  float M = -INFINITY;
+  for (int pp = 0; pp < n_parts; ++pp) M = fmaxf(M, mlb[(size_t)pp * R * 2]);
+  float L = 0.0f;
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
+  for (int pp = 0; pp < n_parts; ++pp) {
+    const float w = fast_exp2(mlb[(size_t)pp * R * 2] - M);
+    L += w * mlb[(size_t)pp * R * 2 + 1];
+    const float* op = pob + (size_t)pp * R * HD;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] += w * op[i];
+  }
+  const float inv = 1.0f / L;
+  const size_t eo = ((size_t)b * a.kvh * R + g * R + h) * HD + lane * DPL;
+  if (a.out_f32) {
+    float* o = reinterpret_cast<float*>(a.out) + eo;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = acc[i] * inv;
+  } else {
+    uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + eo;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i)
+      o[i] = (uint16_t)(dt == PKV_BF16 ? f32_to_bf16_bits(acc[i] * inv) : f32_to_f16_bits(acc[i] * inv));
   }
 }
 
@@ -622,8 +621,12 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
     default: e = launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream); break;
   }
   if (e != hipSuccess || mp <= 1) return e;
-  unsigned grid = (unsigned)((pairs + kWavesPerBlock - 1) / kWavesPerBlock);
-  decode_merge_kernel<<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->head_dim, p->dtype);
+  unsigned grid = (unsigned)((pairs * R + kWavesPerBlock - 1) / kWavesPerBlock);
+  switch (p->head_dim) {
+    case 64: decode_merge_kernel<64><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+    case 128: decode_merge_kernel<128><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+    default: decode_merge_kernel<256><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+  }
   return hipGetLastError();
 }
 
