@@ -255,6 +255,10 @@ int pkv_pool_destroy(pkv_pool* p) {
   if (p->base) (void)hipFree(p->base);
   if (p->err) (void)hipFree(p->err);
   if (p->ws) (void)hipFree(p->ws);
+  for (auto& ev : p->prof_events) {
+    (void)hipEventDestroy(ev.first);
+    (void)hipEventDestroy(ev.second);
+  }
   delete p;
   return PKV_OK;
 }
@@ -439,7 +443,19 @@ int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int o
   if (int rc = ensure_workspace(p, need, cb)) return rc;
   pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
                     max_context_len, batch, n_head, scale, k_new, v_new};
-  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream));
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (p->prof_on) {
+    if (p->prof_used == p->prof_events.size()) {
+      hipEvent_t x = nullptr, y = nullptr;
+      if (hipEventCreate(&x) != hipSuccess || hipEventCreate(&y) != hipSuccess)
+        return fail(p, PKV_ERR_HIP, "profile: hipEventCreate failed");
+      p->prof_events.emplace_back(x, y);
+    }
+    eb = p->prof_events[p->prof_used].first;
+    ee = p->prof_events[p->prof_used].second;
+    ++p->prof_used;
+  }
+  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "decode launch");
   return PKV_OK;
 }
@@ -470,6 +486,29 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale};
   hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(p, e, "prefill launch");
+  return PKV_OK;
+}
+
+int pkv_pool_profile(pkv_pool* p, int enable) {
+  CHECK_POOL(p);
+  p->prof_on = enable != 0;
+  return PKV_OK;
+}
+
+int pkv_pool_profile_read(pkv_pool* p, double* total_ms, int* launches) {
+  CHECK_POOL(p);
+  DeviceGuard dg(p->device);
+  double sum = 0.0;
+  for (size_t i = 0; i < p->prof_used; ++i) {
+    hipError_t e = hipEventSynchronize(p->prof_events[i].second);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, p->prof_events[i].first, p->prof_events[i].second);
+    if (e != hipSuccess) return hip_fail(p, e, "profile read");
+    sum += ms;
+  }
+  if (total_ms) *total_ms = sum;
+  if (launches) *launches = (int)p->prof_used;
+  p->prof_used = 0;
   return PKV_OK;
 }
 

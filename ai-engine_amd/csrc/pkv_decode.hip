@@ -584,7 +584,7 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
 }
 
 hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
-                         hipStream_t stream) {
+                         hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   int pt = 0, mp = 0;
   decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
   size_t pairs = (size_t)a.batch * p->n_kv_head;
@@ -615,12 +615,15 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   k.err = p->err;
   long long items = (long long)pairs * mp;
   hipError_t e;
+  if (ev_begin && (e = hipEventRecord(ev_begin, stream)) != hipSuccess) return e;
   switch (p->dtype) {
     case PKV_F32: e = launch_hd<PKV_F32>(p->head_dim, R, k, items, stream); break;
     case PKV_F16: e = launch_hd<PKV_F16>(p->head_dim, R, k, items, stream); break;
     default: e = launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream); break;
   }
-  if (e != hipSuccess || mp <= 1) return e;
+  if (e != hipSuccess) return e;
+  if (ev_end && (e = hipEventRecord(ev_end, stream)) != hipSuccess) return e;
+  if (mp <= 1) return e;
   unsigned grid = (unsigned)((pairs * R + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (p->head_dim) {
     case 64: decode_merge_kernel<64><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;

@@ -7,6 +7,8 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/pagedkv.h"
 
@@ -26,10 +28,15 @@ struct pkv_pool {
   size_t layer_bytes = 0;  // one layer's K (or V): num_blocks * block_bytes
   char* base = nullptr;    // device slab
   uint32_t* err = nullptr; // device error word, bit set by kernels
-  // decode workspace: [counters][partials]; counters stay zero between calls
+  // decode workspace: split-context partials (m, l, O); ws_counter_bytes is
+  // a reserved prefix (0 in this version)
   char* ws = nullptr;
   size_t ws_bytes = 0;
   size_t ws_counter_bytes = 0;
+  // main-kernel timing events (pkv_pool_profile)
+  bool prof_on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
+  size_t prof_used = 0;
   std::string last_error;
 
   char* layer_k(int layer) const {
@@ -90,8 +97,11 @@ void decode_plan(const pkv_pool* p, int batch, int n_head,
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
                               int max_context_len, size_t* counter_bytes);
 bool decode_supported(const pkv_pool* p, int n_head);
+// ev_begin / ev_end (may be null) are recorded on `stream` right before and
+// right after the main partition kernel.
 hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
-                         hipStream_t stream);
+                         hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                         hipEvent_t ev_end = nullptr);
 
 struct PrefillArgs {
   const void* q;

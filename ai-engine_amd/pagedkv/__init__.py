@@ -215,6 +215,17 @@ class PagedKvCache:
         """Raise if a kernel met an out-of-range id or length since last check."""
         check(lib().pkv_pool_check(self._h), self._h)
 
+    def profile(self, enable: bool) -> None:
+        """Record HIP events around every decode call's main kernel."""
+        check(lib().pkv_pool_profile(self._h, 1 if enable else 0), self._h)
+
+    def profile_read(self) -> tuple[float, int]:
+        """(summed main-kernel ms, launches) since the last read."""
+        ms = ctypes.c_double()
+        n = ctypes.c_int()
+        check(lib().pkv_pool_profile_read(self._h, ctypes.byref(ms), ctypes.byref(n)), self._h)
+        return float(ms.value), int(n.value)
+
     def reserve_decode(self, batch: int, n_head: int, max_context_len: int) -> None:
         check(lib().pkv_pool_reserve_decode(self._h, batch, n_head, max_context_len), self._h)
 

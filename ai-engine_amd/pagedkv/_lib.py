@@ -51,6 +51,8 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_prefill_attention": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                    ctypes.c_float, _P]),
     "pkv_pool_check": (_I, [_P]),
+    "pkv_pool_profile": (_I, [_P, _I]),
+    "pkv_pool_profile_read": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "pkv_allocator_new": (_P, [_SZ, _SZ]),
     "pkv_allocator_free": (None, [_P]),
     "pkv_allocator_free_count": (_SZ, [_P]),

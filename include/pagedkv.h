@@ -185,6 +185,15 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_seqs, int max_q_len, int max_context_len,
                           int n_head, float scale, void* stream);
 
+/* Kernel timing (instrumentation; no reference counterpart).  While enabled,
+ * every pkv_decode_attention call records HIP events, owned by the pool, on
+ * its stream right before and right after its main (partition) kernel --
+ * not around the split-context merge.  pkv_pool_profile_read synchronises,
+ * returns the summed main-kernel time in ms and the number of timed
+ * launches since the last read, and clears the record. */
+int pkv_pool_profile(pkv_pool* pool, int enable);
+int pkv_pool_profile_read(pkv_pool* pool, double* total_ms, int* launches);
+
 /* Synchronise the pool's device and report (then clear) any out-of-range
  * slot/block id or length a kernel met since the last check:
  * PKV_OK or PKV_ERR_DEVICE_DATA. */

@@ -239,3 +239,16 @@ def test_batched_equals_solo(gpu):
                                     out_dtype=torch.float32)
         np.testing.assert_allclose(out.cpu().numpy()[0], full[b], rtol=1e-5, atol=1e-6)
     c.close()
+
+
+def test_profile_hook_times_main_kernel(gpu):
+    c = Case(gpu, wl.BF16, 32, 8, 128, 16, list(wl.randint(3, 16, 100, 2000)), seed=31)
+    c.cache.profile(True)
+    for _ in range(3):
+        c.run()
+    ms, n = c.cache.profile_read()
+    assert n == 3 and ms > 0
+    c.cache.profile(False)
+    c.run()
+    assert c.cache.profile_read() == (0.0, 0)
+    c.close()
