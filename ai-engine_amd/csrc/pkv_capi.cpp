@@ -411,6 +411,22 @@ int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_
   return ensure_workspace(p, need, cb);
 }
 
+// Timing events for the next attention call's main kernel when profiling is
+// on (pkv_pool_profile); both stay null otherwise.
+static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
+  if (!p->prof_on) return PKV_OK;
+  if (p->prof_used == p->prof_events.size()) {
+    hipEvent_t x = nullptr, y = nullptr;
+    if (hipEventCreate(&x) != hipSuccess || hipEventCreate(&y) != hipSuccess)
+      return fail(p, PKV_ERR_HIP, "profile: hipEventCreate failed");
+    p->prof_events.emplace_back(x, y);
+  }
+  *eb = p->prof_events[p->prof_used].first;
+  *ee = p->prof_events[p->prof_used].second;
+  ++p->prof_used;
+  return PKV_OK;
+}
+
 int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
                          const int32_t* block_tables, int max_blocks_per_seq,
                          const int32_t* context_lens, int max_context_len, int batch,
@@ -444,17 +460,7 @@ int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int o
   pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
                     max_context_len, batch, n_head, scale, k_new, v_new};
   hipEvent_t eb = nullptr, ee = nullptr;
-  if (p->prof_on) {
-    if (p->prof_used == p->prof_events.size()) {
-      hipEvent_t x = nullptr, y = nullptr;
-      if (hipEventCreate(&x) != hipSuccess || hipEventCreate(&y) != hipSuccess)
-        return fail(p, PKV_ERR_HIP, "profile: hipEventCreate failed");
-      p->prof_events.emplace_back(x, y);
-    }
-    eb = p->prof_events[p->prof_used].first;
-    ee = p->prof_events[p->prof_used].second;
-    ++p->prof_used;
-  }
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
   hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "decode launch");
   return PKV_OK;
@@ -484,7 +490,9 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
   DeviceGuard dg(p->device);
   pkv::PrefillArgs a{q, out, out_dtype, cu_q_lens, context_lens, block_tables,
                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale};
-  hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream));
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
+  hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "prefill launch");
   return PKV_OK;
 }

@@ -119,6 +119,7 @@ struct PrefillArgs {
 };
 bool prefill_supported(const pkv_pool* p, int n_head);
 hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
-                          hipStream_t stream);
+                          hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                          hipEvent_t ev_end = nullptr);
 
 }  // namespace pkv

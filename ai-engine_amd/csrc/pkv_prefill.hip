@@ -358,7 +358,7 @@ bool prefill_supported(const pkv_pool* p, int n_head) {
 }
 
 hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
-                          hipStream_t stream) {
+                          hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   PrefillKArgs k{};
   k.k_pool = p->layer_k(layer);
   k.v_pool = p->layer_v(layer);
@@ -378,11 +378,16 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.err = p->err;
   int R = a.n_head / p->n_kv_head;
+  hipError_t e = hipSuccess;
+  if (ev_begin) e = hipEventRecord(ev_begin, stream);
+  if (e != hipSuccess) return e;
   switch (p->dtype) {
-    case PKV_F32: return plaunch_hd<PKV_F32>(p->head_dim, R, k, stream);
-    case PKV_F16: return plaunch_hd<PKV_F16>(p->head_dim, R, k, stream);
-    default: return plaunch_hd<PKV_BF16>(p->head_dim, R, k, stream);
+    case PKV_F32: e = plaunch_hd<PKV_F32>(p->head_dim, R, k, stream); break;
+    case PKV_F16: e = plaunch_hd<PKV_F16>(p->head_dim, R, k, stream); break;
+    default: e = plaunch_hd<PKV_BF16>(p->head_dim, R, k, stream); break;
   }
+  if (e == hipSuccess && ev_end) e = hipEventRecord(ev_end, stream);
+  return e;
 }
 
 }  // namespace pkv

@@ -176,3 +176,71 @@ def decode_bytes(shape: Shape, ctx: np.ndarray, n_layers: int | None = None) -> 
     per = (c1 * kvh * hd * 2 * e + 2 * kvh * hd * e * 2 + 2 * H * hd * e
            + 4 * (-(-c1 // shape.block_size)) + 12)
     return int(per.sum()) * L
+
+
+@dataclasses.dataclass
+class MixBatch:
+    """One continuous-batching step: `prior`/`chunk` of the sequences in
+    chunked prefill, `ctx` of the decoding ones, and one block table per
+    sequence (prefill sequences first) over a shared pool."""
+    shape: Shape
+    prior: np.ndarray        # (Sp,) int64 tokens cached before the chunk
+    chunk: np.ndarray        # (Sp,) int64 chunk tokens appended this step
+    ctx: np.ndarray          # (Sd,) int64 seq_lens of decoding sequences
+    tables: np.ndarray       # (Sp + Sd, max_nb) int32, -1 padded
+    num_blocks: int
+
+    @property
+    def n_prefill(self) -> int:
+        return int(self.prior.size)
+
+    @property
+    def cu_q_lens(self) -> np.ndarray:
+        return np.concatenate([[0], np.cumsum(self.chunk)]).astype(np.int32)
+
+    def chunk_slots(self) -> np.ndarray:
+        """Slot (block * bs + offset) of every chunk token, in cu_q_lens order."""
+        bs = self.shape.block_size
+        out = []
+        for s in range(self.n_prefill):
+            pos = np.arange(self.prior[s], self.prior[s] + self.chunk[s])
+            out.append(self.tables[s, pos // bs].astype(np.int64) * bs + pos % bs)
+        return np.concatenate(out).astype(np.int32)
+
+
+def mix_batch(shape: Shape, n_prefill: int, chunk: int, prior_lo: int, prior_hi: int,
+              n_decode: int, ctx_lo: int, ctx_hi: int, seed: int,
+              pool_factor: float = 1.2) -> MixBatch:
+    """Priors U[prior_lo, prior_hi], decode contexts U[ctx_lo, ctx_hi];
+    pool = ceil(pool_factor * live / bs); tables from one permutation."""
+    bs = shape.block_size
+    prior = randint(seed, n_prefill, prior_lo, prior_hi)
+    ctx = randint(seed + 1, n_decode, ctx_lo, ctx_hi)
+    lens = np.concatenate([prior + chunk, ctx + 1])
+    need = -(-lens // bs)
+    num_blocks = max(int(math.ceil(pool_factor * int(lens.sum()) / bs)), int(need.sum()))
+    perm = permutation(seed ^ 0x5EED, num_blocks)
+    tables = np.full((lens.size, int(need.max())), -1, dtype=np.int32)
+    o = 0
+    for s in range(lens.size):
+        tables[s, :need[s]] = perm[o:o + need[s]]
+        o += int(need[s])
+    return MixBatch(shape, prior, np.full(n_prefill, chunk, np.int64), ctx, tables, num_blocks)
+
+
+def prefill_bytes(shape: Shape, prior: np.ndarray, chunk: np.ndarray) -> int:
+    """Algorithmic HBM bytes of one layer's prefill attention: K and V reads
+    of prior + chunk rows, Q read and O write of the chunk (the chunk's K/V
+    store is the append's, counted there)."""
+    e = 4 if shape.dtype == F32 else 2
+    kvh, hd, H = shape.n_kv_head, shape.head_dim, shape.n_head
+    p, c = prior.astype(np.int64), chunk.astype(np.int64)
+    return int(((p + c) * kvh * hd * 2 * e + 2 * c * H * hd * e).sum())
+
+
+def prefill_flops(shape: Shape, prior: np.ndarray, chunk: np.ndarray) -> int:
+    """Algorithmic flops of one layer's causal prefill attention: QK^T and
+    PV over the unmasked (query, key) pairs, 2 flops per multiply-add."""
+    p, c = prior.astype(np.int64), chunk.astype(np.int64)
+    pairs = c * p + c * (c + 1) // 2
+    return int((4 * shape.head_dim * shape.n_head * pairs).sum())

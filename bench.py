@@ -49,7 +49,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg5"])
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg2", "cfg5"])
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="layer passes of the CPU baseline sample (0 = skip)")
@@ -75,6 +75,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.config == "cfg5":
         return churn(args, dev)
+    if args.config == "cfg2":
+        return mix(args, dev)
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
     L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
@@ -242,6 +244,193 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
             "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
                        f"{args.cpu_layers} passes of {dt:.2f} s, scaled x{shape.n_layers} layers"),
             "agrees_with_gpu": agree}
+
+
+def mix(args, dev) -> int:
+    """TinyLlama-1.1B continuous-batching mix (22
+    layers, 32q/4kv heads, hd 64, bs 16, f16).  Per layer: the 8 sequences
+    in chunked prefill store their 256-token chunk (pkv_append) and attend
+    it causally over prior context U[0,1024] (pkv_prefill_attention); the
+    56 decoding sequences (context U[256,2048]) append one token and attend
+    (pkv_decode_attention, fused append).  value = tokens advanced per
+    second (8*256 + 56 per step).  roofline = the prefill kernel's
+    algorithmic flops (unmasked query-key pairs) over its average duration
+    against 2.5 PFLOP/s dense f16; the decode kernel's HBM roofline beside."""
+    import numpy as np
+    import torch
+
+    import pagedkv
+    from pagedkv import workload as wl
+
+    shape = wl.CFG2
+    L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
+    NP, C, ND = 8, 256, 56
+    m = wl.mix_batch(shape, NP, C, 0, 1024, ND, 256, 2048, args.seed)
+    T = NP * C
+    log(f"[bench] cfg2: {NP} prefill chunks of {C} (priors {m.prior.tolist()}), {ND} decode "
+        f"(ctx mean {m.ctx.mean():.0f}), pool {m.num_blocks} blocks x {L} layers")
+    tdt = torch.float16
+    cache = pagedkv.PagedKvCache(L, m.num_blocks, bs, KVH, hd, tdt)
+    cache.fill_normal(args.seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+
+    def rnd(*shp, sc=1.0):
+        return (torch.randn(shp, generator=g, device=dev, dtype=torch.float32) * sc).to(tdt)
+
+    sc = 1.0 / math.sqrt(hd)
+    qp, kc, vc = rnd(L, T, H, hd, sc=sc), rnd(L, T, KVH, hd), rnd(L, T, KVH, hd)
+    qd, kd, vd = rnd(L, ND, H, hd, sc=sc), rnd(L, ND, KVH, hd), rnd(L, ND, KVH, hd)
+    outp = torch.empty((L, T, H * hd), dtype=tdt, device=dev)
+    outd = torch.empty((L, ND, H * hd), dtype=tdt, device=dev)
+    tables = np.where(m.tables < 0, 0, m.tables).astype(np.int32)
+    ptab = torch.from_numpy(np.ascontiguousarray(tables[:NP])).to(dev)
+    dtab = torch.from_numpy(np.ascontiguousarray(tables[NP:])).to(dev)
+    slots = torch.from_numpy(m.chunk_slots()).to(dev)
+    cu = torch.from_numpy(m.cu_q_lens).to(dev)
+    pctx_np = (m.prior + m.chunk).astype(np.int32)
+    dctx_np = (m.ctx + 1).astype(np.int32)
+    pctx, dctx = torch.from_numpy(pctx_np).to(dev), torch.from_numpy(dctx_np).to(dev)
+    max_p, max_d = int(pctx_np.max()), int(dctx_np.max())
+    mbps = tables.shape[1]
+    cache.reserve_decode(ND, H, max_d)
+    torch.cuda.synchronize()
+
+    lib = pagedkv.lib()
+    stream = torch.cuda.current_stream(dev)
+    sp = int(stream.cuda_stream) or None
+    h = cache.handle
+    odt = pagedkv.pkv_dtype(tdt)
+    chk = pagedkv._lib.check
+
+    def append(l):
+        rc = lib.pkv_append(h, l, kc[l].data_ptr(), vc[l].data_ptr(), slots.data_ptr(), T, sp)
+        if rc:
+            chk(rc, h)
+
+    def prefill(l):
+        rc = lib.pkv_prefill_attention(h, l, qp[l].data_ptr(), outp[l].data_ptr(), odt,
+                                       cu.data_ptr(), pctx.data_ptr(), ptab.data_ptr(), mbps, NP, C,
+                                       max_p, H, sc, sp)
+        if rc:
+            chk(rc, h)
+
+    def decode(l):
+        rc = lib.pkv_decode_attention(h, l, qd[l].data_ptr(), outd[l].data_ptr(), odt,
+                                      dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND, H, sc,
+                                      kd[l].data_ptr(), vd[l].data_ptr(), sp)
+        if rc:
+            chk(rc, h)
+
+    def step():
+        for l in range(L):
+            append(l)
+            prefill(l)
+            decode(l)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    cache.check()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+
+    n_kt = max(1, min(args.steps, 5))
+
+    def kernel_ms(fn):
+        cache.profile(True)
+        for _ in range(n_kt):
+            for l in range(L):
+                fn(l)
+        torch.cuda.synchronize()
+        tot, n = cache.profile_read()
+        cache.profile(False)
+        return tot / max(1, n), n
+
+    pre_ms, pre_n = kernel_ms(prefill)
+    dec_ms, dec_n = kernel_ms(decode)
+    t0.record(stream)
+    for _ in range(n_kt):
+        for l in range(L):
+            append(l)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    app_ms = t0.elapsed_time(t1) / (n_kt * L)
+    cache.check()
+
+    flops = wl.prefill_flops(shape, m.prior, m.chunk)
+    pbytes = wl.prefill_bytes(shape, m.prior, m.chunk)
+    dbytes = wl.decode_bytes(shape, m.ctx, 1)
+    abytes = 2 * T * KVH * hd * 2 * 2 + 4 * T
+    tflops = flops / (pre_ms / 1e3) / 1e12
+    dec_gbps = dbytes / (dec_ms / 1e3) / 1e9
+    tok_s = (T + ND) / (ms_step / 1e3)
+    log(f"[bench] {ms_step:.3f} ms/step, {tok_s:.0f} tok/s; per layer: prefill {pre_ms * 1e3:.1f} us "
+        f"({tflops:.1f} TFLOP/s), decode {dec_ms * 1e3:.1f} us ({dec_gbps:.0f} GB/s), "
+        f"chunk append {app_ms * 1e3:.1f} us")
+
+    cpu = None
+    if args.cpu_layers > 0:
+        import oracle
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        shp = (m.num_blocks, bs, KVH, hd)
+        kp = cache.read_bytes(0, pagedkv.K).view(np.uint16).reshape(shp)
+        vp = cache.read_bytes(0, pagedkv.V).view(np.uint16).reshape(shp)
+
+        def host(t):
+            return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+        hq, hk, hv = host(qp[0]), host(kc[0]), host(vc[0])
+        dq, dk, dv = host(qd[0]), host(kd[0]), host(vd[0])
+        oracle.lib()
+        tc = time.time()
+        for _ in range(args.cpu_layers):
+            rp = oracle.prefill_inplace(kp, vp, wl.F16, bs, tables[:NP], m.cu_q_lens, pctx_np, hq, hk,
+                                        hv, sc, n_threads=threads)
+            rd = oracle.decode_inplace(kp, vp, wl.F16, bs, tables[NP:], dctx_np, dq, dk, dv, sc,
+                                       n_threads=threads)
+        dt = (time.time() - tc) / args.cpu_layers
+        gp, gd = outp[0].float().cpu().numpy(), outd[0].float().cpu().numpy()
+        agree = bool(np.all(np.abs(gp - rp) <= 1e-3 + 2e-2 * np.abs(rp))
+                     and np.all(np.abs(gd - rd) <= 1e-3 + 2e-2 * np.abs(rd)))
+        log(f"[bench] cpu baseline: {dt:.2f} s/layer (gpu/cpu layer-0 agreement: {agree})")
+        cpu = {"value": round((T + ND) / (dt * L), 2), "unit": "tok/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"layer 0 of the same mix (chunk store + causal prefill of {NP}x{C}, "
+                          f"append + decode of {ND}), {args.cpu_layers} passes of {dt:.2f} s, "
+                          f"scaled x{L} layers"),
+               "agrees_with_gpu": agree}
+
+    res = {
+        "metric": "continuous-batching mix tokens/s (chunked prefill + decode), TinyLlama-1.1B shape, 1 GPU",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, random block tables)",
+        "config": {"workload": "cfg2: 22 layers, 32q/4kv heads, hd 64, bs 16, f16 KV; 8 chunked "
+                               "prefills of 256 over prior U[0,1024] + 56 decodes, ctx U[256,2048]",
+                   "priors": m.prior.tolist(), "mean_decode_context": round(float(m.ctx.mean()), 1),
+                   "seed": args.seed, "num_blocks": m.num_blocks, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "pkv::prefill_kernel", "kernel_avg_us": round(pre_ms * 1e3, 2),
+                     "algorithmic_flops_per_launch": flops,
+                     "algorithmic_bytes_per_launch": pbytes},
+        "roofline_decode": {"bound": "hbm", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS,
+                            "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
+                            "kernel": "pkv::decode_kernel", "kernel_avg_us": round(dec_ms * 1e3, 2),
+                            "algorithmic_bytes_per_launch": dbytes},
+        "append": {"us": round(app_ms * 1e3, 2), "GBps": round(abytes / (app_ms / 1e3) / 1e9, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    cache.close()
+    return 0
 
 
 def churn(args, dev) -> int:

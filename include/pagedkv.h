@@ -186,9 +186,10 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_head, float scale, void* stream);
 
 /* Kernel timing (instrumentation; no reference counterpart).  While enabled,
- * every pkv_decode_attention call records HIP events, owned by the pool, on
- * its stream right before and right after its main (partition) kernel --
- * not around the split-context merge.  pkv_pool_profile_read synchronises,
+ * every pkv_decode_attention and pkv_prefill_attention call records HIP
+ * events, owned by the pool, on its stream right before and right after its
+ * main kernel -- the partition kernel of decode, not its split-context
+ * merge; the one kernel of prefill.  pkv_pool_profile_read synchronises,
  * returns the summed main-kernel time in ms and the number of timed
  * launches since the last read, and clears the record. */
 int pkv_pool_profile(pkv_pool* pool, int enable);

@@ -72,6 +72,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_decode_inplace.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P, _P,
                                      _SZ, _SZ, ctypes.c_float, _P, ctypes.c_int]
     L.orc_decode_inplace.restype = None
+    L.orc_prefill_inplace.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _SZ,
+                                      _P, _P, _P, _SZ, ctypes.c_float, _P, ctypes.c_int]
+    L.orc_prefill_inplace.restype = None
     L.orc_threads.argtypes = [ctypes.c_int]
     L.orc_threads.restype = ctypes.c_int
 
@@ -255,6 +258,25 @@ def decode_inplace(k_pool, v_pool, dtype: int, block_size: int, tables, ctx_lens
     lib().orc_decode_inplace(_p(k_pool), _p(v_pool), dtype, block_size, KVH, hd, _p(tables),
                              tables.shape[1], _p(cl), _p(q), kn, vn, B, H, float(scale),
                              _p(out), int(n_threads))
+    return out
+
+
+def prefill_inplace(k_pool, v_pool, dtype: int, block_size: int, tables, cu_q_lens, ctx_lens,
+                    q, k_new, v_new, scale: float, n_threads: int = 0) -> np.ndarray:
+    """CPU baseline: reference prefill math (f32, causal) over a prior
+    context, chunk K/V stored first, in place, OpenMP.  Pools/q/k_new/v_new
+    hold stored elements of `dtype`; q (T, H, hd).  Returns (T, H*hd) f32."""
+    KVH, hd = k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.int32)
+    cu = np.ascontiguousarray(cu_q_lens, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    T, H = q.shape[0], q.shape[1]
+    out = np.empty((T, H * hd), dtype=np.float32)
+    kn = _p(k_new) if k_new is not None else None
+    vn = _p(v_new) if v_new is not None else None
+    lib().orc_prefill_inplace(_p(k_pool), _p(v_pool), dtype, block_size, KVH, hd, _p(tables),
+                              tables.shape[1], _p(cu), _p(cl), cl.size, _p(q), kn, vn, H,
+                              float(scale), _p(out), int(n_threads))
     return out
 
 

@@ -490,6 +490,113 @@ void orc_decode_inplace(void* k_pool, void* v_pool, int dtype, size_t bs,
     }
 }
 
+/* CPU baseline for chunked prefill: the reference's prefill_seq attention
+ * math (transformer.rs:139-148,179-196: per-token K/V store, then
+ * S = q.k^T * scale with the causal mask, max/exp/sum/divide softmax, P.V,
+ * all f32) in place on the pool, extended to a prior context: sequence s's
+ * chunk of ql = cu_q[s+1]-cu_q[s] tokens sits at positions
+ * ctx_lens[s]-ql .. ctx_lens[s]-1.  k_new/v_new (T, KVH, hd) are stored first
+ * when non-NULL.  OpenMP over (sequence, query head, 16-query row block). */
+void orc_prefill_inplace(void* k_pool, void* v_pool, int dtype, size_t bs,
+                         size_t KVH, size_t hd, const int32_t* tables,
+                         size_t max_nb, const int32_t* cu_q,
+                         const int32_t* ctx_lens, size_t n_seqs, const void* q,
+                         const void* k_new, const void* v_new, size_t H,
+                         float scale, float* out, int n_threads) {
+    const size_t es = orc_esize(dtype);
+    const size_t rep = H / KVH;
+    const size_t RB = 16;
+    if (k_new) {
+        for (size_t sq = 0; sq < n_seqs; sq++) {
+            size_t q0 = (size_t)cu_q[sq], ql = (size_t)(cu_q[sq + 1] - cu_q[sq]);
+            size_t p0 = (size_t)ctx_lens[sq] - ql;
+            for (size_t i = 0; i < ql; i++) {
+                size_t pos = p0 + i;
+                size_t slot = (size_t)tables[sq * max_nb + pos / bs] * bs + pos % bs;
+                memcpy((char*)k_pool + slot * KVH * hd * es,
+                       (const char*)k_new + (q0 + i) * KVH * hd * es, KVH * hd * es);
+                memcpy((char*)v_pool + slot * KVH * hd * es,
+                       (const char*)v_new + (q0 + i) * KVH * hd * es, KVH * hd * es);
+            }
+        }
+    }
+    size_t n_work = 0, maxn = 1;
+    for (size_t sq = 0; sq < n_seqs; sq++) {
+        size_t ql = (size_t)(cu_q[sq + 1] - cu_q[sq]);
+        n_work += H * ((ql + RB - 1) / RB);
+        if ((size_t)ctx_lens[sq] > maxn) maxn = (size_t)ctx_lens[sq];
+    }
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#pragma omp parallel
+#endif
+    {
+        float* s = (float*)malloc(sizeof(float) * RB * maxn);
+        float* qf = (float*)malloc(sizeof(float) * RB * hd);
+        float* kf = (float*)malloc(sizeof(float) * hd);
+        float* acc = (float*)malloc(sizeof(float) * RB * hd);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long long w = 0; w < (long long)n_work; w++) {
+            /* locate (sequence, head, row block) of work item w */
+            size_t rem = (size_t)w, sq = 0, nrb = 0;
+            for (; sq < n_seqs; sq++) {
+                size_t ql = (size_t)(cu_q[sq + 1] - cu_q[sq]);
+                nrb = (ql + RB - 1) / RB;
+                if (rem < H * nrb) break;
+                rem -= H * nrb;
+            }
+            size_t h = rem / nrb, rb = rem % nrb, g = h / rep;
+            size_t q0 = (size_t)cu_q[sq], ql = (size_t)(cu_q[sq + 1] - cu_q[sq]);
+            size_t n = (size_t)ctx_lens[sq], p0 = n - ql;
+            size_t i0 = rb * RB, ni = ql - i0 < RB ? ql - i0 : RB;
+            size_t nk = p0 + i0 + ni; /* keys the block's last row attends */
+            const int32_t* tb = tables + sq * max_nb;
+            for (size_t r = 0; r < ni; r++)
+                for (size_t d = 0; d < hd; d++)
+                    qf[r * hd + d] = orc_load(q, dtype, ((q0 + i0 + r) * H + h) * hd + d);
+            for (size_t p = 0; p < nk; p++) {
+                size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                for (size_t d = 0; d < hd; d++) kf[d] = orc_load(k_pool, dtype, base + d);
+                for (size_t r = 0; r < ni; r++) {
+                    float dot = 0.0f;
+                    for (size_t d = 0; d < hd; d++) dot += qf[r * hd + d] * kf[d];
+                    /* causal mask (transformer.rs:139-148): key p > query position -> -inf */
+                    s[r * maxn + p] = p > p0 + i0 + r ? -INFINITY : dot * scale;
+                }
+            }
+            for (size_t r = 0; r < ni; r++) {
+                float mx = -INFINITY, sum = 0.0f;
+                float* sr = s + r * maxn;
+                for (size_t p = 0; p < nk; p++) mx = sr[p] > mx ? sr[p] : mx;
+                for (size_t p = 0; p < nk; p++) {
+                    sr[p] = expf(sr[p] - mx);
+                    sum += sr[p];
+                }
+                for (size_t p = 0; p < nk; p++) sr[p] /= sum;
+            }
+            for (size_t i = 0; i < ni * hd; i++) acc[i] = 0.0f;
+            for (size_t p = 0; p < nk; p++) {
+                size_t slot = (size_t)tb[p / bs] * bs + p % bs;
+                size_t base = (slot * KVH + g) * hd;
+                for (size_t d = 0; d < hd; d++) kf[d] = orc_load(v_pool, dtype, base + d);
+                for (size_t r = 0; r < ni; r++) {
+                    float wt = s[r * maxn + p];
+                    for (size_t d = 0; d < hd; d++) acc[r * hd + d] += wt * kf[d];
+                }
+            }
+            for (size_t r = 0; r < ni; r++)
+                memcpy(out + ((q0 + i0 + r) * H + h) * hd, acc + r * hd, sizeof(float) * hd);
+        }
+        free(s);
+        free(qf);
+        free(kf);
+        free(acc);
+    }
+}
+
 /* Number of OpenMP threads the baseline uses for a requested count. */
 int orc_threads(int requested) {
 #ifdef _OPENMP

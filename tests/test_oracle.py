@@ -328,6 +328,39 @@ def test_prefill_brute_force_tiny():
             np.testing.assert_allclose(got[i, h * hd:(h + 1) * hd], o, rtol=1e-12, atol=1e-14)
 
 
+def test_prefill_inplace_baseline_matches_closed_form():
+    # the CPU baseline's chunked prefill (f32, stored chunk K/V first) against
+    # the fp64 closed form over the same pool, two sequences with priors
+    H, KVH, hd, bs = 8, 2, 32, 16
+    priors, chunks = np.array([0, 45]), np.array([37, 20])
+    lens = priors + chunks
+    need = -(-lens // bs)
+    nb = int(need.sum()) + 2
+    perm = wl.permutation(61, nb)
+    tables = np.zeros((2, int(need.max())), np.int32)
+    tables[0, :need[0]] = perm[:need[0]]
+    tables[1, :need[1]] = perm[need[0]:need[0] + need[1]]
+    kp = wl.normal_storage(62, (nb, bs, KVH, hd), wl.F16)
+    vp = wl.normal_storage(63, (nb, bs, KVH, hd), wl.F16)
+    T = int(chunks.sum())
+    q = wl.normal_storage(64, (T, H, hd), wl.F16, scale=1 / math.sqrt(hd))
+    kn = wl.normal_storage(65, (T, KVH, hd), wl.F16)
+    vn = wl.normal_storage(66, (T, KVH, hd), wl.F16)
+    cu = np.array([0, chunks[0], T], np.int32)
+    kp2, vp2 = kp.copy(), vp.copy()
+    out = oracle.prefill_inplace(kp2, vp2, wl.F16, bs, tables, cu, lens.astype(np.int32), q, kn, vn,
+                                 1 / math.sqrt(hd), n_threads=3)
+    # the chunk store is the closed-form scatter
+    kp3, vp3 = kp.copy(), vp.copy()
+    for s_ in range(2):
+        tb = tables[s_].astype(np.uint32)
+        oracle.kv_write(kp3, vp3, bs, tb, int(priors[s_]), kn[cu[s_]:cu[s_ + 1]], vn[cu[s_]:cu[s_ + 1]])
+    assert np.array_equal(kp2, kp3) and np.array_equal(vp2, vp3)
+    ref = oracle.prefill_attention_f64(kp2, vp2, wl.F16, bs, tables.astype(np.uint32), cu, lens,
+                                       wl.widen(q, wl.F16), 1 / math.sqrt(hd))
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
+
+
 # ---------------------------------------------------------------------------
 # block copy / compaction closed forms
 # ---------------------------------------------------------------------------
