@@ -42,6 +42,13 @@ COMMON = [
 ]
 
 
+# Per-source extras.  Prefill keeps its MFMA accumulators in ordinary VGPRs
+# (no AGPR round trips for the softmax rescale; measured faster on gfx950).
+EXTRA = {
+    "pkv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _headers() -> list[str]:
     hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
     hs.append(os.path.join(ROOT, "include", "pagedkv.h"))
@@ -61,7 +68,7 @@ def _stale(src: str, hdr_mtime: float) -> bool:
 
 
 def _compile(src: str) -> tuple[str, int, str]:
-    cmd = [HIPCC, *COMMON]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, [])]
     if src.endswith(".hip"):
         cmd += ["-x", "hip"]
     cmd += ["-c", os.path.join(CSRC, src), "-o", _obj(src)]

@@ -3,6 +3,7 @@
 // Validates every argument on the host (shapes, ranges, alignment, device),
 // records a per-handle error string, and enqueues the HIP kernels on the
 // caller's stream.  No C++ exception crosses the boundary.
+#include <cmath>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -485,6 +486,8 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
     return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
   if (!pkv::prefill_supported(p, n_head))
     return fail(p, PKV_ERR_UNSUPPORTED, "prefill: shape not supported");
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return fail(p, PKV_ERR_INVALID, "prefill: scale must be positive and finite");
   if (out_dtype != PKV_F32 && out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   DeviceGuard dg(p->device);

@@ -8,21 +8,28 @@
 // keys 0 .. its position.  The chunk's own K/V rows are stored first with
 // pkv_append (the reference's per-token KvPool::write loop, :173-177).
 //
-// Work decomposition: one wavefront per (sequence, kv head, tile of 32 rows),
-// a row being a (query token, GQA head) pair, heads consecutive -- so K/V
-// tiles are shared by the whole query group.  Key tiles of 32 keys stream
-// from the pool through the block table.
+// Work decomposition: one workgroup of 4 waves per (sequence, kv head, block
+// of ROWS rows), a row being a (query token, GQA head) pair with the group's
+// heads consecutive, so every K/V tile serves the whole query group.  Each
+// wave owns 16 * NR rows.  Key tiles of KT keys stream from the pool through
+// the block table into double-buffered LDS, K and V row-major (V of f32
+// pools transposed); the PV operand of 16-bit pools comes from
+// ds_read_b64_tr_b16 transposing reads.  Global loads for the next tiles and
+// the block ids after them are in flight while a tile is computed.
 //
-//   S^T = K Q^T on MFMA (K fragments straight from HBM as the A operand, the
-//   rows' Q as the B operand).  The accumulator layout puts, in each lane,
-//   the scores of 8 keys (two 16-key tiles x 4) of ONE row (lane % 16):
-//   exactly the per-lane k-slice of the B operand of O^T = V^T P^T under a
-//   consistent permutation of the key index, so P never leaves registers.
-//   V^T is the A operand, gathered from a padded LDS copy of the V tile
-//   (16-bit gathers, conflict-free).  P is split into a 16-bit high part and
-//   a 16-bit residual, two MFMAs, so the weights keep ~16 significant bits
-//   (f32 pools use v_mfma_f32_16x16x4f32 with exact fp32 P).  Online softmax
-//   per row in the exp2 domain; fp32 accumulation throughout.
+//   S^T = K Q^T on MFMA (K from LDS as the A operand, the rows' Q, held in
+//   registers, as B).  The accumulator puts in each lane the scores of 4
+//   keys per 16-key tile of ONE row (lane % 16): the per-lane k-slice of the
+//   B operand of O^T = V^T P^T, so P never leaves registers.  Online softmax
+//   per row in the exp2 domain, fp32 accumulation throughout.  P enters the
+//   PV product as f16 for f16 pools (relative rounding 2^-12); for bf16 pools
+//   as a bf16 high part plus a bf16 residual (two MFMAs, ~16 significant
+//   bits); for f32 pools exactly, on v_mfma_f32_16x16x4f32.
+//
+// Workgroups are mapped XCD-aware: with at least 8 (sequence, kv head) pairs,
+// XCD x (= blockIdx % 8) serves the pairs congruent to x mod 8, so the row
+// blocks that share a pair's K/V share one L2; row blocks are dispatched
+// longest (last) first.
 #include <type_traits>
 
 #include "pkv_device.h"
@@ -31,21 +38,34 @@
 namespace pkv {
 namespace {
 
-constexpr int kPWaves = 4;  // waves per workgroup (independent items)
-constexpr int kKT = 32;     // keys per tile (two 16-key MFMA tiles)
+constexpr int kPW = 4;   // waves per workgroup
+constexpr int kXcd = 8;  // XCDs; workgroups go round-robin over them
 
 template <int DT, int HD, int R>
 struct PCfg {
   static constexpr int E = DT == PKV_F32 ? 4 : 2;
-  static constexpr int RB = HD * E;                 // row bytes
-  static constexpr int NF = RB / 64;                // 16-B fragments per lane per row
-  static constexpr int NR = (HD <= 128 && DT != PKV_F32) ? 2 : 1;  // 16-row tiles per wave
-  static constexpr int ROWS = 16 * NR;
-  static constexpr int ND = HD / 16;                // 16-dim tiles of O^T
-  static constexpr int CH = RB / 16;                // 16-B chunks per row
-  static constexpr int VPITCH = RB + (DT == PKV_F32 ? 16 : 8);  // LDS row pitch (bytes)
-  static constexpr int TPL = 64 / CH;               // keys per V load
-  static constexpr int NVL = kKT / TPL;             // V loads per key tile
+  static constexpr int RB = HD * E;                                // row bytes
+  static constexpr int NF = RB / 64;                               // 16-B fragments per lane per row
+  static constexpr int NR = (DT != PKV_F32 && HD <= 128) ? 2 : 1;  // 16-row tiles per wave
+  static constexpr int RW = 16 * NR;                               // rows per wave
+  static constexpr int ROWS = kPW * RW;                            // rows per workgroup
+  static constexpr int ND = HD / 16;                               // 16-dim tiles of O^T
+  static constexpr int KT = RB >= 512 ? 32 : 64;                   // keys per tile
+  static constexpr int NKM = KT / 16;                              // 16-key MFMA tiles
+  static constexpr int CH = RB / 16;                               // 16-B chunks per row
+  static constexpr int EPC = 16 / E;                               // elements per chunk
+  static constexpr int KPITCH = RB + 16;                           // K row pitch in LDS
+  static constexpr int VTP = KT * E + 16;                          // f32: V^T row pitch in LDS
+  static constexpr int VP = RB + 32;                               // 16-bit: V row pitch in LDS
+  static constexpr int KLDS = KT * KPITCH;
+  static constexpr int STAGE = KLDS + (DT == PKV_F32 ? HD * VTP : KT * VP);
+  static constexpr int NKL = KT * CH / (kPW * kWave);              // K chunks per thread
+  static constexpr int NVP = (KT / 2) * CH / (kPW * kWave);        // V key-pair chunks per thread
+  // register sets for tiles in flight: loads run NSET + 1 tiles ahead
+  static constexpr int NSET = (NKL + 2 * NVP) <= 4 ? 2 : 1;
+  static constexpr int D = NSET + 1;
+  static_assert(NKL >= 1 && NVP >= 1, "tile too small for the workgroup");
+  static_assert(KT * CH % (kPW * kWave) == 0 && (KT / 2) * CH % (kPW * kWave) == 0, "");
 };
 
 struct PrefillKArgs {
@@ -64,7 +84,8 @@ struct PrefillKArgs {
   int bs_log2;
   int max_q_len;
   int max_context_len;
-  int row_tiles;  // ceil(max_q_len * R / ROWS): grid stride per (seq, head)
+  int row_blocks;  // ceil(max_q_len * R / ROWS)
+  int per_xcd;     // workgroup slots per XCD (affinity mapping), 0 = plain order
   float scale_log2;
   uint32_t* err;
 };
@@ -73,43 +94,74 @@ template <int DT>
 __device__ __forceinline__ uint32_t to16(float x) {
   return DT == PKV_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
 }
+
+constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units): weights <= 256
+
+// Max over the four lane groups (rows of 16 lanes) holding one score row:
+// permlane16_swap pairs rows 0/1 and 2/3, permlane32_swap the two halves.
+__device__ __forceinline__ float row_group_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Two floats to packed 16-bit (round to nearest even, v_cvt_pk_*_f32).
 template <int DT>
-__device__ __forceinline__ float from16(uint32_t h) {
-  return DT == PKV_BF16 ? bf16lo(h) : f16lo(h);
+__device__ __forceinline__ uint32_t cvt_pk16(float x0, float x1) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 v = {x0, x1};
+  if constexpr (DT == PKV_BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+  }
 }
 
 template <int DT, int HD, int R>
-__global__ void __launch_bounds__(kPWaves * kWave) prefill_kernel(PrefillKArgs a) {
+__global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
   using C = PCfg<DT, HD, R>;
-  __shared__ __attribute__((aligned(16))) char v_lds_all[kPWaves][kKT * C::VPITCH];
+  __shared__ __attribute__((aligned(16))) char lds[2 * C::STAGE];
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  char* v_lds = v_lds_all[wave];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int G = lane >> 4;
   const int col = lane & 15;
 
-  // item = (seq, kv head, row tile); row tiles in descending order so the
-  // tiles that see the most keys are dispatched first
-  const long long item = (long long)blockIdx.x * kPWaves + wave;
-  const int rt = a.row_tiles - 1 - (int)(item % a.row_tiles);
-  const long long sg = item / a.row_tiles;
-  const int g = (int)(sg % a.kvh);
-  const int s = (int)(sg / a.kvh);
-  if (s >= a.n_seqs) return;
+  // ---- work item: (sequence, kv head) pair sg, row block rb ----
+  const int n_sg = a.n_seqs * a.kvh;
+  int sg, rb;
+  if (a.per_xcd > 0) {
+    const int x = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
+    const int nx = (n_sg - x + kXcd - 1) / kXcd;  // pairs of this XCD
+    if (slot >= nx * a.row_blocks) return;
+    rb = a.row_blocks - 1 - slot / nx;
+    sg = x + kXcd * (slot % nx);
+  } else {
+    if ((int)blockIdx.x >= n_sg * a.row_blocks) return;
+    rb = a.row_blocks - 1 - (int)blockIdx.x / n_sg;
+    sg = (int)blockIdx.x % n_sg;
+  }
+  const int g = sg % a.kvh;
+  const int s = sg / a.kvh;
 
   const int q0 = a.cu_q_lens[s];
   const int q_len_raw = a.cu_q_lens[s + 1] - q0;
   const int q_len = min(q_len_raw, a.max_q_len);
-  if (q_len_raw > a.max_q_len && lane == 0 && rt == 0 && g == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
+  const bool reporter = tid == 0 && rb == 0 && g == 0;
+  if (q_len_raw > a.max_q_len && reporter) atomicOr(a.err, PKV_EBIT_LENGTH);
   const int BS = 1 << a.bs_log2;
-  int ctx = a.context_lens[s];
+  const int ctx = a.context_lens[s];
   if (ctx > a.max_context_len || ctx > a.mbps * BS || ctx < q_len || q_len < 0) {
-    if (lane == 0 && rt == 0 && g == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
+    if (reporter) atomicOr(a.err, PKV_EBIT_LENGTH);
     return;
   }
-  const int row0 = rt * C::ROWS;
-  if (row0 >= q_len * R) return;
+  const int n_rows = q_len * R;
+  const int row0 = rb * C::ROWS;
+  if (row0 >= n_rows) return;  // uniform over the workgroup
   const int prior = ctx - q_len;
   const int H = a.kvh * R;
   const int tmask = BS - 1;
@@ -119,30 +171,108 @@ __global__ void __launch_bounds__(kPWaves * kWave) prefill_kernel(PrefillKArgs a
   const char* vh = a.v_pool + (size_t)g * C::RB;
   const int32_t* table = a.block_tables + (size_t)s * a.mbps;
 
-  // Rows of this lane (B operand / output): row n = 16 * rn + col.
-  int tok_of[C::NR];
+  // keys the workgroup needs: 0 .. prior + its last token
+  const int n_keys = prior + min(row0 + C::ROWS - 1, n_rows - 1) / R + 1;
+  const int n_tiles = (n_keys + C::KT - 1) / C::KT;
+
+  // ---- this wave's rows (B operand / output): row 16 rn + col ----
+  const int roww = row0 + wave * C::RW;
+  const bool has_rows = roww < n_rows;
+  const int klim_lo = prior + min(roww, n_rows - 1) / R;              // smallest row limit
+  const int klim_hi = prior + min(roww + C::RW - 1, n_rows - 1) / R;  // largest row limit
+  int lim[C::NR];
   u32x4 qf[C::NR][C::NF];
 #pragma unroll
   for (int rn = 0; rn < C::NR; ++rn) {
-    const int r = row0 + 16 * rn + col;
-    const int rc = min(r, q_len * R - 1);
-    tok_of[rn] = rc / R;
+    const int rc = min(roww + 16 * rn + col, n_rows - 1);
+    lim[rn] = prior + rc / R;
     const char* qrow = a.q + ((size_t)(q0 + rc / R) * H + g * R + rc % R) * C::RB;
 #pragma unroll
     for (int f = 0; f < C::NF; ++f) qf[rn][f] = ld16(qrow + 64 * f + 16 * G);
   }
-  // Keys needed: 0 .. prior + last token of the tile.
-  const int last_tok = min((row0 + C::ROWS - 1) / R, q_len - 1);
-  const int n_keys = prior + last_tok + 1;
-  const int n_tiles = (n_keys + kKT - 1) / kKT;
 
-  auto block_of = [&](int key) {
-    int blk = table[key >> a.bs_log2];
-    if (blk < 0 || blk >= a.num_blocks) {
-      atomicOr(a.err, PKV_EBIT_BLOCK);
-      blk = 0;
+  // ---- cooperative tile loads.  K chunk i of a thread: key
+  //      (tid + 256 i) / CH, bytes 16 (tid % CH); V pair chunk v: keys
+  //      2 ((tid + 256 v) / CH) and +1.  CH divides 64, so one wave's share
+  //      of a load covers at most 16 aligned keys -- one block (block_size
+  //      >= 16): its block id is wave-uniform (a scalar load) and a lane
+  //      adds a 32-bit offset.  Keys past n_keys are clamped to n_keys - 1.
+  //      Block ids are checked where they are used; a bad one reads block 0
+  //      and is reported once at the end. ----
+  const int wkey = (wave * kWave) / C::CH;  // wave's first key within a load
+  const int lkey = lane / C::CH;            // lane's key within the wave's share
+  const uint32_t lbyte = 16 * (lane % C::CH);
+  bool bad_block = false;
+  auto table_at = [&](int key) __attribute__((always_inline)) {
+    const int k = min(key, n_keys - 1) >> a.bs_log2;
+    typedef const __attribute__((address_space(4))) int32_t cint;  // read-only: scalar load
+    return *(cint*)(table + k);
+  };
+  auto checked = [&](int blk) __attribute__((always_inline)) {
+    const bool bad = (unsigned)blk >= (unsigned)a.num_blocks;
+    bad_block |= bad;
+    return bad ? 0 : blk;
+  };
+  int kb[2][C::NKL], vb[2][C::NVP];  // raw block ids, two sets by tile parity
+  auto ids = [&](int t, int (&kbs)[C::NKL], int (&vbs)[C::NVP]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::NKL; ++i) kbs[i] = table_at(t * C::KT + wkey + 256 * i / C::CH);
+    if constexpr (DT == PKV_F32) {  // 16-bit pools load V with K's keys and block ids
+#pragma unroll
+      for (int v = 0; v < C::NVP; ++v) vbs[v] = table_at(t * C::KT + 2 * (wkey + 256 * v / C::CH));
     }
-    return blk;
+  };
+  u32x4 kreg[C::NSET][C::NKL], vreg[C::NSET][C::NVP][2];
+  auto loads = [&](int t, u32x4 (&kr)[C::NKL], u32x4 (&vr)[C::NVP][2],
+                   const int (&kbs)[C::NKL], const int (&vbs)[C::NVP]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::NKL; ++i) {
+      const int key = min(t * C::KT + wkey + 256 * i / C::CH + lkey, n_keys - 1);
+      const char* base = kh + (size_t)checked(kbs[i]) * blk_stride;
+      kr[i] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
+    }
+    if constexpr (DT == PKV_F32) {
+#pragma unroll
+      for (int v = 0; v < C::NVP; ++v) {
+        const int k0 = t * C::KT + 2 * (wkey + 256 * v / C::CH + lkey);
+        const char* base = vh + (size_t)checked(vbs[v]) * blk_stride;
+        vr[v][0] = ld16(base + ((uint32_t)((min(k0, n_keys - 1) & tmask) * slot_stride) + lbyte));
+        vr[v][1] = ld16(base + ((uint32_t)((min(k0 + 1, n_keys - 1) & tmask) * slot_stride) + lbyte));
+      }
+    } else {  // V chunk 2 v + h: the same key and bytes as K chunk 2 v + h
+#pragma unroll
+      for (int i = 0; i < C::NKL; ++i) {
+        const int key = min(t * C::KT + wkey + 256 * i / C::CH + lkey, n_keys - 1);
+        const char* base = vh + (size_t)checked(kbs[i]) * blk_stride;
+        vr[i >> 1][i & 1] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
+      }
+    }
+  };
+  auto store = [&](int stage, const u32x4 (&kr)[C::NKL], const u32x4 (&vr)[C::NVP][2]) __attribute__((always_inline)) {
+    char* kl = lds + stage * C::STAGE;
+    char* vl = kl + C::KLDS;
+#pragma unroll
+    for (int i = 0; i < C::NKL; ++i) {
+      const int idx = tid + 256 * i;
+      st16(kl + (idx / C::CH) * C::KPITCH + 16 * (idx % C::CH), kr[i]);
+    }
+    if constexpr (DT == PKV_F32) {  // V^T: dim-major rows, keys in natural order
+#pragma unroll
+      for (int v = 0; v < C::NVP; ++v) {
+        const int idx = tid + 256 * v;
+        char* dst = vl + C::EPC * (idx % C::CH) * C::VTP + 2 * (idx / C::CH) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          *reinterpret_cast<uint64_t*>(dst + e * C::VTP) =
+              (uint64_t)vr[v][0][e] | ((uint64_t)vr[v][1][e] << 32);
+      }
+    } else {  // V row-major like K; read transposed by ds_read_b64_tr_b16
+#pragma unroll
+      for (int i = 0; i < C::NKL; ++i) {
+        const int idx = tid + 256 * i;
+        st16(vl + (idx / C::CH) * C::VP + 16 * (idx % C::CH), vr[i >> 1][i & 1]);
+      }
+    }
   };
 
   float m[C::NR], lsum[C::NR];
@@ -155,132 +285,173 @@ __global__ void __launch_bounds__(kPWaves * kWave) prefill_kernel(PrefillKArgs a
     for (int dm = 0; dm < C::ND; ++dm) o[dm][rn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  const int vtok = lane / C::CH;  // V load mapping: key, 16-B chunk
-  const int vch = lane % C::CH;
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int k0 = t * kKT;
-    // ---- V tile -> LDS (coalesced loads; keys past n_keys clamped) ----
-    u32x4 vreg[C::NVL];
+  // A operand of O^T += V^T P^T for 16-bit pools, from row-major V in LDS:
+  // lane (dim 16 dm + col, group G) needs keys 32 ks + 4 G + {0..3} and
+  // 32 ks + 16 + 4 G + {0..3}.  ds_read_b64_tr_b16 gives lane i of a 16-lane
+  // group, element j, the (i & 3)-th 16-bit value at the address of lane
+  // 4 j + (i >> 2); so lane s of the group points at key 4 G + (s >> 2),
+  // dims 4 (s & 3) .. +3 of the 16-dim tile.
+  auto v_frag = [&](const char* vl, int ks, int dm) __attribute__((always_inline)) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    const int src = lane & 15;
+    const char* b = vl + (32 * ks + 4 * G + (src >> 2)) * C::VP + (16 * dm + 4 * (src & 3)) * 2;
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(b));
+    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(b + 16 * C::VP));
+    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+    return u32x4{l2.x, l2.y, h2.x, h2.y};
+  };
+  auto compute = [&](int t, bool masked) __attribute__((always_inline)) {
+    const char* kl = lds + (t & 1) * C::STAGE;
+    const char* vl = kl + C::KLDS;
+    const int k0 = t * C::KT;
+    // ---- S^T = K Q^T: sacc[km][rn][j] = S[key k0 + 16 km + 4 G + j][row] ----
+    f32x4 sacc[C::NKM][C::NR];
 #pragma unroll
-    for (int i = 0; i < C::NVL; ++i) {
-      const int key = min(k0 + i * C::TPL + vtok, n_keys - 1);
-      const char* base = vh + (size_t)block_of(key) * blk_stride;
-      vreg[i] = ld16(base + (size_t)(key & tmask) * slot_stride + 16 * vch);
-    }
-    // ---- K fragments (A operand): key = k0 + 16 km + col ----
-    u32x4 kf[2][C::NF];
+    for (int km = 0; km < C::NKM; ++km) {
 #pragma unroll
-    for (int km = 0; km < 2; ++km) {
-      const int key = min(k0 + 16 * km + col, n_keys - 1);
-      const char* r = kh + (size_t)block_of(key) * blk_stride +
-                      (size_t)(key & tmask) * slot_stride + 16 * G;
+      for (int rn = 0; rn < C::NR; ++rn) sacc[km][rn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int f = 0; f < C::NF; ++f) kf[km][f] = ld16(r + 64 * f);
-    }
-    __builtin_amdgcn_wave_barrier();
+      for (int f = 0; f < C::NF; ++f) {
+        const u32x4 kf = ld16(kl + (16 * km + col) * C::KPITCH + 64 * f + 16 * G);
 #pragma unroll
-    for (int i = 0; i < C::NVL; ++i) {
-      char* dst = v_lds + (i * C::TPL + vtok) * C::VPITCH + 16 * vch;
-      *reinterpret_cast<uint64_t*>(dst) = (uint64_t)vreg[i][0] | ((uint64_t)vreg[i][1] << 32);
-      *reinterpret_cast<uint64_t*>(dst + 8) = (uint64_t)vreg[i][2] | ((uint64_t)vreg[i][3] << 32);
-    }
-
-    // ---- S^T = K Q^T: acc[km][rn][j] = S[key k0 + 16 km + 4 G + j][row] ----
-    f32x4 sacc[2][C::NR];
-#pragma unroll
-    for (int km = 0; km < 2; ++km)
-#pragma unroll
-      for (int rn = 0; rn < C::NR; ++rn) {
-        sacc[km][rn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int f = 0; f < C::NF; ++f) mfma_frag<DT>(kf[km][f], qf[rn][f], sacc[km][rn]);
+        for (int rn = 0; rn < C::NR; ++rn) mfma_frag<DT>(kf, qf[rn][f], sacc[km][rn]);
       }
-
+    }
     // ---- causal mask + online softmax per row (rows along lane % 16) ----
-    float p[2][C::NR][4];
+    // Causal mask (wave-uniform branch): scores of keys past a row's
+    // position become -inf in place, so the shared softmax below gives them
+    // weight exactly 0 and a row's arithmetic does not depend on which rows
+    // share its wave or workgroup.
+    if (masked) {
+#pragma unroll
+      for (int km = 0; km < C::NKM; ++km)
+#pragma unroll
+        for (int rn = 0; rn < C::NR; ++rn)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (k0 + 16 * km + 4 * G + j > lim[rn]) sacc[km][rn][j] = -INFINITY;
+    }
+    // Online softmax with a lazily raised reference max m (log2 domain): m
+    // moves only when a tile's row max exceeds it by more than kTau, so
+    // weights stay <= 2^kTau and the O/l rescale is skipped whenever no row
+    // of the wave moved.  Scores enter the exponent through one fma.
+    float p[C::NKM][C::NR][4];
+    bool moved = false;
+    float alpha[C::NR];
 #pragma unroll
     for (int rn = 0; rn < C::NR; ++rn) {
-      const int lim = prior + tok_of[rn];  // last key this row may see
       float tmax = -INFINITY;
 #pragma unroll
-      for (int km = 0; km < 2; ++km)
+      for (int km = 0; km < C::NKM; ++km)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = k0 + 16 * km + 4 * G + j;
-          const float sv = key <= lim ? sacc[km][rn][j] * a.scale_log2 : -INFINITY;
-          p[km][rn][j] = sv;
-          tmax = fmaxf(tmax, sv);
-        }
-      tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-      const float mnew = fmaxf(m[rn], tmax);
-      const float alpha = fast_exp2(m[rn] - mnew);
-      m[rn] = mnew;
+        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sacc[km][rn][j]);
+      tmax = row_group_max(tmax) * a.scale_log2;  // scale > 0 (checked by the host)
+      alpha[rn] = 1.0f;
+      if (tmax > m[rn] + kTau) {  // always in tile 0: m starts at -inf, key 0 is visible
+        alpha[rn] = fast_exp2(m[rn] - tmax);
+        m[rn] = tmax;
+        moved = true;
+      }
+      const float nm = -m[rn];
       float ssum = 0.0f;
 #pragma unroll
-      for (int km = 0; km < 2; ++km)
+      for (int km = 0; km < C::NKM; ++km)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          p[km][rn][j] = fast_exp2(p[km][rn][j] - mnew);
+          p[km][rn][j] = fast_exp2(fmaf(sacc[km][rn][j], a.scale_log2, nm));
           ssum += p[km][rn][j];
         }
-      lsum[rn] = lsum[rn] * alpha + ssum;  // lane-partial over its 8 keys
-#pragma unroll
-      for (int dm = 0; dm < C::ND; ++dm) o[dm][rn] *= alpha;
+      lsum[rn] = fmaf(lsum[rn], alpha[rn], ssum);  // lane-partial over its keys
     }
-    __builtin_amdgcn_wave_barrier();
-
-    // ---- O^T += V^T P^T ----
-    if constexpr (DT == PKV_F32) {
-      // k-step (km, j): lane group G supplies key 16 km + 4 G + j.
-#pragma unroll
-      for (int dm = 0; dm < C::ND; ++dm)
-#pragma unroll
-        for (int km = 0; km < 2; ++km)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int kl = 16 * km + 4 * G + j;
-            const float va = *reinterpret_cast<const float*>(
-                v_lds + kl * C::VPITCH + (16 * dm + col) * 4);
-#pragma unroll
-            for (int rn = 0; rn < C::NR; ++rn)
-              o[dm][rn] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, p[km][rn][j], o[dm][rn], 0, 0, 0);
-          }
-    } else {
-      // one 16x16x32 step: lane group G supplies keys {4G..4G+3, 16+4G..16+4G+3}
-      u32x4 phi[C::NR], plo[C::NR];
+    if (__builtin_amdgcn_ballot_w64(moved)) {  // wave-uniform
 #pragma unroll
       for (int rn = 0; rn < C::NR; ++rn)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float x0 = p[w >> 1][rn][(w & 1) * 2];
-          const float x1 = p[w >> 1][rn][(w & 1) * 2 + 1];
-          const uint32_t h0 = to16<DT>(x0), h1 = to16<DT>(x1);
-          phi[rn][w] = h0 | (h1 << 16);
-          plo[rn][w] = to16<DT>(x0 - from16<DT>(h0)) | (to16<DT>(x1 - from16<DT>(h1)) << 16);
+        for (int dm = 0; dm < C::ND; ++dm) o[dm][rn] *= alpha[rn];
+    }
+    // ---- O^T += V^T P^T ----
+    if constexpr (DT == PKV_F32) {
+      // k-step (km, j): lane group G supplies key 16 km + 4 G + j
+#pragma unroll
+      for (int dm = 0; dm < C::ND; ++dm)
+#pragma unroll
+        for (int km = 0; km < C::NKM; ++km) {
+          const u32x4 va = ld16(vl + (16 * dm + col) * C::VTP + (16 * km + 4 * G) * 4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rn = 0; rn < C::NR; ++rn)
+              o[dm][rn] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(va[j]),
+                                                               p[km][rn][j], o[dm][rn], 0, 0, 0);
         }
+    } else {
+      // k-step ks (32 keys): lane group G supplies keys 32 ks + {4G..4G+3, 16+4G..16+4G+3}
 #pragma unroll
-      for (int dm = 0; dm < C::ND; ++dm) {
-        u32x4 va;
+      for (int ks = 0; ks < C::KT / 32; ++ks) {
+        u32x4 phi[C::NR], plo[C::NR];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int kla = (w >> 1) * 16 + 4 * G + (w & 1) * 2;
-          const uint16_t* p0 = reinterpret_cast<const uint16_t*>(
-              v_lds + kla * C::VPITCH + (16 * dm + col) * 2);
-          const uint16_t* p1 = reinterpret_cast<const uint16_t*>(
-              v_lds + (kla + 1) * C::VPITCH + (16 * dm + col) * 2);
-          va[w] = (uint32_t)*p0 | ((uint32_t)*p1 << 16);
-        }
+        for (int rn = 0; rn < C::NR; ++rn)
 #pragma unroll
-        for (int rn = 0; rn < C::NR; ++rn) {
-          mfma_frag<DT>(va, phi[rn], o[dm][rn]);
-          mfma_frag<DT>(va, plo[rn], o[dm][rn]);
+          for (int w = 0; w < 4; ++w) {
+            const float x0 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2];
+            const float x1 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2 + 1];
+            phi[rn][w] = cvt_pk16<DT>(x0, x1);
+            if constexpr (DT == PKV_BF16)
+              plo[rn][w] = cvt_pk16<DT>(x0 - bf16lo(phi[rn][w]), x1 - bf16hi(phi[rn][w]));
+          }
+#pragma unroll
+        for (int dm = 0; dm < C::ND; ++dm) {
+          const u32x4 va = v_frag(vl, ks, dm);
+#pragma unroll
+          for (int rn = 0; rn < C::NR; ++rn) {
+            mfma_frag<DT>(va, phi[rn], o[dm][rn]);
+            if constexpr (DT == PKV_BF16) mfma_frag<DT>(va, plo[rn], o[dm][rn]);
+          }
         }
       }
     }
-    __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- pipeline: tile t is computed from LDS stage t & 1 while the data
+  //      of tiles t + 1 .. t + D sit in registers or in flight and the block
+  //      ids of tile t + D + 1 resolve.  Loads return in issue order, so
+  //      each tile's block ids are issued before the previous tile's data:
+  //      waiting for them never waits for data still needed in flight. ----
+  // Loads and block ids past the last tile are clamped to key n_keys - 1
+  // (valid, unused) and stores past it fill an LDS stage nobody reads, so the
+  // memory operations run unconditionally: the in-order wait counts stay
+  // exact across the loop.  Iterations run in pairs (register sets and LDS
+  // stages alternate); a tile past the end computes nothing.
+  constexpr int NS = C::NSET, D = C::D;
+  ids(0, kb[0], vb[0]);
+  loads(0, kreg[0], vreg[0], kb[0], vb[0]);
+  if constexpr (D > 2) {
+    ids(1, kb[1], vb[1]);
+    loads(1, kreg[1 % NS], vreg[1 % NS], kb[1], vb[1]);
   }
+  store(0, kreg[0], vreg[0]);
+  ids(D - 1, kb[(D - 1) & 1], vb[(D - 1) & 1]);
+  ids(D, kb[D & 1], vb[D & 1]);
+  loads(D - 1, kreg[(D - 1) % NS], vreg[(D - 1) % NS], kb[(D - 1) & 1], vb[(D - 1) & 1]);
+  __syncthreads();
+
+  auto iter = [&](int t, auto parity) __attribute__((always_inline)) {
+    constexpr int P = decltype(parity)::value;  // t & 1
+    const int k0 = t * C::KT;
+    if (has_rows && k0 <= klim_hi)  // wave-uniform: some row sees a key of this tile
+      compute(t, k0 + C::KT - 1 > klim_lo);
+    store((P + 1) & 1, kreg[(P + 1) % NS], vreg[(P + 1) % NS]);
+    ids(t + D + 1, kb[(P + D + 1) & 1], vb[(P + D + 1) & 1]);
+    loads(t + D, kreg[(P + D) % NS], vreg[(P + D) % NS], kb[(P + D) & 1], vb[(P + D) & 1]);
+    __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    iter(t, std::integral_constant<int, 0>{});
+    iter(t + 1, std::integral_constant<int, 1>{});
+  }
+  if (bad_block && lane == 0) atomicOr(a.err, PKV_EBIT_BLOCK);
+  if (!has_rows) return;
 
   // ---- epilogue: lane holds O^T[dims 16 dm + 4 G + j][row 16 rn + col] ----
 #pragma unroll
@@ -288,8 +459,8 @@ __global__ void __launch_bounds__(kPWaves * kWave) prefill_kernel(PrefillKArgs a
     float l = lsum[rn];
     l += shfl_xor_f(l, 16);
     l += shfl_xor_f(l, 32);
-    const int r = row0 + 16 * rn + col;
-    if (r >= q_len * R) continue;
+    const int r = roww + 16 * rn + col;
+    if (r >= n_rows) continue;
     const float inv = 1.0f / l;
     const size_t base = ((size_t)(q0 + r / R) * H + g * R + r % R) * HD;
 #pragma unroll
@@ -310,11 +481,19 @@ __global__ void __launch_bounds__(kPWaves * kWave) prefill_kernel(PrefillKArgs a
 template <int DT, int HD, int R>
 hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
   using C = PCfg<DT, HD, R>;
-  k.row_tiles = (k.max_q_len * R + C::ROWS - 1) / C::ROWS;
-  long long items = (long long)k.n_seqs * k.kvh * k.row_tiles;
+  k.row_blocks = (k.max_q_len * R + C::ROWS - 1) / C::ROWS;
+  const long long n_sg = (long long)k.n_seqs * k.kvh;
+  const long long items = n_sg * k.row_blocks;
   if (items <= 0) return hipSuccess;
-  unsigned grid = (unsigned)((items + kPWaves - 1) / kPWaves);
-  prefill_kernel<DT, HD, R><<<grid, kPWaves * kWave, 0, s>>>(k);
+  if (items >= (1ll << 31)) return hipErrorInvalidValue;
+  long long grid = items;
+  k.per_xcd = 0;
+  if (n_sg >= kXcd) {
+    const long long per = ((n_sg + kXcd - 1) / kXcd) * k.row_blocks;
+    k.per_xcd = (int)per;
+    grid = per * kXcd;
+  }
+  prefill_kernel<DT, HD, R><<<(unsigned)grid, kPW * kWave, 0, s>>>(k);
   return hipGetLastError();
 }
 

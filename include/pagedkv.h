@@ -177,7 +177,9 @@ int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,
  *  q:   [total_q][n_head][head_dim] pool dtype;  out: [total_q][n_head*head_dim].
  *  cu_q_lens: [n_seqs+1] int32; context_lens: [n_seqs] int32;
  *  block_tables: [n_seqs][max_blocks_per_seq] int32.
- *  max_q_len, max_context_len: host upper bounds. */
+ *  max_q_len, max_context_len: host upper bounds.  scale > 0 and finite
+ *  (the reference's 1/sqrt(head_dim)); otherwise PKV_ERR_INVALID.
+ *  Supported: n_head/n_kv_head in {1,2,4,8}; f32 pools up to head_dim 128. */
 int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int out_dtype, const int32_t* cu_q_lens,
                           const int32_t* context_lens,
