@@ -54,6 +54,16 @@ constexpr int kWavesPerBlock = 4;
 #define PKV_DECODE_TILE 64
 #endif
 
+// Partition planning: the longest context partition in tokens, and the
+// number of (sequence, kv head, partition) waves below which partitions
+// are halved (down to 64 tokens) to spread a small batch over the CUs.
+#ifndef PKV_DECODE_PART_MAX
+#define PKV_DECODE_PART_MAX 512
+#endif
+#ifndef PKV_DECODE_MIN_ITEMS
+#define PKV_DECODE_MIN_ITEMS 2048
+#endif
+
 template <int DT, int HD, int R>
 struct DCfg {
   static constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
@@ -460,13 +470,30 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 // Merge of the partitions of (b, g) for sequences with more than one
 // partition: M = max_p m_p, L = sum_p l_p 2^(m_p - M),
 // O = sum_p O_p 2^(m_p - M) / L (all in the exp2 domain of the main kernel).
-// One wave per query head (b, g, h): lane d covers HD / 64 consecutive
-// dimensions; the per-partition (m, l) pairs are wave-uniform.  Context
-// clamping is identical to the main kernel.
+// One wave per query head (b, g, h).  The partitions are read in parallel:
+// (m, l) with one partition per lane, the partial rows O_p as 16-byte chunks
+// with HD / 4 lanes per row and 64 / (HD / 4) rows per load instruction,
+// kMergeUnroll instructions in flight per lane; the row groups are summed
+// with lane shuffles at the end.  Context clamping is identical to the main
+// kernel.
+constexpr int kMergeUnroll = 4;
+
+__device__ __forceinline__ float wave_max_f(float x) {
+#pragma unroll
+  for (int mk = 1; mk < kWave; mk <<= 1) x = fmaxf(x, shfl_xor_f(x, mk));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+#pragma unroll
+  for (int mk = 1; mk < kWave; mk <<= 1) x += shfl_xor_f(x, mk);
+  return x;
+}
+
 template <int HD>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_merge_kernel(DecodeKArgs a, int R, int dt) {
-  constexpr int DPL = HD / kWave;  // dims per lane: 1, 2 or 4
+  constexpr int LPR = HD / 4;      // lanes per partial row (16 B each)
+  constexpr int PPI = kWave / LPR; // partial rows per load instruction
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const long long qh = (long long)blockIdx.x * kWavesPerBlock + wave;  // (b, g, h)
@@ -479,32 +506,65 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int ctx = clamp_ctx(a, a.context_lens[b], BS);
   const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
   if (n_parts <= 1) return;
-  const float* mlb = a.part_ml + (size_t)pair * a.max_parts * R * 2 + 2 * h;
-  const float* pob = a.part_o + ((size_t)pair * a.max_parts * R + h) * HD + lane * DPL;
+  const size_t pstride_ml = (size_t)R * 2;   // floats between partitions
+  const size_t pstride_o = (size_t)R * HD;
+  const float* mlb = a.part_ml + (size_t)pair * a.max_parts * pstride_ml + 2 * h;
+  const int q = lane / LPR;  // row group
+  const int c = lane % LPR;  // 16-byte chunk of the row
+  const float* pob = a.part_o + ((size_t)pair * a.max_parts * R + h) * HD + 4 * c;
+
   float M = -INFINITY;
-  for (int pp = 0; pp < n_parts; ++pp) M = fmaxf(M, mlb[(size_t)pp * R * 2]);
+  for (int p0 = 0; p0 < n_parts; p0 += kWave)
+    if (p0 + lane < n_parts) M = fmaxf(M, mlb[(size_t)(p0 + lane) * pstride_ml]);
+  M = wave_max_f(M);
   float L = 0.0f;
-  float acc[DPL];
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
-  for (int pp = 0; pp < n_parts; ++pp) {
-    const float w = fast_exp2(mlb[(size_t)pp * R * 2] - M);
-    L += w * mlb[(size_t)pp * R * 2 + 1];
-    const float* op = pob + (size_t)pp * R * HD;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] += w * op[i];
+  for (int p0 = 0; p0 < n_parts; p0 += kWave) {
+    const int pp = p0 + lane;
+    if (pp < n_parts) {
+      const float* e = mlb + (size_t)pp * pstride_ml;
+      L += fast_exp2(e[0] - M) * e[1];
+    }
   }
+  L = wave_sum_f(L);
+
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int p0 = 0; p0 < n_parts; p0 += PPI * kMergeUnroll) {
+    f32x4 ov[kMergeUnroll];
+    float mv[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int pp = p0 + u * PPI + q;
+      const bool ok = pp < n_parts;
+      ov[u] = ok ? *reinterpret_cast<const f32x4*>(pob + (size_t)pp * pstride_o)
+                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      mv[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const float w = fast_exp2(mv[u] - M);  // 0 for absent rows
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, ov[u][i], acc[i]);
+    }
+  }
+#pragma unroll
+  for (int mk = LPR; mk < kWave; mk <<= 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += shfl_xor_f(acc[i], mk);
+  if (lane >= LPR) return;
+
   const float inv = 1.0f / L;
-  const size_t eo = ((size_t)b * a.kvh * R + g * R + h) * HD + lane * DPL;
+  const size_t eo = ((size_t)b * a.kvh * R + g * R + h) * HD + 4 * c;
   if (a.out_f32) {
-    float* o = reinterpret_cast<float*>(a.out) + eo;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) o[i] = acc[i] * inv;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) =
+        f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
   } else {
-    uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + eo;
+    uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i)
-      o[i] = (uint16_t)(dt == PKV_BF16 ? f32_to_bf16_bits(acc[i] * inv) : f32_to_f16_bits(acc[i] * inv));
+    for (int i = 0; i < 4; ++i)
+      w[i] = dt == PKV_BF16 ? f32_to_bf16_bits(acc[i] * inv) : f32_to_f16_bits(acc[i] * inv);
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + eo) =
+        u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
   }
 }
 
@@ -561,8 +621,8 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   // the K/V stream (measured: 512 beats 256 by ~7% on the Llama-3-8B
   // decode); shorter partitions are used when the batch is too small to
   // give every CU several waves.
-  int pt = 512;
-  while (pt > 64 && pairs * ((mc + pt - 1) / pt) < 4096) pt >>= 1;
+  int pt = PKV_DECODE_PART_MAX;
+  while (pt > 64 && pairs * ((mc + pt - 1) / pt) < PKV_DECODE_MIN_ITEMS) pt >>= 1;
   // The per-partition table slice must fit one wave (<= 64 block ids).
   while (pt > 64 && (pt >> ilog2i(p->block_size)) + 1 > 64) pt >>= 1;
   *part_tokens = pt;

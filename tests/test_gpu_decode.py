@@ -142,6 +142,20 @@ def test_decode_matches_oracle(gpu, dt, hd, R):
     c.close()
 
 
+@pytest.mark.parametrize("dt,hd,R", [(wl.BF16, 64, 4), (wl.F16, 64, 8), (wl.BF16, 128, 4),
+                                     (wl.BF16, 128, 8), (wl.F16, 256, 2), (wl.F32, 128, 4)])
+def test_many_partitions_merge(gpu, dt, hd, R):
+    # a small batch with long contexts: 64-token partitions, up to ~150 per
+    # sequence, so the merge covers several (m, l) lane groups and unrolled
+    # partial-row loads, plus a sequence with exactly one partition
+    ctx = [9500, 4096, 63, 4097, 1500]
+    c = Case(gpu, dt, 2 * R, 2, hd, 16, ctx, seed=hd + R, fused=True)
+    got = c.run(out_dtype=torch.float32 if dt == wl.F32 else TD[dt])
+    ref, _, _ = c.reference()
+    _close(got, ref, f"many partitions dt={dt} hd={hd} R={R}")
+    c.close()
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64, 256])
 def test_decode_block_sizes(gpu, bs):
     c = Case(gpu, wl.BF16, 8, 2, 128, bs, [0, bs - 2, bs - 1, bs, 3 * bs + 5, 1000], seed=bs)
