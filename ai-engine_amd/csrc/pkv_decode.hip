@@ -144,23 +144,41 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
   return x;
 }
 
+// Context lengths of up to kCtxCache sequences are staged in LDS once per
+// workgroup; the work-list search and every item's length read them there.
+constexpr int kCtxCache = 2048;
+
+struct CtxLens {
+  const int32_t* g;  // global context_lens
+  const int* lds;    // LDS copy of the first n entries
+  int n;
+  __device__ __forceinline__ int operator[](int b) const { return b < n ? lds[b] : g[b]; }
+};
+
+// Buckets of the last partitions' lengths, (j * PT / NB, (j + 1) * PT / NB].
+constexpr int kLptBuckets = 16;
+
 // Work list of one launch, in dispatch order: first every full partition
 // (p < n_parts(b) - 1, PT tokens each) in sequence order, then the last,
 // shorter partition of every sequence (p = n_parts(b) - 1; p = 0 with an
-// empty context).  Hardware dispatch in grid order then approximates
-// longest-first scheduling, and the grid's surplus waves (the host sizes it
-// for the longest context) all sit past the end of the list.  Each wave
-// finds its (b, p) from the context lengths: 64 sequences per step, wave
-// prefix sum of full-partition counts, ballot for the owning lane.
-__device__ bool locate_pair(const DecodeKArgs& a, long long kpair, int lane, int BS,
-                            int& b, int& p) {
+// empty context) from the longest length bucket down, sequence order within
+// a bucket.  Hardware dispatch in grid order then approximates
+// longest-processing-time-first scheduling, and the grid's surplus waves
+// (the host sizes it for the longest context) sit past the end of the list.
+// Each wave finds its (b, p) from the context lengths, 64 sequences per
+// step: a wave prefix sum of full-partition counts, per-bucket ballot
+// counts of the last partitions, and the rank of the wanted sequence within
+// its bucket.
+__device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long kpair, int lane,
+                            int BS, int& b, int& p) {
+  const int PT = a.part_tokens;
   long long base = 0;
   for (int b0 = 0; b0 < a.batch; b0 += 64) {
     const int bb = b0 + lane;
     int f = 0;
     if (bb < a.batch) {
-      const int ctx = clamp_ctx(a, a.context_lens[bb], BS);
-      const int np = (ctx + a.part_tokens - 1) / a.part_tokens;
+      const int ctx = clamp_ctx(a, cl[bb], BS);
+      const int np = (ctx + PT - 1) / PT;
       f = np > 1 ? np - 1 : 0;
     }
     const int incl = wave_incl_scan(f, lane);
@@ -174,13 +192,51 @@ __device__ bool locate_pair(const DecodeKArgs& a, long long kpair, int lane, int
     }
     base += readlane_i(incl, 63);
   }
-  const long long k2 = kpair - base;
+  long long k2 = kpair - base;
   if (k2 >= a.batch) return false;
-  b = (int)k2;
-  const int ctx = clamp_ctx(a, a.context_lens[b], BS);
-  const int np = (ctx + a.part_tokens - 1) / a.part_tokens;
-  p = np > 0 ? np - 1 : 0;
-  return true;
+
+  // Last partition of sequence bb: its bucket and partition index.
+  auto last_of = [&](int bb, int& np) -> int {
+    const int ctx = clamp_ctx(a, cl[bb], BS);
+    np = (ctx + PT - 1) / PT;
+    const int len = ctx - (np > 0 ? np - 1 : 0) * PT;  // 0 (empty context) .. PT
+    return len <= 0 ? 0 : (len - 1) * kLptBuckets / PT;
+  };
+  int cnt[kLptBuckets];
+#pragma unroll
+  for (int j = 0; j < kLptBuckets; ++j) cnt[j] = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    int np = 0;
+    const int bk = b0 + lane < a.batch ? last_of(b0 + lane, np) : -1;
+#pragma unroll
+    for (int j = 0; j < kLptBuckets; ++j) cnt[j] += __popcll(__ballot(bk == j));
+  }
+  int want = -1;
+#pragma unroll
+  for (int j = kLptBuckets - 1; j >= 0; --j) {
+    if (want < 0) {
+      if (k2 < cnt[j]) want = j;
+      else k2 -= cnt[j];
+    }
+  }
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    int np = 0;
+    const int bk = b0 + lane < a.batch ? last_of(b0 + lane, np) : -1;
+    const unsigned long long mask = __ballot(bk == want);
+    const int c = __popcll(mask);
+    if (k2 < c) {
+      const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+      const unsigned long long hit = __ballot(bk == want && below == (int)k2);
+      const int hl = __ffsll((long long)hit) - 1;
+      b = b0 + hl;
+      const int npb = readlane_i(np, hl);
+      p = npb > 0 ? npb - 1 : 0;
+      return true;
+    }
+    k2 -= c;
+  }
+  return false;  // not reached: the bucket counts cover every sequence
 }
 
 template <int DT, int HD, int R>
@@ -188,6 +244,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
   using C = DCfg<DT, HD, R>;
   __shared__ float p_lds_all[kWavesPerBlock][C::TILE * C::RP];
+  __shared__ int ctx_lds[kCtxCache];
 
   // The wave index is uniform within a wave; readfirstlane tells the
   // compiler so, which keeps every per-wave quantity in SGPRs.
@@ -195,14 +252,19 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int lane = threadIdx.x & 63;
   float* p_lds = p_lds_all[wave];
 
+  const int ncache = min(a.batch, kCtxCache);
+  for (int i = threadIdx.x; i < ncache; i += kWavesPerBlock * kWave) ctx_lds[i] = a.context_lens[i];
+  __syncthreads();
+  const CtxLens cl{a.context_lens, ctx_lds, ncache};
+
   const int H = a.kvh * R;
   const int BS = 1 << a.bs_log2;
   const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
   const int g = (int)(item % a.kvh);
   int b = 0, p = 0;
-  if (!locate_pair(a, item / a.kvh, lane, BS, b, p)) return;
+  if (!locate_pair(a, cl, item / a.kvh, lane, BS, b, p)) return;
 
-  const int ctx_raw = a.context_lens[b];
+  const int ctx_raw = cl[b];
   const int ctx = clamp_ctx(a, ctx_raw, BS);
   const bool clamped = ctx != ctx_raw;
   if (clamped && lane == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
@@ -316,10 +378,10 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   for (int st = 0; st < C::NST; ++st) {
     const char* r = k_row(t_begin, st);
 #pragma unroll
-    for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(r + 64 * f);
+    for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16_stream(r + 64 * f);
   }
 #pragma unroll
-  for (int i = 0; i < C::NV; ++i) vf[i] = ld16(v_chunk(t_begin, i));
+  for (int i = 0; i < C::NV; ++i) vf[i] = ld16_stream(v_chunk(t_begin, i));
 
   // One tile, software-pipelined at distance one tile: every K fragment is
   // reloaded with the next tile's fragment right after its MFMA has read
@@ -339,7 +401,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       if constexpr (PF) {
         const char* r = k_row(next, st);
 #pragma unroll
-        for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(r + 64 * f);
+        for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16_stream(r + 64 * f);
       }
     }
 
@@ -403,7 +465,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       }
       float x[C::EPL];
       widen16<DT, C::EPL>(vf[i], x);
-      if constexpr (PF) vf[i] = ld16(v_chunk(next, i));
+      if constexpr (PF) vf[i] = ld16_stream(v_chunk(next, i));
 #pragma unroll
       for (int h = 0; h < R; ++h)
 #pragma unroll
@@ -416,14 +478,16 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   tile_body(t_begin + (ntiles - 1) * C::TILE, std::false_type{});
 
   // ---- partition epilogue ----
+  // P.V accumulators are summed over the token groups (lanes with equal
+  // chunk c) on the VALU; every group then holds the full row and the
+  // groups share the stores: group tg writes heads tg, tg + NG, ...
+  constexpr int NG = 64 / C::CH;
 #pragma unroll
   for (int j = 0; j < 4; ++j) lsum[j] = row_sum16(lsum[j]);
 #pragma unroll
   for (int h = 0; h < R; ++h)
 #pragma unroll
-    for (int e = 0; e < C::EPL; ++e)
-#pragma unroll
-      for (int mk = C::CH; mk < 64; mk <<= 1) o[h][e] += shfl_xor_f(o[h][e], mk);
+    for (int e = 0; e < C::EPL; ++e) o[h][e] = group_sum<C::CH>(o[h][e]);
 
   float mh[R], lh[R];
 #pragma unroll
@@ -433,16 +497,15 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   }
 
   if (n_parts == 1) {
-    if (lane < C::CH) {
 #pragma unroll
-      for (int h = 0; h < R; ++h) {
-        float inv = 1.0f / lh[h];
-        float x[C::EPL];
+    for (int h = 0; h < R; ++h) {
+      if (h % NG != tg) continue;
+      float inv = 1.0f / lh[h];
+      float x[C::EPL];
 #pragma unroll
-        for (int e = 0; e < C::EPL; ++e) x[e] = o[h][e] * inv;
-        store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
-                          a.out_f32, DT, x);
-      }
+      for (int e = 0; e < C::EPL; ++e) x[e] = o[h][e] * inv;
+      store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
+                        a.out_f32, DT, x);
     }
     return;
   }
@@ -450,13 +513,13 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const size_t pair = (size_t)b * a.kvh + g;
   float* ml = a.part_ml + (pair * a.max_parts + p) * R * 2;
   float* po = a.part_o + (pair * a.max_parts + p) * R * HD;
-  if (lane < C::CH) {
 #pragma unroll
-    for (int h = 0; h < R; ++h)
+  for (int h = 0; h < R; ++h) {
+    if (h % NG != tg) continue;
 #pragma unroll
-      for (int e = 0; e < C::EPL; e += 4)
-        *reinterpret_cast<f32x4*>(po + h * HD + c * C::EPL + e) =
-            f32x4{o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]};
+    for (int e = 0; e < C::EPL; e += 4)
+      *reinterpret_cast<f32x4*>(po + h * HD + c * C::EPL + e) =
+          f32x4{o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]};
   }
   if (lane == 0) {
 #pragma unroll

@@ -84,6 +84,31 @@ __device__ __forceinline__ float row_sum16(float x) {
   return x;
 }
 
+// Sums across rows of 16 lanes with the gfx950 permlane swaps (VALU, no
+// LDS round trip): given the same register twice, the two results hold each
+// lane's own value and its partner's (lane ^ 16, resp. lane ^ 32).
+__device__ __forceinline__ float swap16_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of x over the lanes l' with l' % CH == l % CH (CH a power of two in
+// [4, 64]); every lane receives the sum.
+template <int CH>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (CH <= 4) x += dpp_f<0x124>(x);  // row_ror:4
+  if constexpr (CH <= 8) x += dpp_f<0x128>(x);  // row_ror:8
+  if constexpr (CH <= 16) x = swap16_sum(x);
+  if constexpr (CH <= 32) x = swap32_sum(x);
+  return x;
+}
+
 __device__ __forceinline__ float readlane_f(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
@@ -127,6 +152,13 @@ __device__ __forceinline__ void mfma_frag(const u32x4& a, const u32x4& b,
 
 __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
+}
+// Non-temporal 16-byte load for data read once per launch (the K/V
+// stream): the L2 evicts such lines first, which keeps the small partial
+// results a kernel writes resident instead of sending them to HBM in the
+// middle of the read stream.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
