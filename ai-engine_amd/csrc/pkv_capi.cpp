@@ -245,10 +245,6 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   }
   p->base = static_cast<char*>(base);
   p->err = static_cast<uint32_t*>(err);
-  if (hipDeviceGetAttribute(&p->num_cus, hipDeviceAttributeMultiprocessorCount, device) !=
-          hipSuccess ||
-      p->num_cus <= 0)
-    p->num_cus = 256;
   *out = p;
   return PKV_OK;
 }

@@ -58,7 +58,7 @@ constexpr int kWavesPerBlock = 4;
 // number of (sequence, kv head, partition) waves below which partitions
 // are halved (down to 64 tokens) to spread a small batch over the CUs.
 #ifndef PKV_DECODE_PART_MAX
-#define PKV_DECODE_PART_MAX 512
+#define PKV_DECODE_PART_MAX 1024
 #endif
 #ifndef PKV_DECODE_MIN_ITEMS
 #define PKV_DECODE_MIN_ITEMS 2048
@@ -70,7 +70,9 @@ struct DCfg {
   static constexpr int RB = HD * E;                // row bytes
   static constexpr int NF = RB / 64;               // QK fragments per lane per row
   static constexpr int NST0 = 16 / NF;
-  static constexpr int NSTMAX = PKV_DECODE_TILE / 16;
+  // GQA 8 holds twice the P.V accumulators; a 32-token tile keeps it at
+  // two waves per SIMD.
+  static constexpr int NSTMAX = (R >= 8 ? 32 : PKV_DECODE_TILE) / 16;
   static constexpr int NST = NST0 < 1 ? 1 : (NST0 > NSTMAX ? NSTMAX : NST0);  // sub-tiles
   static constexpr int TILE = 16 * NST;            // tokens per tile
   static constexpr int CH = RB / 16;               // 16-byte chunks per row
@@ -679,15 +681,20 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   (void)n_head;
   long long pairs = (long long)batch * p->n_kv_head;
   int mc = max_context_len > 0 ? max_context_len : 1;
-  // Partition length: 512 tokens (256 KB of K+V per bf16 head of 128) keeps
-  // the partial (m, l, O) traffic of the split-context merge near 1.5% of
-  // the K/V stream (measured: 512 beats 256 by ~7% on the Llama-3-8B
-  // decode); shorter partitions are used when the batch is too small to
-  // give every CU several waves.
+  // Partition length: 1024 tokens (512 KB of K+V per bf16 head of 128).
+  // The split-context partials (m, l, O) are written in the middle of the
+  // K/V read stream, and those writes cost far more than their bytes
+  // (measured on the Llama-3-8B decode: 0-10 % of the kernel depending on
+  // where the workspace lands in HBM with 512-token partitions, a third of
+  // that with 1024); the longest-first work list keeps the longer items
+  // from lengthening the tail.  Shorter partitions are used when the batch
+  // is too small to give every CU several waves.
   int pt = PKV_DECODE_PART_MAX;
   while (pt > 64 && pairs * ((mc + pt - 1) / pt) < PKV_DECODE_MIN_ITEMS) pt >>= 1;
   // The per-partition table slice must fit one wave (<= 64 block ids).
-  while (pt > 64 && (pt >> ilog2i(p->block_size)) + 1 > 64) pt >>= 1;
+  // Partitions start at multiples of pt, so with block_size <= pt they are
+  // block-aligned and span pt / block_size blocks (one block otherwise).
+  while (pt > 64 && (pt >> ilog2i(p->block_size)) > 64) pt >>= 1;
   *part_tokens = pt;
   *max_parts = (mc + pt - 1) / pt;
 }

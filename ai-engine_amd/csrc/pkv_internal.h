@@ -22,7 +22,6 @@ struct pkv_pool {
   int head_dim = 0;
   int dtype = 0;
   int device = 0;
-  int num_cus = 0;         // compute units of `device` (persistent grids)
   size_t elem_bytes = 0;
   size_t row_bytes = 0;    // one (slot, kv head) row: head_dim * elem_bytes
   size_t block_bytes = 0;  // one block of one layer's K (or V)
