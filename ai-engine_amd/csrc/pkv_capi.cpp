@@ -104,6 +104,11 @@ int ensure_workspace(pkv_pool* p, size_t total, size_t counter_bytes) {
 }
 
 // ---- compaction planning ------------------------------------------------
+// Bytes of the largest plan for a pool of n blocks: at most n moves (2 ints
+// each), at most n / 2 cycles (a cycle has >= 2 moves) adding 2 ops (4 ints)
+// each, and one start per chain or cycle plus the end marker.
+size_t plan_capacity_bytes(size_t n) { return (5 * n + 2) * sizeof(int32_t); }
+
 // Moves m = (s -> d).  A move whose destination is still some other move's
 // source must wait until that block has been read: the chain is built from
 // a move whose dst is free, then repeatedly the move that fills the block
@@ -245,6 +250,23 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   }
   p->base = static_cast<char*>(base);
   p->err = static_cast<uint32_t*>(err);
+  // Compaction plan buffers (device + pinned host staging), sized once for
+  // the largest plan so that pkv_compact never allocates.
+  p->plan_bytes = plan_capacity_bytes(num_blocks);
+  void* dplan = nullptr;
+  void* hplan = nullptr;
+  e = hipMalloc(&dplan, p->plan_bytes);
+  if (e == hipSuccess) e = hipHostMalloc(&hplan, p->plan_bytes, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    if (dplan) (void)hipFree(dplan);
+    (void)hipFree(base);
+    (void)hipFree(err);
+    delete p;
+    return fail(nullptr, PKV_ERR_OOM, "compaction plan buffers (%zu bytes): %s",
+                plan_capacity_bytes(num_blocks), hipGetErrorString(e));
+  }
+  p->plan = static_cast<char*>(dplan);
+  p->plan_host = static_cast<char*>(hplan);
   *out = p;
   return PKV_OK;
 }
@@ -256,6 +278,8 @@ int pkv_pool_destroy(pkv_pool* p) {
   if (p->base) (void)hipFree(p->base);
   if (p->err) (void)hipFree(p->err);
   if (p->ws) (void)hipFree(p->ws);
+  if (p->plan) (void)hipFree(p->plan);
+  if (p->plan_host) (void)hipHostFree(p->plan_host);
   for (auto& ev : p->prof_events) {
     (void)hipEventDestroy(ev.first);
     (void)hipEventDestroy(ev.second);
@@ -356,13 +380,20 @@ int pkv_gather_seq(pkv_pool* p, int layer, const int32_t* block_table, int len,
   return PKV_OK;
 }
 
+static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee);
+
 int pkv_copy_blocks(pkv_pool* p, const int32_t* src, const int32_t* dst, int n, void* stream) {
   CHECK_POOL(p);
   if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
   if (n == 0) return PKV_OK;
   if (!src || !dst) return fail(p, PKV_ERR_INVALID, "src and dst must be non-NULL");
   DeviceGuard dg(p->device);
-  hipError_t e = pkv::launch_copy_blocks(p, src, dst, n, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
+  hipError_t e = eb ? hipEventRecord(eb, s) : hipSuccess;
+  if (e == hipSuccess) e = pkv::launch_copy_blocks(p, src, dst, n, s);
+  if (e == hipSuccess && ee) e = hipEventRecord(ee, s);
   if (e != hipSuccess) return hip_fail(p, e, "copy_blocks launch");
   return PKV_OK;
 }
@@ -378,19 +409,25 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
   if (n_chains <= 0) return PKV_OK;
   DeviceGuard dg(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Plan buffers: uploaded synchronously w.r.t. the host copy, freed after
-  // the launch completes (stream sync) so the call is self-contained.
+  // The plan goes to a device buffer the pool keeps between calls (grown
+  // when a larger plan comes); the call returns once the moves are done, so
+  // the host plan can go out of scope.
   size_t ob = ops.size() * sizeof(int32_t), sb = starts.size() * sizeof(int32_t);
-  void* dplan = nullptr;
-  hipError_t e = hipMalloc(&dplan, ob + sb);
-  if (e != hipSuccess) return fail(p, PKV_ERR_OOM, "compact plan hipMalloc: %s", hipGetErrorString(e));
-  int32_t* d_ops = static_cast<int32_t*>(dplan);
+  // The plan buffers were sized at pool creation for the largest plan (see
+  // plan_capacity_bytes); the call ends with a stream sync, so they are free.
+  if (ob + sb > p->plan_bytes)
+    return fail(p, PKV_ERR_INVALID, "compact: plan of %zu bytes exceeds its buffer", ob + sb);
+  std::memcpy(p->plan_host, ops.data(), ob);
+  std::memcpy(p->plan_host + ob, starts.data(), sb);
+  int32_t* d_ops = reinterpret_cast<int32_t*>(p->plan);
   int32_t* d_starts = d_ops + ops.size();
-  e = hipMemcpyAsync(d_ops, ops.data(), ob, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(d_starts, starts.data(), sb, hipMemcpyHostToDevice, s);
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
+  hipError_t e = hipMemcpyAsync(p->plan, p->plan_host, ob + sb, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && eb) e = hipEventRecord(eb, s);
   if (e == hipSuccess) e = pkv::launch_compact(p, d_ops, d_starts, n_chains, s);
+  if (e == hipSuccess && ee) e = hipEventRecord(ee, s);
   hipError_t e2 = hipStreamSynchronize(s);
-  (void)hipFree(dplan);
   if (e != hipSuccess) return hip_fail(p, e, "compact");
   if (e2 != hipSuccess) return hip_fail(p, e2, "compact sync");
   return PKV_OK;

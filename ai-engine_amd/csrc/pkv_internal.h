@@ -33,6 +33,11 @@ struct pkv_pool {
   char* ws = nullptr;
   size_t ws_bytes = 0;
   size_t ws_counter_bytes = 0;
+  // compaction plan (chains of block moves), kept between calls: device
+  // buffer and its pinned host staging copy
+  char* plan = nullptr;
+  char* plan_host = nullptr;
+  size_t plan_bytes = 0;
   // main-kernel timing events (pkv_pool_profile)
   bool prof_on = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;

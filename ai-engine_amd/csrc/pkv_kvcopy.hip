@@ -89,12 +89,12 @@ __global__ void __launch_bounds__(kCopyThreads)
 #pragma unroll
   for (int j = 0; j < kVecPerThread; ++j) {
     int v = v0 + j * kCopyThreads;
-    if (v < block_vec) r[j] = from[v];
+    if (v < block_vec) r[j] = __builtin_nontemporal_load(from + v);
   }
 #pragma unroll
   for (int j = 0; j < kVecPerThread; ++j) {
     int v = v0 + j * kCopyThreads;
-    if (v < block_vec) to[v] = r[j];
+    if (v < block_vec) __builtin_nontemporal_store(r[j], to + v);
   }
 }
 
@@ -120,14 +120,14 @@ __global__ void __launch_bounds__(kCopyThreads)
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) {
       int v = v0 + j * kCopyThreads;
-      if (v < block_vec) r[j] = s >= 0 ? pool[(size_t)s * block_vec + v] : held[j];
+      if (v < block_vec) r[j] = s >= 0 ? __builtin_nontemporal_load(pool + (size_t)s * block_vec + v) : held[j];
     }
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) {
       int v = v0 + j * kCopyThreads;
       if (v < block_vec) {
         if (d >= 0)
-          pool[(size_t)d * block_vec + v] = r[j];
+          __builtin_nontemporal_store(r[j], pool + (size_t)d * block_vec + v);
         else
           held[j] = r[j];
       }

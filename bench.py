@@ -44,6 +44,16 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def timed_passes(fn, args):
+    """Runs fn() at least args.cpu_layers times and for at least
+    args.cpu_seconds; returns (seconds per pass, passes, last result)."""
+    n, res, t0 = 0, None, time.time()
+    while n < max(1, args.cpu_layers) or (time.time() - t0 < args.cpu_seconds and n < 100000):
+        res = fn()
+        n += 1
+    return (time.time() - t0) / n, n, res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -52,7 +62,9 @@ def main() -> int:
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg2", "cfg5"])
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
-                    help="layer passes of the CPU baseline sample (0 = skip)")
+                    help="minimum layer passes of the CPU baseline sample (0 = skip it)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="the CPU baseline repeats its sample for at least this long")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--replicas", type=int, default=0,
                     help="pool replicas rotated across steps so that every step reads its K/V "
@@ -247,7 +259,8 @@ def main() -> int:
 def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     """Times the oracle's CPU restatement of the reference decode math
     (append + attention per layer, OpenMP over (sequence, kv head)) on layer
-    0's data copied to host, `cpu_layers` passes, scaled to a full step."""
+    0's data copied to host, repeated for a bounded sample (timed_passes),
+    scaled to a full step."""
     import numpy as np
     import oracle
     import pagedkv
@@ -272,12 +285,9 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     log(f"[bench] cpu baseline: host copy {time.time() - t_copy:.1f}s, {threads} threads")
     scale = 1.0 / math.sqrt(shape.head_dim)
     oracle.lib()
-    t = time.time()
-    res = None
-    for _ in range(args.cpu_layers):
-        res = oracle.decode_inplace(kp, vp, shape.dtype, shape.block_size, tables, cl, qh, knh, vnh,
-                                    scale, n_threads=threads)
-    dt = (time.time() - t) / args.cpu_layers
+    dt, passes, res = timed_passes(
+        lambda: oracle.decode_inplace(kp, vp, shape.dtype, shape.block_size, tables, cl, qh, knh,
+                                      vnh, scale, n_threads=threads), args)
     step_s = dt * shape.n_layers
     # sanity: the CPU result agrees with the GPU's layer-0 output
     gpu0 = out[0].float().cpu().numpy()
@@ -287,7 +297,7 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     return {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads,
             "kind": "port",
             "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
-                       f"{args.cpu_layers} passes of {dt:.2f} s, scaled x{shape.n_layers} layers"),
+                       f"{passes} passes of {dt * 1e3:.1f} ms, scaled x{shape.n_layers} layers"),
             "agrees_with_gpu": agree}
 
 
@@ -433,13 +443,13 @@ def mix(args, dev) -> int:
         hq, hk, hv = host(qp[0]), host(kc[0]), host(vc[0])
         dq, dk, dv = host(qd[0]), host(kd[0]), host(vd[0])
         oracle.lib()
-        tc = time.time()
-        for _ in range(args.cpu_layers):
-            rp = oracle.prefill_inplace(kp, vp, wl.F16, bs, tables[:NP], m.cu_q_lens, pctx_np, hq, hk,
-                                        hv, sc, n_threads=threads)
-            rd = oracle.decode_inplace(kp, vp, wl.F16, bs, tables[NP:], dctx_np, dq, dk, dv, sc,
-                                       n_threads=threads)
-        dt = (time.time() - tc) / args.cpu_layers
+
+        def one_layer():
+            return (oracle.prefill_inplace(kp, vp, wl.F16, bs, tables[:NP], m.cu_q_lens, pctx_np,
+                                           hq, hk, hv, sc, n_threads=threads),
+                    oracle.decode_inplace(kp, vp, wl.F16, bs, tables[NP:], dctx_np, dq, dk, dv,
+                                          sc, n_threads=threads))
+        dt, passes, (rp, rd) = timed_passes(one_layer, args)
         gp, gd = outp[0].float().cpu().numpy(), outd[0].float().cpu().numpy()
         agree = bool(np.all(np.abs(gp - rp) <= 1e-3 + 2e-2 * np.abs(rp))
                      and np.all(np.abs(gd - rd) <= 1e-3 + 2e-2 * np.abs(rd)))
@@ -447,7 +457,7 @@ def mix(args, dev) -> int:
         cpu = {"value": round((T + ND) / (dt * L), 2), "unit": "tok/s", "cores": threads,
                "kind": "port",
                "sample": (f"layer 0 of the same mix (chunk store + causal prefill of {NP}x{C}, "
-                          f"append + decode of {ND}), {args.cpu_layers} passes of {dt:.2f} s, "
+                          f"append + decode of {ND}), {passes} passes of {dt * 1e3:.1f} ms, "
                           f"scaled x{L} layers"),
                "agrees_with_gpu": agree}
 
@@ -522,15 +532,19 @@ def churn(args, dev) -> int:
     d_t = torch.tensor(dst, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    cache.copy_blocks(s_t, d_t)  # warm-up (idempotent: same src -> same dst)
+    for _ in range(max(1, args.warmup)):
+        cache.copy_blocks(s_t, d_t)  # idempotent: same src -> same dst
     torch.cuda.synchronize()
-    e0.record()
     reps = max(1, args.steps)
+    cache.profile(True)
+    e0.record()
     for _ in range(reps):
         cache.copy_blocks(s_t, d_t)
     e1.record()
     torch.cuda.synchronize()
     cow_ms = e0.elapsed_time(e1) / reps
+    cow_kms, cow_n = cache.profile_read()
+    cow_kms /= max(1, cow_n)
     cow_bytes = 2 * 512 * cache.block_bytes * 2 * L
     cache.check()
     # eviction of a random 25% of sequences
@@ -550,24 +564,81 @@ def churn(args, dev) -> int:
     torch.cuda.synchronize()
     comp_wall_ms = (time.time() - t0) * 1e3
     comp_ms = e0.elapsed_time(e1)
-    comp_bytes = 2 * int((surv != remap).sum()) * cache.block_bytes * 2 * L
+    comp_kms, _ = cache.profile_read()
+    cache.profile(False)
+    moved = int((surv != remap).sum())
+    comp_bytes = 2 * moved * cache.block_bytes * 2 * L
     cache.check()
+    step_ms = cow_ms + comp_ms
+    log(f"[bench] cfg5: CoW {cow_ms:.3f} ms ({cow_bytes / (cow_ms / 1e3) / 1e9:.0f} GB/s), "
+        f"compaction {comp_ms:.2f} ms incl. plan upload, kernel {comp_kms:.2f} ms "
+        f"({comp_bytes / (comp_kms / 1e3) / 1e9:.0f} GB/s)")
+
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "churn_cfg5_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            tr = json.load(f)
+        if tr.get("seed") == args.seed:
+            traffic = tr.get("bytes_per_launch")
+
+    cpu = None
+    if args.cpu_layers > 0:
+        cpu = churn_cpu_baseline(cache, args)
+
     res = {
         "metric": "block churn: copy-on-write + compaction GB/s (bytes moved x2), Llama-3-8B KV, 1 GPU",
-        "value": round(comp_bytes / (comp_ms / 1e3) / 1e9, 1), "unit": "GB/s",
-        "n_gpus": 1, "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+        "value": round((cow_bytes + comp_bytes) / (step_ms / 1e3) / 1e9, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": reps, "warmup": max(1, args.warmup), "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool, seeded fork/evict/remap events)",
         "config": {"workload": "cfg5: 32 layers x 8 kv heads x hd 128, bs 16, bf16, 65536 blocks, "
                                "60% occupancy, 512 CoW copies, 25% eviction, compaction",
-                   "live_blocks": live, "sequences": len(seqs), "survivor_blocks": int(n_surv)},
-        "cow": {"copies": 512, "ms": round(cow_ms, 4), "GBps": round(cow_bytes / (cow_ms / 1e3) / 1e9, 1)},
-        "compaction": {"moved_blocks": int((surv != remap).sum()), "ms_device": round(comp_ms, 3),
-                       "ms_wall_incl_plan": round(comp_wall_ms, 3),
-                       "GBps": round(comp_bytes / (comp_ms / 1e3) / 1e9, 1),
-                       "frac_of_8TBps": round(comp_bytes / (comp_ms / 1e3) / 8e12, 4)},
+                   "live_blocks": live, "sequences": len(seqs), "survivor_blocks": int(n_surv),
+                   "seed": args.seed, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(comp_bytes / (comp_kms / 1e3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(comp_bytes / (comp_kms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "kernel": "pkv::compact_kernel",
+                     "kernel_avg_us": round(comp_kms * 1e3, 1),
+                     "algorithmic_bytes_per_launch": comp_bytes},
+        "cow": {"copies": 512, "ms": round(cow_ms, 4), "kernel_ms": round(cow_kms, 4),
+                "GBps": round(cow_bytes / (cow_ms / 1e3) / 1e9, 1)},
+        "compaction": {"moved_blocks": moved, "ms_device_incl_plan_upload": round(comp_ms, 3),
+                       "ms_wall_incl_plan": round(comp_wall_ms, 3), "kernel_ms": round(comp_kms, 3),
+                       "GBps": round(comp_bytes / (comp_ms / 1e3) / 1e9, 1)},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
     cache.close()
     return 0
+
+
+def churn_cpu_baseline(cache, args):
+    """The oracle's closed-form compaction (memcpy of every moved block, K
+    and V; single thread) on a 1-layer, 8,192-block pool of the same block
+    shape with a 45 % survivor remap like cfg5's, repeated for a bounded
+    sample; GB/s counts bytes moved x2 as the GPU figure does."""
+    import numpy as np
+    import oracle
+    from pagedkv import workload as wl
+
+    nb = 8192
+    bb = cache.block_bytes
+    pool = np.zeros(2 * nb * bb, dtype=np.uint8)
+    pool[::4096] = 1
+    perm = wl.permutation(args.seed ^ 0xCB, nb)
+    n_surv = int(nb * 0.6 * 0.75)
+    src = perm[:n_surv].astype(np.int32)
+    dst = wl.permutation(args.seed ^ 0xCD, n_surv).astype(np.int32)
+    oracle.lib()
+    dt, passes, _ = timed_passes(lambda: oracle.compact(pool, 1, bb, src, dst), args)
+    moved = int((src != dst).sum())
+    gbps = 2 * moved * bb * 2 / dt / 1e9
+    log(f"[bench] cpu baseline: compaction of {moved} blocks in {dt * 1e3:.1f} ms -> {gbps:.2f} GB/s")
+    return {"value": round(gbps, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"closed-form compaction (memcpy) of {moved} of 8192 blocks, 1 layer K+V, "
+                       f"{passes} passes of {dt * 1e3:.1f} ms")}
 
 
 if __name__ == "__main__":

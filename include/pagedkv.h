@@ -126,8 +126,10 @@ int pkv_copy_blocks(pkv_pool* pool, const int32_t* src, const int32_t* dst,
  * Moves block src_host[i] to dst_host[i] for every layer and K/V, in place:
  * the dst set may overlap the src set (e.g. survivors gathered into a
  * contiguous prefix).  src ids distinct, dst ids distinct.  The plan (chains
- * and cycles of the move graph) is built on the host, so ids are host arrays.
- * Each byte is read once and written once; no scratch pool is allocated. */
+ * and cycles of the move graph) is built on the host, so ids are host arrays;
+ * it is uploaded to a device buffer the pool keeps (grown on demand) and the
+ * call returns when the moves are done.  Each byte is read once and written
+ * once; no scratch pool is allocated. */
 int pkv_compact(pkv_pool* pool, const int32_t* src_host,
                 const int32_t* dst_host, int n, void* stream);
 
@@ -188,10 +190,11 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_head, float scale, void* stream);
 
 /* Kernel timing (instrumentation; no reference counterpart).  While enabled,
- * every pkv_decode_attention and pkv_prefill_attention call records HIP
- * events, owned by the pool, on its stream right before and right after its
- * main kernel -- the partition kernel of decode, not its split-context
- * merge; the one kernel of prefill.  pkv_pool_profile_read synchronises,
+ * every pkv_decode_attention, pkv_prefill_attention, pkv_copy_blocks and
+ * pkv_compact call records HIP events, owned by the pool, on its stream right
+ * before and right after its main kernel -- the partition kernel of decode,
+ * not its split-context merge; the one kernel of the others (for compaction,
+ * after the plan upload).  pkv_pool_profile_read synchronises,
  * returns the summed main-kernel time in ms and the number of timed
  * launches since the last read, and clears the record. */
 int pkv_pool_profile(pkv_pool* pool, int enable);
