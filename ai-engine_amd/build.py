@@ -30,6 +30,7 @@ SOURCES = [
     "pkv_kvcopy.hip",
     "pkv_decode.hip",
     "pkv_prefill.hip",
+    "pkv_rope.hip",
 ]
 
 # Packed-FP32 instructions stay off (the compiler would otherwise form

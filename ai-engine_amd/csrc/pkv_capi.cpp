@@ -465,43 +465,75 @@ static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
   return PKV_OK;
 }
 
+// Shared validation and launch of pkv_decode_attention(_rope).
+static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream) {
+  if (int rc = check_layer(p, layer)) return rc;
+  if (a.batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", a.batch);
+  if (a.batch == 0) return PKV_OK;
+  if (!a.q || !a.out || !a.block_tables || !a.context_lens)
+    return fail(p, PKV_ERR_INVALID, "q, out, block_tables and context_lens must be non-NULL");
+  if ((a.k_new == nullptr) != (a.v_new == nullptr))
+    return fail(p, PKV_ERR_INVALID, "k_new and v_new must both be set or both be NULL");
+  if (!aligned16(a.q) || !aligned16(a.out) ||
+      (a.k_new && (!aligned16(a.k_new) || !aligned16(a.v_new))))
+    return fail(p, PKV_ERR_INVALID, "q, out, k_new, v_new must be 16-byte aligned");
+  if (a.max_blocks_per_seq <= 0 || a.max_context_len <= 0)
+    return fail(p, PKV_ERR_INVALID, "max_blocks_per_seq (%d) and max_context_len (%d) must be > 0",
+                a.max_blocks_per_seq, a.max_context_len);
+  if (a.n_head <= 0 || a.n_head % p->n_kv_head != 0)
+    return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", a.n_head,
+                p->n_kv_head);
+  if (!pkv::decode_supported(p, a.n_head))
+    return fail(p, PKV_ERR_UNSUPPORTED, "decode: n_head/n_kv_head = %d not in {1,2,4,8}",
+                a.n_head / p->n_kv_head);
+  if (a.out_dtype != PKV_F32 && a.out_dtype != p->dtype)
+    return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
+  if (!(a.scale == a.scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
+  DeviceGuard dg(p->device);
+  size_t cb = 0;
+  size_t need = pkv::decode_workspace_bytes(p, a.batch, a.n_head, a.max_context_len, &cb);
+  if (int rc = ensure_workspace(p, need, cb)) return rc;
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
+  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
+  if (e != hipSuccess) return hip_fail(p, e, "decode launch");
+  return PKV_OK;
+}
+
 int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
                          const int32_t* block_tables, int max_blocks_per_seq,
                          const int32_t* context_lens, int max_context_len, int batch,
                          int n_head, float scale, const void* k_new, const void* v_new,
                          void* stream) {
   CHECK_POOL(p);
-  if (int rc = check_layer(p, layer)) return rc;
-  if (batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", batch);
-  if (batch == 0) return PKV_OK;
-  if (!q || !out || !block_tables || !context_lens)
-    return fail(p, PKV_ERR_INVALID, "q, out, block_tables and context_lens must be non-NULL");
-  if ((k_new == nullptr) != (v_new == nullptr))
-    return fail(p, PKV_ERR_INVALID, "k_new and v_new must both be set or both be NULL");
-  if (!aligned16(q) || !aligned16(out) || (k_new && (!aligned16(k_new) || !aligned16(v_new))))
-    return fail(p, PKV_ERR_INVALID, "q, out, k_new, v_new must be 16-byte aligned");
-  if (max_blocks_per_seq <= 0 || max_context_len <= 0)
-    return fail(p, PKV_ERR_INVALID, "max_blocks_per_seq (%d) and max_context_len (%d) must be > 0",
-                max_blocks_per_seq, max_context_len);
-  if (n_head <= 0 || n_head % p->n_kv_head != 0)
-    return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
-  if (!pkv::decode_supported(p, n_head))
-    return fail(p, PKV_ERR_UNSUPPORTED, "decode: n_head/n_kv_head = %d not in {1,2,4,8}",
-                n_head / p->n_kv_head);
-  if (out_dtype != PKV_F32 && out_dtype != p->dtype)
-    return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
-  if (!(scale == scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
-  DeviceGuard dg(p->device);
-  size_t cb = 0;
-  size_t need = pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, &cb);
-  if (int rc = ensure_workspace(p, need, cb)) return rc;
   pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
                     max_context_len, batch, n_head, scale, k_new, v_new};
-  hipEvent_t eb = nullptr, ee = nullptr;
-  if (int rc = profile_slot(p, &eb, &ee)) return rc;
-  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
-  if (e != hipSuccess) return hip_fail(p, e, "decode launch");
-  return PKV_OK;
+  return decode_call(p, layer, a, stream);
+}
+
+int pkv_decode_attention_rope(pkv_pool* p, int layer, const pkv_rope* rope,
+                              const int32_t* positions, int in_dtype, const void* q, void* out,
+                              int out_dtype, const int32_t* block_tables, int max_blocks_per_seq,
+                              const int32_t* context_lens, int max_context_len, int batch,
+                              int n_head, float scale, const void* k_new, const void* v_new,
+                              void* stream) {
+  CHECK_POOL(p);
+  if (!rope) return fail(p, PKV_ERR_INVALID, "rope is NULL");
+  if (rope->rope_dim != p->head_dim)
+    return fail(p, PKV_ERR_INVALID, "rope_dim %d != head_dim %d", rope->rope_dim, p->head_dim);
+  if (rope->device != p->device)
+    return fail(p, PKV_ERR_INVALID, "rope tables on device %d, pool on device %d", rope->device,
+                p->device);
+  if (in_dtype != PKV_F32 && in_dtype != p->dtype)
+    return fail(p, PKV_ERR_INVALID, "in_dtype must be PKV_F32 or the pool dtype");
+  pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
+                    max_context_len, batch, n_head, scale, k_new, v_new};
+  a.rope_cos = rope->cos;
+  a.rope_sin = rope->sin;
+  a.rope_max = rope->max_seq;
+  a.positions = positions;
+  a.in_f32 = in_dtype == PKV_F32;
+  return decode_call(p, layer, a, stream);
 }
 
 int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
@@ -560,6 +592,105 @@ int pkv_pool_profile_read(pkv_pool* p, double* total_ms, int* launches) {
   return PKV_OK;
 }
 
+int pkv_rope_tables_host(int rope_dim, float freq_base, int max_seq, float* cos_host,
+                         float* sin_host) {
+  if (rope_dim <= 0 || rope_dim % 8 != 0 || max_seq <= 0 || !(freq_base > 0.0f))
+    return fail(nullptr, PKV_ERR_INVALID,
+                "rope: rope_dim %d (a positive multiple of 8), max_seq %d, freq_base %g",
+                rope_dim, max_seq, (double)freq_base);
+  if (!cos_host || !sin_host) return fail(nullptr, PKV_ERR_INVALID, "rope: NULL table");
+  pkv::rope_tables_host(rope_dim, freq_base, max_seq, cos_host, sin_host);
+  return PKV_OK;
+}
+
+int pkv_rope_create(pkv_rope** out, int rope_dim, float freq_base, int max_seq, int device) {
+  if (!out) return fail(nullptr, PKV_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(nullptr, PKV_ERR_INVALID, "device %d not available (%d devices)", device, ndev);
+  size_t n = (size_t)max_seq * (size_t)(rope_dim > 0 ? rope_dim / 2 : 0);
+  std::vector<float> c(n), s(n);
+  if (int rc = pkv_rope_tables_host(rope_dim, freq_base, max_seq, c.data(), s.data())) return rc;
+  pkv_rope* r = new (std::nothrow) pkv_rope();
+  if (!r) return fail(nullptr, PKV_ERR_OOM, "host allocation failed");
+  r->rope_dim = rope_dim;
+  r->max_seq = max_seq;
+  r->device = device;
+  DeviceGuard dg(device);
+  void *dc = nullptr, *ds = nullptr, *de = nullptr;
+  hipError_t e = hipMalloc(&dc, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&ds, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&de, 256);
+  if (e == hipSuccess) e = hipMemcpy(dc, c.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(ds, s.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(de, 0, 256);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    if (dc) (void)hipFree(dc);
+    if (ds) (void)hipFree(ds);
+    if (de) (void)hipFree(de);
+    delete r;
+    return fail(nullptr, PKV_ERR_OOM, "rope tables: %s", hipGetErrorString(e));
+  }
+  r->cos = static_cast<float*>(dc);
+  r->sin = static_cast<float*>(ds);
+  r->err = static_cast<uint32_t*>(de);
+  *out = r;
+  return PKV_OK;
+}
+
+int pkv_rope_destroy(pkv_rope* r) {
+  if (!r) return PKV_OK;
+  DeviceGuard dg(r->device);
+  (void)hipDeviceSynchronize();
+  if (r->cos) (void)hipFree(r->cos);
+  if (r->sin) (void)hipFree(r->sin);
+  if (r->err) (void)hipFree(r->err);
+  delete r;
+  return PKV_OK;
+}
+
+int pkv_rope_tables(const pkv_rope* r, const float** cos_dev, const float** sin_dev) {
+  if (!r) return fail(nullptr, PKV_ERR_INVALID, "rope is NULL");
+  if (cos_dev) *cos_dev = r->cos;
+  if (sin_dev) *sin_dev = r->sin;
+  return PKV_OK;
+}
+
+int pkv_rope_apply(pkv_rope* r, const void* x, int in_dtype, void* out, int out_dtype,
+                   const int32_t* positions, int n_tokens, int n_head, void* stream) {
+  if (!r) return fail(nullptr, PKV_ERR_INVALID, "rope is NULL");
+  if (n_tokens < 0 || n_head <= 0)
+    return fail(nullptr, PKV_ERR_INVALID, "n_tokens %d, n_head %d", n_tokens, n_head);
+  if (n_tokens == 0) return PKV_OK;
+  auto dt_ok = [](int dt) { return dt == PKV_F32 || dt == PKV_F16 || dt == PKV_BF16; };
+  if (!dt_ok(in_dtype) || !dt_ok(out_dtype))
+    return fail(nullptr, PKV_ERR_INVALID, "rope: dtypes %d -> %d", in_dtype, out_dtype);
+  if (!x || !out || !positions) return fail(nullptr, PKV_ERR_INVALID, "rope: NULL argument");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return fail(nullptr, PKV_ERR_INVALID, "rope: x and out must be 16-byte aligned");
+  if (x == out && in_dtype != out_dtype)
+    return fail(nullptr, PKV_ERR_INVALID, "rope: in-place needs equal dtypes");
+  DeviceGuard dg(r->device);
+  hipError_t e = pkv::launch_rope_apply(r, x, in_dtype, out, out_dtype, positions, n_tokens,
+                                        n_head, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(nullptr, e, "rope launch");
+  return PKV_OK;
+}
+
+int pkv_rope_check(pkv_rope* r) {
+  if (!r) return fail(nullptr, PKV_ERR_INVALID, "rope is NULL");
+  DeviceGuard dg(r->device);
+  uint32_t bits = 0;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(&bits, r->err, 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && bits) e = hipMemset(r->err, 0, 4);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "rope check");
+  if (bits) return fail(nullptr, PKV_ERR_DEVICE_DATA, "rope: position outside the table");
+  return PKV_OK;
+}
+
 int pkv_pool_check(pkv_pool* p) {
   CHECK_POOL(p);
   DeviceGuard dg(p->device);
@@ -573,6 +704,7 @@ int pkv_pool_check(pkv_pool* p) {
     if (bits & PKV_EBIT_SLOT) what += " slot-out-of-range";
     if (bits & PKV_EBIT_BLOCK) what += " block-id-out-of-range";
     if (bits & PKV_EBIT_LENGTH) what += " context-length-out-of-range";
+    if (bits & PKV_EBIT_POSITION) what += " rope-position-out-of-range";
     return fail(p, PKV_ERR_DEVICE_DATA, "device data errors:%s", what.c_str());
   }
   return PKV_OK;

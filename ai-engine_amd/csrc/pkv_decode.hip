@@ -107,7 +107,70 @@ struct DecodeKArgs {
   float* part_ml;
   float* part_o;
   uint32_t* err;
+  const float* rope_cos;  // RoPE tables [rope_max][HD / 2], or null
+  const float* rope_sin;
+  int rope_max;
+  const int32_t* positions;  // null: position = context_len - 1
+  int in_f32;                // q / k_new / v_new are f32 (else the pool dtype)
 };
+
+// N elements of a row, from f32 or 16-bit storage, as floats.
+template <int DT, int N>
+__device__ __forceinline__ void load_elems(const char* row, int elem, bool f32,
+                                           float (&x)[N]) {
+  auto from_f32 = [&]() {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(row + (size_t)(elem + i) * 4);
+      x[i] = v[0];
+      x[i + 1] = v[1];
+      x[i + 2] = v[2];
+      x[i + 3] = v[3];
+    }
+  };
+  if constexpr (DT == PKV_F32) {
+    from_f32();
+  } else {
+    static_assert(N == 8, "16-bit rows are read 8 elements (16 bytes) at a time");
+    if (f32)
+      from_f32();
+    else
+      widen16<DT, 8>(ld16(row + (size_t)elem * 2), x);
+  }
+}
+
+// 16 bytes of pool-dtype storage from EPL floats (round to nearest even).
+template <int DT, int EPL>
+__device__ __forceinline__ u32x4 pack16(const float (&x)[EPL]) {
+  if constexpr (DT == PKV_F32) {
+    return u32x4{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                 __float_as_uint(x[3])};
+  } else {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = DT == PKV_BF16 ? f32_to_bf16_bits(x[2 * i]) : f32_to_f16_bits(x[2 * i]);
+      const uint32_t hi =
+          DT == PKV_BF16 ? f32_to_bf16_bits(x[2 * i + 1]) : f32_to_f16_bits(x[2 * i + 1]);
+      w[i] = lo | (hi << 16);
+    }
+    return w;
+  }
+}
+
+// Rotate-half RoPE of N element pairs (x1 = first half, x2 = second half):
+// o1 = x1 cos - x2 sin, o2 = x1 sin + x2 cos, each product rounded in f32.
+template <int N>
+__device__ __forceinline__ void rope_rotate(float (&x1)[N], float (&x2)[N], const float* c,
+                                            const float* s) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float a = x1[i], b = x2[i];
+    x1[i] = a * c[i] - b * s[i];
+    x2[i] = a * s[i] + b * c[i];
+  }
+}
 
 template <int EPL>
 __device__ __forceinline__ void store_out(void* out, size_t elem_off, int out_f32,
@@ -241,7 +304,7 @@ __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long k
   return false;  // not reached: the bucket counts cover every sequence
 }
 
-template <int DT, int HD, int R>
+template <int DT, int HD, int R, bool ROPE>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
   using C = DCfg<DT, HD, R>;
@@ -304,7 +367,33 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   int tbl = 0;
   if (lane < nblk) tbl = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
   u32x4 qf[C::NF];
-  {
+  int rpos = 0;  // RoPE position of this sequence's new token
+  if constexpr (ROPE) {
+    // Rotate Q in the kernel (transformer.rs:252-269).  Fragment f of a lane
+    // holds elements f * 64/E + G * EPL .. + EPL - 1, so the partner of each
+    // element (+ HD/2) sits in fragment f + NF/2 of the same lane.
+    rpos = a.positions ? a.positions[b] : ctx_raw - 1;
+    if (rpos < 0 || rpos >= a.rope_max) {
+      if (lane == 0) atomicOr(a.err, PKV_EBIT_POSITION);
+      rpos = 0;
+    }
+    const size_t irb = a.in_f32 ? (size_t)HD * 4 : (size_t)C::RB;
+    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * irb;
+    const float* cr = a.rope_cos + (size_t)rpos * (HD / 2);
+    const float* sr = a.rope_sin + (size_t)rpos * (HD / 2);
+#pragma unroll
+    for (int f = 0; f < C::NF / 2; ++f) {
+      const int e0 = f * (64 / C::E) + G * C::EPL;
+      float x1[C::EPL], x2[C::EPL], cs[C::EPL], sn[C::EPL];
+      load_elems<DT, C::EPL>(qrow, e0, a.in_f32, x1);
+      load_elems<DT, C::EPL>(qrow, e0 + HD / 2, a.in_f32, x2);
+      load_elems<PKV_F32, C::EPL>(reinterpret_cast<const char*>(cr), e0, true, cs);
+      load_elems<PKV_F32, C::EPL>(reinterpret_cast<const char*>(sr), e0, true, sn);
+      rope_rotate<C::EPL>(x1, x2, cs, sn);
+      qf[f] = col < R ? pack16<DT, C::EPL>(x1) : u32x4{0, 0, 0, 0};
+      qf[f + C::NF / 2] = col < R ? pack16<DT, C::EPL>(x2) : u32x4{0, 0, 0, 0};
+    }
+  } else {
     const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * C::RB;
 #pragma unroll
     for (int f = 0; f < C::NF; ++f)
@@ -324,7 +413,31 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     const char* vnew_row = a.v_new + ((size_t)b * a.kvh + g) * C::RB;
     int blk = readlane_i(tbl, (new_pos >> a.bs_log2) - blk_begin);
     size_t off = ((size_t)blk * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
-    if (lane < C::CH) {
+    if constexpr (ROPE) {
+      // k rotated like q (same position), v converted; chunk c < CH/2 and its
+      // partner c + CH/2 are rotated together by lane c.
+      const size_t irb = a.in_f32 ? (size_t)HD * 4 : (size_t)C::RB;
+      const char* krow = a.k_new + ((size_t)b * a.kvh + g) * irb;
+      const char* vrow = a.v_new + ((size_t)b * a.kvh + g) * irb;
+      if (lane < C::CH / 2) {
+        const int e0 = lane * C::EPL;
+        float x1[C::EPL], x2[C::EPL], cs[C::EPL], sn[C::EPL];
+        load_elems<DT, C::EPL>(krow, e0, a.in_f32, x1);
+        load_elems<DT, C::EPL>(krow, e0 + HD / 2, a.in_f32, x2);
+        load_elems<PKV_F32, C::EPL>(
+            reinterpret_cast<const char*>(a.rope_cos + (size_t)rpos * (HD / 2)), e0, true, cs);
+        load_elems<PKV_F32, C::EPL>(
+            reinterpret_cast<const char*>(a.rope_sin + (size_t)rpos * (HD / 2)), e0, true, sn);
+        rope_rotate<C::EPL>(x1, x2, cs, sn);
+        st16(a.k_pool + off + lane * 16, pack16<DT, C::EPL>(x1));
+        st16(a.k_pool + off + (lane + C::CH / 2) * 16, pack16<DT, C::EPL>(x2));
+      }
+      if (lane < C::CH) {
+        float x[C::EPL];
+        load_elems<DT, C::EPL>(vrow, lane * C::EPL, a.in_f32, x);
+        st16(a.v_pool + off + lane * 16, pack16<DT, C::EPL>(x));
+      }
+    } else if (lane < C::CH) {
       st16(a.k_pool + off + lane * 16, ld16(knew_row + lane * 16));
       st16(a.v_pool + off + lane * 16, ld16(vnew_row + lane * 16));
     }
@@ -636,7 +749,10 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 template <int DT, int HD, int R>
 hipError_t launch_t(const DecodeKArgs& k, long long items, hipStream_t s) {
   unsigned grid = (unsigned)((items + kWavesPerBlock - 1) / kWavesPerBlock);
-  decode_kernel<DT, HD, R><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  if (k.rope_cos)
+    decode_kernel<DT, HD, R, true><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  else
+    decode_kernel<DT, HD, R, false><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
   return hipGetLastError();
 }
 
@@ -738,6 +854,11 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.k_new = reinterpret_cast<const char*>(a.k_new);
   k.v_new = reinterpret_cast<const char*>(a.v_new);
+  k.rope_cos = a.rope_cos;
+  k.rope_sin = a.rope_sin;
+  k.rope_max = a.rope_max;
+  k.positions = a.positions;
+  k.in_f32 = a.in_f32;
   size_t cb = p->ws_counter_bytes;
   size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   k.part_ml = reinterpret_cast<float*>(p->ws + cb);

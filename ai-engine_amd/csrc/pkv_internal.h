@@ -50,11 +50,22 @@ struct pkv_pool {
   char* layer_v(int layer) const { return layer_k(layer) + layer_bytes; }
 };
 
-// Device error bits (pkv_pool::err).
+// RoPE tables (Rope::new) in device memory.
+struct pkv_rope {
+  int rope_dim = 0;
+  int max_seq = 0;
+  int device = 0;
+  float* cos = nullptr;     // [max_seq][rope_dim / 2]
+  float* sin = nullptr;
+  uint32_t* err = nullptr;  // device error word of pkv_rope_apply
+};
+
+// Device error bits (pkv_pool::err, pkv_rope::err).
 enum : uint32_t {
   PKV_EBIT_SLOT = 1u,      // append/gather slot out of range
   PKV_EBIT_BLOCK = 2u,     // block table entry out of range
   PKV_EBIT_LENGTH = 4u,    // context length beyond max_context_len / table
+  PKV_EBIT_POSITION = 8u,  // RoPE position outside the table
 };
 
 namespace pkv {
@@ -80,6 +91,13 @@ hipError_t launch_compact(const pkv_pool* p, const int32_t* ops,
 hipError_t launch_fill_normal(const pkv_pool* p, uint64_t seed,
                               hipStream_t stream);
 
+// Host computation of the RoPE tables (Rope::new, rope.rs:14-23).
+void rope_tables_host(int rope_dim, float freq_base, int max_seq, float* cos_t,
+                      float* sin_t);
+hipError_t launch_rope_apply(const pkv_rope* r, const void* x, int in_dtype,
+                             void* out, int out_dtype, const int32_t* positions,
+                             int n_tokens, int n_head, hipStream_t stream);
+
 struct DecodeArgs {
   const void* q;
   void* out;
@@ -93,6 +111,12 @@ struct DecodeArgs {
   float scale;
   const void* k_new;
   const void* v_new;
+  // RoPE inside the kernel (rope_cos == nullptr: q and k_new are final)
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  int rope_max = 0;
+  const int32_t* positions = nullptr;
+  int in_f32 = 0;  // q, k_new, v_new are f32 (else the pool dtype)
 };
 
 // Partition length (tokens) and number of partitions the decode kernel uses

@@ -23,7 +23,8 @@ from ._lib import (BF16, F16, F32, K, V, CapacityError, PagedKvError, check, lib
                    LIB_PATH)
 
 __all__ = [
-    "BlockAllocator", "BlockTable", "PagedKvCache", "KvPool", "CapacityError",
+    "BlockAllocator", "BlockTable", "PagedKvCache", "KvPool", "Rope", "rope_tables_host",
+    "CapacityError",
     "PagedKvError", "F32", "F16", "BF16", "lib", "LIB_PATH", "torch_dtype",
     "pkv_dtype",
 ]
@@ -134,6 +135,61 @@ def _i32(x, device):
     else:
         t = torch.as_tensor(x, dtype=torch.int32).to(device)
     return t.contiguous()
+
+
+def rope_tables_host(rope_dim: int, freq_base: float, max_seq: int):
+    """Rope::new's cos/sin tables (rope.rs:14-23) computed by the library on
+    the host: two float32 arrays (max_seq, rope_dim // 2)."""
+    import numpy as np
+    c = np.zeros((max_seq, rope_dim // 2), np.float32)
+    s = np.zeros_like(c)
+    check(lib().pkv_rope_tables_host(rope_dim, freq_base, max_seq, c.ctypes.data,
+                                     s.ctypes.data), None)
+    return c, s
+
+
+class Rope:
+    """The reference's Rope (rope.rs:6-33): cos/sin tables in device memory;
+    apply() is apply_rope (rope.rs:38-42) with per-token positions."""
+
+    def __init__(self, rope_dim: int, freq_base: float, max_seq: int, device: int = 0) -> None:
+        import torch
+        h = ctypes.c_void_p()
+        check(lib().pkv_rope_create(ctypes.byref(h), rope_dim, freq_base, max_seq, device), None)
+        self._h = h
+        self.rope_dim, self.freq_base, self.max_seq = rope_dim, freq_base, max_seq
+        self.device = torch.device("cuda", device)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        h = getattr(self, "_h", None)
+        if h:
+            lib().pkv_rope_destroy(h)
+            self._h = None
+
+    def __del__(self) -> None:
+        self.close()
+
+    def apply(self, x, positions, out_dtype=None, out=None, stream=None):
+        """x: (n_tokens, n_head, rope_dim) f32/f16/bf16 on the device;
+        positions: (n_tokens,) int32.  Returns the rotated rows."""
+        import torch
+        if x.dim() != 3 or x.shape[2] != self.rope_dim:
+            raise ValueError(f"x must be (n, heads, {self.rope_dim})")
+        xx = x.contiguous()
+        if out is None:
+            out = torch.empty(xx.shape, dtype=out_dtype or xx.dtype, device=xx.device)
+        pos = _i32(positions, xx.device)
+        check(lib().pkv_rope_apply(self._h, _dev_ptr(xx), pkv_dtype(xx.dtype), _dev_ptr(out),
+                                   pkv_dtype(out.dtype), _dev_ptr(pos), xx.shape[0],
+                                   xx.shape[1], _stream_ptr(stream)), None)
+        return out
+
+    def check(self) -> None:
+        check(lib().pkv_rope_check(self._h), None)
 
 
 class PagedKvCache:
@@ -291,11 +347,17 @@ class KvPool:
     # -- decode attention ---------------------------------------------------
     def decode_attention(self, q, block_tables, context_lens, max_context_len: int | None = None,
                          k_new=None, v_new=None, scale: float | None = None, out_dtype=None,
-                         out=None, stream=None):
+                         out=None, stream=None, rope: "Rope | None" = None, positions=None):
         """q: (B, H, hd); block_tables: (B, max_nb) int32 device; context_lens:
         (B,) int32 device = keys attended (seq_lens + 1).  With k_new/v_new
         (B, n_kv, hd) the new token is stored at position context_lens-1 first.
-        Returns (B, H*hd)."""
+        With `rope`, q and k_new are the projections before rotation (f32 or
+        the pool dtype) and the kernel applies the rotary embedding at
+        `positions` (default context_lens - 1).  Returns (B, H*hd)."""
+        if rope is not None:
+            return self._decode_attention_rope(q, block_tables, context_lens, max_context_len,
+                                               k_new, v_new, scale, out_dtype, out, stream,
+                                               rope, positions)
         import torch
         c = self.cache
         B, H, hd = q.shape
@@ -322,6 +384,38 @@ class KvPool:
             _dev_ptr(bt), bt.shape[1], _dev_ptr(cl), int(max_context_len), B, H, float(scale),
             _dev_ptr(k_new) if k_new is not None else None,
             _dev_ptr(v_new) if v_new is not None else None, _stream_ptr(stream)), self._h)
+        return out
+
+    def _decode_attention_rope(self, q, block_tables, context_lens, max_context_len, k_new,
+                               v_new, scale, out_dtype, out, stream, rope, positions):
+        import torch
+        c = self.cache
+        B, H, hd = q.shape
+        if hd != c.head_dim:
+            raise ValueError("head_dim mismatch")
+        if q.dtype not in (torch.float32, c.dtype):
+            raise TypeError("q must be float32 or the pool dtype")
+        for t, name in ((k_new, "k_new"), (v_new, "v_new")):
+            if t is not None and (t.dtype != q.dtype or t.shape != (B, c.n_kv_head, hd)):
+                raise ValueError(f"{name} must be ({B}, {c.n_kv_head}, {hd}) in q's dtype")
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        bt = _i32(block_tables, c.device)
+        cl = _i32(context_lens, c.device)
+        if max_context_len is None:
+            max_context_len = int(cl.max().item()) if B else 1
+        if out is None:
+            out = torch.empty((B, H * hd), dtype=out_dtype or c.dtype, device=c.device)
+        pos = _i32(positions, c.device) if positions is not None else None
+        qq = q.contiguous()
+        kk = k_new.contiguous() if k_new is not None else None
+        vv = v_new.contiguous() if v_new is not None else None
+        check(lib().pkv_decode_attention_rope(
+            self._h, self.layer_index, rope.handle, _dev_ptr(pos) if pos is not None else None,
+            pkv_dtype(qq.dtype), _dev_ptr(qq), _dev_ptr(out), pkv_dtype(out.dtype), _dev_ptr(bt),
+            bt.shape[1], _dev_ptr(cl), int(max_context_len), B, H, float(scale),
+            _dev_ptr(kk) if kk is not None else None, _dev_ptr(vv) if vv is not None else None,
+            _stream_ptr(stream)), self._h)
         return out
 
     # -- chunked prefill attention -------------------------------------------

@@ -51,6 +51,14 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_prefill_attention": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                    ctypes.c_float, _P]),
     "pkv_pool_check": (_I, [_P]),
+    "pkv_rope_tables_host": (_I, [_I, ctypes.c_float, _I, _P, _P]),
+    "pkv_rope_create": (_I, [ctypes.POINTER(_P), _I, ctypes.c_float, _I, _I]),
+    "pkv_rope_destroy": (_I, [_P]),
+    "pkv_rope_tables": (_I, [_P, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "pkv_rope_apply": (_I, [_P, _P, _I, _P, _I, _P, _I, _I, _P]),
+    "pkv_rope_check": (_I, [_P]),
+    "pkv_decode_attention_rope": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I,
+                                       ctypes.c_float, _P, _P, _P]),
     "pkv_pool_profile": (_I, [_P, _I]),
     "pkv_pool_profile_read": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "pkv_allocator_new": (_P, [_SZ, _SZ]),

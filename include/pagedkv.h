@@ -189,6 +189,58 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_seqs, int max_q_len, int max_context_len,
                           int n_head, float scale, void* stream);
 
+/* ---- rotary position embedding (crates/ai-engine-candle/src/paged/rope.rs,
+ * applied per row in the decode step, transformer.rs:252-269) ---------------
+ * Tables as Rope::new (rope.rs:14-23): theta_i = 1 / freq_base^(2 i / rope_dim)
+ * in f32, angle[p][i] = (float)p * theta_i, cos/sin in f32, shape
+ * [max_seq][rope_dim / 2].  The rotation is candle's rotate-half rope that
+ * apply_rope uses (rope.rs:38-42): for the halves x1 = x[i], x2 = x[i + d/2]
+ * of a head row, out[i] = x1 cos - x2 sin, out[i + d/2] = x1 sin + x2 cos,
+ * in f32 with every product rounded (no fused multiply-add), then rounded to
+ * the output dtype.  rope_dim is the head_dim of the rows it rotates. */
+typedef struct pkv_rope pkv_rope;
+
+/* Fills host arrays cos_host, sin_host [max_seq][rope_dim / 2] (host only). */
+int pkv_rope_tables_host(int rope_dim, float freq_base, int max_seq,
+                         float* cos_host, float* sin_host);
+/* Tables computed on the host (as above) and kept in device memory. */
+int pkv_rope_create(pkv_rope** out, int rope_dim, float freq_base, int max_seq,
+                    int device);
+int pkv_rope_destroy(pkv_rope* rope);
+/* Device pointers of the tables (e.g. to share them with other kernels). */
+int pkv_rope_tables(const pkv_rope* rope, const float** cos_dev,
+                    const float** sin_dev);
+/* x: [n_tokens][n_head][rope_dim] in in_dtype; out: same shape in out_dtype
+ * (each PKV_F32, PKV_F16 or PKV_BF16; out may alias x when the dtypes
+ * match).  positions: device int32 [n_tokens], token t rotated by row
+ * positions[t] (Rope::gather, rope.rs:28-32).  A position outside
+ * [0, max_seq) leaves that token's rows unwritten and makes the next
+ * pkv_rope_check() report PKV_ERR_DEVICE_DATA. */
+int pkv_rope_apply(pkv_rope* rope, const void* x, int in_dtype, void* out,
+                   int out_dtype, const int32_t* positions, int n_tokens,
+                   int n_head, void* stream);
+int pkv_rope_check(pkv_rope* rope);
+
+/* Decode attention with the rotary embedding applied inside the kernel: the
+ * decode step's per-row RoPE of q and of the new k (transformer.rs:252-269)
+ * followed by pkv_decode_attention (same arguments and results).  q and
+ * k_new are the projections before rotation and v_new the new values, all
+ * in in_dtype (PKV_F32 -- the reference's activations -- or the pool dtype);
+ * the rotated q and k are rounded to the pool dtype, as stored k rows are.
+ * positions: device int32 [batch] or NULL; NULL uses context_lens[b] - 1,
+ * the reference's decode position (positions == seq_lens, engine.rs:130-133).
+ * rope->rope_dim must equal the pool's head_dim.  A position outside
+ * [0, max_seq) is reported by pkv_pool_check() and rotates by position 0. */
+int pkv_decode_attention_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
+                              const int32_t* positions, int in_dtype,
+                              const void* q, void* out, int out_dtype,
+                              const int32_t* block_tables,
+                              int max_blocks_per_seq,
+                              const int32_t* context_lens, int max_context_len,
+                              int batch, int n_head, float scale,
+                              const void* k_new, const void* v_new,
+                              void* stream);
+
 /* Kernel timing (instrumentation; no reference counterpart).  While enabled,
  * every pkv_decode_attention, pkv_prefill_attention, pkv_copy_blocks and
  * pkv_compact call records HIP events, owned by the pool, on its stream right

@@ -75,6 +75,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_prefill_inplace.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _SZ,
                                       _P, _P, _P, _SZ, ctypes.c_float, _P, ctypes.c_int]
     L.orc_prefill_inplace.restype = None
+    L.orc_rope_table.argtypes = [_SZ, ctypes.c_float, _SZ, _P, _P]
+    L.orc_rope_table.restype = None
+    L.orc_rope_apply.argtypes = [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P]
+    L.orc_rope_apply.restype = None
     L.orc_threads.argtypes = [ctypes.c_int]
     L.orc_threads.restype = ctypes.c_int
 
@@ -277,6 +281,29 @@ def prefill_inplace(k_pool, v_pool, dtype: int, block_size: int, tables, cu_q_le
     lib().orc_prefill_inplace(_p(k_pool), _p(v_pool), dtype, block_size, KVH, hd, _p(tables),
                               tables.shape[1], _p(cu), _p(cl), cl.size, _p(q), kn, vn, H,
                               float(scale), _p(out), int(n_threads))
+    return out
+
+
+def rope_table(rope_dim: int, freq_base: float, max_seq: int):
+    """Rope::new (rope.rs:14-23): f32 cos/sin tables (max_seq, rope_dim/2)."""
+    half = rope_dim // 2
+    c = np.zeros((max_seq, half), np.float32)
+    s = np.zeros((max_seq, half), np.float32)
+    lib().orc_rope_table(rope_dim, freq_base, max_seq, _p(c), _p(s))
+    return c, s
+
+
+def rope_apply(x, cos_t, sin_t, positions) -> np.ndarray:
+    """apply_rope (rope.rs:38-42) on x (n_tokens, n_head, d) float32, each
+    token at its own position (transformer.rs:252-269)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, h, d = x.shape
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    assert pos.shape == (n,) and cos_t.shape[1] * 2 == d
+    assert pos.min(initial=0) >= 0 and pos.max(initial=0) < cos_t.shape[0]
+    out = np.empty_like(x)
+    lib().orc_rope_apply(_p(x), _p(out), n, h, d, _p(np.ascontiguousarray(cos_t)),
+                         _p(np.ascontiguousarray(sin_t)), _p(pos))
     return out
 
 

@@ -33,6 +33,13 @@
  *                           decode (one query), chunk-split invariance, and
  *                           brute-force torch float64 on tiny inputs.
  *   orc_copy/compact      - closed-form out-of-place memcpy.
+ *   orc_rope_table        - the reference's KAT (rope.rs:49-63: gathered rows
+ *                           equal table rows), float64 restatement of
+ *                           p * base^(-2i/d) within 1 ulp, cos^2 + sin^2 = 1,
+ *                           position 0 = (1, 0).
+ *   orc_rope_apply        - identity at position 0, pairwise norm
+ *                           preservation, rotation composition, relative-
+ *                           position invariance of q.k, float64 rotation.
  */
 #include <math.h>
 #include <stdint.h>
@@ -598,6 +605,51 @@ void orc_prefill_inplace(void* k_pool, void* v_pool, int dtype, size_t bs,
 }
 
 /* Number of OpenMP threads the baseline uses for a requested count. */
+/* ------------------------------------------------------------------------ */
+/* rotary position embedding (crates/ai-engine-candle/src/paged/rope.rs)      */
+/* ------------------------------------------------------------------------ */
+/* Rope::new (rope.rs:14-23): theta_i = 1 / base^(2 i / dim) in f32 (powf),
+ * freqs[p][i] = (float)p * theta_i (the matmul of a (max_seq, 1) column by a
+ * (1, dim/2) row: one product per element), cos/sin in f32 (libm). */
+void orc_rope_table(size_t rope_dim, float base, size_t max_seq, float* cos_t,
+                    float* sin_t) {
+    size_t half = rope_dim / 2;
+    for (size_t i = 0; i < half; i++) {
+        float theta = 1.0f / powf(base, 2.0f * (float)i / (float)rope_dim);
+        for (size_t p = 0; p < max_seq; p++) {
+            float f = (float)p * theta;
+            cos_t[p * half + i] = cosf(f);
+            sin_t[p * half + i] = sinf(f);
+        }
+    }
+}
+
+/* apply_rope (rope.rs:38-42) = candle_nn::rotary_emb::rope, rotate-half:
+ * for the halves x1 = x[i], x2 = x[i + d/2] of every (token, head) row,
+ * out[i] = x1 cos - x2 sin, out[i + d/2] = x1 sin + x2 cos, in f32 with each
+ * product rounded (no fused multiply-add; the Makefile turns contraction
+ * off).  Row t uses its own position pos[t] (transformer.rs:252-269). */
+void orc_rope_apply(const float* x, float* out, size_t n_tokens, size_t n_head,
+                    size_t d, const float* cos_t, const float* sin_t,
+                    const int32_t* pos) {
+    size_t half = d / 2;
+    for (size_t t = 0; t < n_tokens; t++) {
+        const float* c = cos_t + (size_t)pos[t] * half;
+        const float* s = sin_t + (size_t)pos[t] * half;
+        for (size_t h = 0; h < n_head; h++) {
+            const float* xr = x + (t * n_head + h) * d;
+            float* o = out + (t * n_head + h) * d;
+            for (size_t i = 0; i < half; i++) {
+                float x1 = xr[i], x2 = xr[i + half];
+                float a = x1 * c[i], b = x2 * s[i];
+                float e = x1 * s[i], f = x2 * c[i];
+                o[i] = a - b;
+                o[i + half] = e + f;
+            }
+        }
+    }
+}
+
 int orc_threads(int requested) {
 #ifdef _OPENMP
     if (requested > 0) return requested;
