@@ -27,6 +27,7 @@ ARCH = "gfx950"
 SOURCES = [
     "pkv_capi.cpp",
     "block_table.cpp",
+    "pkv_sched.cpp",
     "pkv_kvcopy.hip",
     "pkv_decode.hip",
     "pkv_prefill.hip",

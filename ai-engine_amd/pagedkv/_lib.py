@@ -59,6 +59,18 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_rope_check": (_I, [_P]),
     "pkv_decode_attention_rope": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I,
                                        ctypes.c_float, _P, _P, _P]),
+    "pkv_sched_last_error": (ctypes.c_char_p, []),
+    "pkv_sched_create": (_I, [ctypes.POINTER(_P), _P]),
+    "pkv_sched_destroy": (None, [_P]),
+    "pkv_sched_submit": (_I, [_P, _I, _I, ctypes.POINTER(ctypes.c_int64)]),
+    "pkv_sched_step": (_I, [_P, _P]),
+    "pkv_sched_complete": (_I, [_P, _P, _I, ctypes.c_char_p]),
+    "pkv_sched_poll": (_I, [_P, _P]),
+    "pkv_sched_fork": (_I, [_P, ctypes.c_int64, _I, ctypes.POINTER(ctypes.c_int64)]),
+    "pkv_sched_compact": (_I, [_P, _P, _P, _I, ctypes.POINTER(_I)]),
+    "pkv_sched_counts": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "pkv_sched_table": (_I, [_P, ctypes.c_int64, ctypes.POINTER(ctypes.POINTER(ctypes.c_uint32)),
+                             ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "pkv_pool_profile": (_I, [_P, _I]),
     "pkv_pool_profile_read": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "pkv_allocator_new": (_P, [_SZ, _SZ]),

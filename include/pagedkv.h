@@ -282,6 +282,94 @@ void pkv_table_free(pkv_table* t);
 size_t pkv_table_len(const pkv_table* t);
 const uint32_t* pkv_table_blocks(const pkv_table* t);
 
+/* ---- continuous-batching scheduler (run_loop / prefill block bookkeeping,
+ * crates/ai-engine-candle/src/paged/engine.rs:62-237).  Pure host code.
+ *
+ * The reference's engine thread interleaves scheduling with the model; here
+ * the scheduling is a step machine the caller drives around its own model
+ * forward:  pkv_sched_step() returns the plan of the next forward (rows, block
+ * tables, context lengths, slot mappings, copy-on-write copies), the caller
+ * runs the layers (pkv_copy_blocks, pkv_append / pkv_decode_attention /
+ * pkv_prefill_attention), samples one token per producing row and hands them
+ * to pkv_sched_complete().  What the reference sends on a request's channel
+ * (Ok(token) / Err(message) / channel closed) comes back as events.
+ *
+ * prefill_chunk == 0 reproduces run_loop exactly: an iteration first admits
+ * requests (engine.rs:77-100) and prefills each whole prompt (a plan of
+ * prefill rows), then runs the capacity/eviction pass and one decode step for
+ * every running sequence (engine.rs:102-178, a plan of decode rows).
+ * prefill_chunk > 0 is chunked prefill: each step carries the next chunk of
+ * every prompt in flight (at most step_token_budget prompt tokens) together
+ * with the decode rows.  Extensions with no reference counterpart: fork
+ * (shared blocks under reference counts; the first write to a shared block
+ * copies it, reported in the plan) and compaction (live blocks renumbered to
+ * [0, live) with the fewest moves, returned for pkv_compact). */
+typedef struct pkv_sched pkv_sched;
+
+typedef struct {
+  int max_num_seqs;      /* EngineConfig (engine.rs:30-36) */
+  int block_size;
+  int kv_cache_blocks;
+  int max_seq;
+  int32_t eos_token_id;
+  int prefill_chunk;     /* 0: whole prompts (the reference) */
+  int step_token_budget; /* chunked mode: prompt tokens per step (0: none) */
+} pkv_sched_config;
+
+#define PKV_EV_TOKEN 0    /* Ok(token) */
+#define PKV_EV_FINISHED 1 /* the sequence ended; its blocks are released */
+#define PKV_EV_ERROR 2    /* Err(message); the sequence ended */
+
+typedef struct {
+  int64_t seq;
+  int kind;
+  int32_t token;
+  char message[120];
+} pkv_sched_event;
+
+/* One forward's plan; the arrays stay valid until the next step, complete,
+ * fork or compact call.  Rows are the prefill rows, then the decode rows. */
+typedef struct {
+  int n_prefill, n_decode, n_rows, max_blocks, n_tokens, n_copies;
+  const int64_t* row_seq;       /* [n_rows] */
+  const int32_t* block_tables;  /* [n_rows][max_blocks], 0-padded */
+  const int32_t* context_lens;  /* [n_rows] keys attended after the writes */
+  const int32_t* cu_q_lens;     /* [n_prefill + 1] offsets of prompt tokens */
+  const int32_t* q_start;       /* [n_prefill] position of each chunk's first token */
+  const int32_t* slot_mapping;  /* [n_tokens] chunk tokens, then one per decode row */
+  const int32_t* positions;     /* [n_tokens] position of each new token */
+  const int8_t* produces;       /* [n_rows] 1 if the row yields a token */
+  const int32_t* copy_src;      /* [n_copies] copy before the writes */
+  const int32_t* copy_dst;
+} pkv_sched_plan;
+
+/* Message of the calling thread's last failed pkv_sched_* call. */
+const char* pkv_sched_last_error(void);
+int pkv_sched_create(pkv_sched** out, const pkv_sched_config* cfg);
+void pkv_sched_destroy(pkv_sched* s);
+/* GenRequest (engine.rs:13-18) without the channel; *id names its events. */
+int pkv_sched_submit(pkv_sched* s, int prompt_len, int max_tokens, int64_t* id);
+/* Plans the next forward; n_rows == 0 means nothing is runnable. */
+int pkv_sched_step(pkv_sched* s, pkv_sched_plan* plan);
+/* tokens: one per producing row, in row order (n = their count).  error !=
+ * NULL reports a failed forward: every row's sequence ends with Err (the
+ * reference's "prefill: ..." / "forward: ..." paths). */
+int pkv_sched_complete(pkv_sched* s, const int32_t* tokens, int n,
+                       const char* error);
+/* Next event; returns 1 and fills *ev, or 0 when there is none. */
+int pkv_sched_poll(pkv_sched* s, pkv_sched_event* ev);
+/* Fork a decoding sequence: the child shares its blocks (copy-on-write) and
+ * continues from the same position and pending token. */
+int pkv_sched_fork(pkv_sched* s, int64_t parent, int max_tokens, int64_t* child);
+/* Renumber live blocks to [0, live); src/dst (capacity cap) receive the moves
+ * for pkv_compact, *n their count. */
+int pkv_sched_compact(pkv_sched* s, int32_t* src, int32_t* dst, int cap, int* n);
+/* Introspection: counts, a sequence's table (NULL if it is not live). */
+int pkv_sched_counts(const pkv_sched* s, int* running, int* waiting,
+                     int* free_blocks);
+int pkv_sched_table(const pkv_sched* s, int64_t seq, const uint32_t** blocks,
+                    int* n_blocks, int* pos);
+
 #ifdef __cplusplus
 }
 #endif
