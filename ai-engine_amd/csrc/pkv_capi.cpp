@@ -409,9 +409,6 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
   if (n_chains <= 0) return PKV_OK;
   DeviceGuard dg(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // The plan goes to a device buffer the pool keeps between calls (grown
-  // when a larger plan comes); the call returns once the moves are done, so
-  // the host plan can go out of scope.
   size_t ob = ops.size() * sizeof(int32_t), sb = starts.size() * sizeof(int32_t);
   // The plan buffers were sized at pool creation for the largest plan (see
   // plan_capacity_bytes); the call ends with a stream sync, so they are free.
