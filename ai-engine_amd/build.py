@@ -32,6 +32,7 @@ SOURCES = [
     "pkv_decode.hip",
     "pkv_prefill.hip",
     "pkv_rope.hip",
+    "pkv_sample.hip",
 ]
 
 # Packed-FP32 instructions stay off (the compiler would otherwise form

@@ -688,6 +688,31 @@ int pkv_rope_check(pkv_rope* r) {
   return PKV_OK;
 }
 
+float pkv_sample_draw(uint64_t seed) { return pkv::sample_draw(seed); }
+
+int pkv_sample(const void* logits, int dtype, long long row_stride, int batch, int vocab,
+               const float* temperatures, int top_k, float top_p, uint64_t seed,
+               int32_t* tokens, void* stream) {
+  if (batch < 0 || vocab < 0 || vocab > (1 << 24))
+    return fail(nullptr, PKV_ERR_INVALID, "sample: batch %d, vocab %d (0 .. 2^24)", batch, vocab);
+  if (batch == 0) return PKV_OK;
+  if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)
+    return fail(nullptr, PKV_ERR_INVALID, "sample: dtype %d", dtype);
+  if (!tokens || (vocab > 0 && !logits))
+    return fail(nullptr, PKV_ERR_INVALID, "sample: NULL logits or tokens");
+  if (batch > 1 && row_stride < vocab)
+    return fail(nullptr, PKV_ERR_INVALID, "sample: row_stride %lld < vocab %d", row_stride, vocab);
+  if (reinterpret_cast<uintptr_t>(logits) % pkv::dtype_bytes(dtype))
+    return fail(nullptr, PKV_ERR_INVALID, "sample: logits not aligned to the element size");
+  if (top_k < 0)
+    return fail(nullptr, PKV_ERR_INVALID, "sample: top_k %d < 0 (0 is None)", top_k);
+  hipError_t e = pkv::launch_sample(logits, dtype, row_stride, batch, vocab, temperatures,
+                                    top_k, top_p, pkv::sample_draw(seed), tokens,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(nullptr, e, "sample launch");
+  return PKV_OK;
+}
+
 int pkv_pool_check(pkv_pool* p) {
   CHECK_POOL(p);
   DeviceGuard dg(p->device);

@@ -72,6 +72,13 @@ namespace pkv {
 
 inline size_t dtype_bytes(int dt) { return dt == PKV_F32 ? 4 : 2; }
 
+// Token selection (pkv_sample.hip): the fixed draw r of a seed, and the
+// launcher of the per-row argmax / sample kernel.
+float sample_draw(uint64_t seed);
+hipError_t launch_sample(const void* logits, int dtype, long long row_stride, int batch,
+                         int vocab, const float* temperatures, int top_k, float top_p,
+                         float r, int32_t* tokens, hipStream_t stream);
+
 // Launchers (defined in the .hip files).  They validate nothing that the
 // C-ABI layer already validated, return hipError_t and enqueue on `stream`.
 hipError_t launch_append(const pkv_pool* p, int layer, const void* k,

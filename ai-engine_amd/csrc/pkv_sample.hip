@@ -1,0 +1,497 @@
+// pkv_sample.hip -- token selection on the device: argmax and sample() of
+// crates/ai-engine-runtime/src/sample.rs:12-55, which the paged engine runs
+// on every logits row it copies to the host (engine.rs:145-162, 226) with
+// SamplingConfig {temperature of the request, top_p: None, top_k: None,
+// seed: 42} (engine.rs:58-60).  Selecting on the device leaves one int32
+// per row to copy back instead of the whole row.
+//
+// Greedy rows (temperature 0, or at most one logit) take the first maximum;
+// a NaN is never chosen and a row with no value above -inf gives 0
+// (argmax's fold from (0, -inf), sample.rs:50-55).
+//
+// Other rows: the reference sorts y = logit / temperature (stable,
+// descending), keeps the first top_k, takes p = softmax, keeps the shortest
+// prefix whose cumulative p reaches top_p, renormalises, and returns the
+// first token at which the cumulative p reaches r, the first f32 of
+// StdRng::seed_from_u64(seed) -- one fixed value for a fixed seed.  All of
+// that only needs the sorted position where a running mass crosses a
+// threshold, which a radix selection finds without sorting: y maps to an
+// order-preserving 32-bit key, and three passes over the row (key bits
+// 31..20, 19..10, 9..0) histogram the mass of the tokens that share the
+// digits chosen so far, walking the buckets from the largest y down until
+// the threshold is reached.  Masses are exp(y - max y) in 2^-40 fixed point,
+// so the LDS histograms add integers: the sums are exact and the result does
+// not depend on the order of the atomics.  Tokens with equal y are ordered
+// by index, as the stable sort leaves them.  The selected token equals the
+// reference's except where the reference's own f32 running sums land within
+// their rounding (~1e-6) of r or top_p.
+//
+// One workgroup of 1024 threads per row.  The row is read once per pass --
+// max; the first digit, whose histogram also gives the total mass and is
+// shared by the top_p and r selections; two more digits per selection (the
+// last one records each bucket's size and smallest index, which settles a
+// tie without another pass unless several tied tokens are needed; three more
+// passes for top_k) -- and stays in L2 / the Infinity Cache between passes.
+#include <climits>
+#include <cmath>
+
+#include "pkv_device.h"
+#include "pkv_internal.h"
+
+namespace pkv {
+
+float sample_draw(uint64_t seed) {
+  // rand_core 0.6.4 SeedableRng::seed_from_u64: a PCG32 stream fills the
+  // 32-byte ChaCha key, eight little-endian words.
+  uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
+  uint64_t st = seed;
+  for (int i = 0; i < 8; ++i) {
+    st = st * 6364136223846793005ull + 11634580027462260723ull;
+    const uint32_t xs = (uint32_t)(((st >> 18) ^ st) >> 27);
+    const uint32_t rot = (uint32_t)(st >> 59);
+    s[4 + i] = (xs >> rot) | (xs << ((32u - rot) & 31u));
+  }
+  // words 12..15: block counter 0 and stream 0 (rand_chacha 0.3.1)
+  uint32_t x[16];
+  for (int i = 0; i < 16; ++i) x[i] = s[i];
+  auto rotl = [](uint32_t v, int n) { return (v << n) | (v >> (32 - n)); };
+  auto qr = [&](int a, int b, int c, int d) {
+    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 16);
+    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 12);
+    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 8);
+    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 7);
+  };
+  for (int r = 0; r < 12; r += 2) {  // StdRng = ChaCha12
+    qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15);
+    qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14);
+  }
+  const uint32_t w0 = x[0] + s[0];
+  // rand 0.8 Standard for f32: the top 24 bits times 2^-24, in [0, 1)
+  return (float)(w0 >> 8) * (1.0f / 16777216.0f);
+}
+
+namespace {
+
+constexpr int kST = 1024;                 // threads per row
+constexpr int kSW = kST / 64;             // waves per row
+constexpr int kB1 = 4096;                 // first digit: key bits 31..20
+constexpr int kB2 = 1024;                 // second / third: bits 19..10, 9..0
+constexpr float kFix = 1099511627776.0f;  // 2^40
+constexpr unsigned long long kOne = 1ull << 40;
+
+struct SampleArgs {
+  const char* logits;
+  long long stride_bytes;
+  int vocab;
+  const float* temps;
+  int top_k;
+  float top_p;
+  float r;
+  int32_t* tokens;
+};
+
+struct SampleSmem {
+  unsigned long long h1[kB1];  // first-digit histogram, kept between selections
+  unsigned long long h[kB2];   // histogram of the later digits
+  unsigned int cnt[kB2];       // last digit: tokens per bucket
+  int minidx[kB2];             // last digit: smallest index per bucket
+  unsigned long long red_u[kSW];
+  float red_f[kSW];
+  int red_i[kSW];
+  unsigned int sel_bucket;
+  unsigned long long sel_rem;
+  int found;
+};
+
+template <int DT>
+__device__ __forceinline__ float logit(const char* row, int i) {
+  if constexpr (DT == PKV_F32) {
+    return reinterpret_cast<const float*>(row)[i];
+  } else if constexpr (DT == PKV_BF16) {
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[i] << 16);
+  } else {
+    return (float)reinterpret_cast<const _Float16*>(row)[i];
+  }
+}
+
+// Calls f(i, logit) for this thread's elements of the row, in increasing i:
+// 16-byte vectors (VEC: the row is 16-byte aligned), then the tail.
+template <int DT, bool VEC, class F>
+__device__ __forceinline__ void for_each(const char* row, int V, F&& f) {
+  int done = 0;
+  if constexpr (VEC) {
+    constexpr int E = DT == PKV_F32 ? 4 : 8;
+    const int nv = V / E;
+    for (int v = threadIdx.x; v < nv; v += kST) {
+      const u32x4 w = ld16(row + (size_t)v * 16);
+      if constexpr (DT == PKV_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f(v * 4 + j, __uint_as_float(w[j]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
+          const float hi = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
+          f(v * 8 + 2 * j, lo);
+          f(v * 8 + 2 * j + 1, hi);
+        }
+      }
+    }
+    done = nv * E;
+  }
+  for (int i = done + (int)threadIdx.x; i < V; i += kST) f(i, logit<DT>(row, i));
+}
+
+// Larger y -> larger key; -0.0 and +0.0 compare equal, as partial_cmp has them.
+__device__ __forceinline__ uint32_t order_key(float y) {
+  uint32_t b = __float_as_uint(y);
+  if (y == 0.0f) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// exp(d) for d = y - max y <= 0, in 2^-40 units.
+__device__ __forceinline__ unsigned long long mass_of(float d) {
+  const float e = expf(d);
+  if (!(e > 0.0f)) return 0ull;
+  if (e >= 1.0f) return kOne;
+  return (unsigned long long)(e * kFix);
+}
+
+__device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, int d) {
+  const int lo = __shfl_up((int)(uint32_t)v, d, 64);
+  const int hi = __shfl_up((int)(uint32_t)(v >> 32), d, 64);
+  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+  const int lo = __shfl_xor((int)(uint32_t)v, m, 64);
+  const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ float block_max(SampleSmem& sm, float v) {
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) sm.red_f[wv] = v;
+  __syncthreads();
+  float r = sm.red_f[0];
+  for (int w = 1; w < kSW; ++w) r = fmaxf(r, sm.red_f[w]);
+  __syncthreads();
+  return r;
+}
+
+__device__ unsigned long long block_sum_u64(SampleSmem& sm, unsigned long long v) {
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_u64(v, m);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) sm.red_u[wv] = v;
+  __syncthreads();
+  unsigned long long r = 0;
+  for (int w = 0; w < kSW; ++w) r += sm.red_u[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ int block_min_i(SampleSmem& sm, int v) {
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, 64));
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) sm.red_i[wv] = v;
+  __syncthreads();
+  int r = sm.red_i[0];
+  for (int w = 1; w < kSW; ++w) r = min(r, sm.red_i[w]);
+  __syncthreads();
+  return r;
+}
+
+// Wave 0 walks the histogram hist[0..nb) from the top bucket down and
+// records in sm.sel_bucket the first bucket where the running total reaches
+// rem, and in sm.sel_rem what is still needed inside it.  Lane L sums the
+// segment of buckets nb-1-L*per down to nb-(L+1)*per (starting at a
+// lane-dependent offset so that the lanes hit different LDS banks), a wave
+// prefix scan finds the segment, and its lane walks it in order.  The
+// histograms always hold at least rem below the digits chosen so far; if
+// that ever failed, the smallest non-empty bucket is taken so that the row
+// still ends with a token.  Call from all threads; ends with a barrier.
+__device__ void scan_buckets(SampleSmem& sm, const unsigned long long* hist, int nb,
+                             unsigned long long rem) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (wv == 0) {
+    const int per = nb / 64;
+    const int hi = nb - 1 - lane * per;
+    unsigned long long seg = 0;
+    for (int j = 0; j < per; ++j) seg += hist[hi - ((j + lane) & (per - 1))];
+    unsigned long long incl = seg;
+    for (int d = 1; d < 64; d <<= 1) {
+      const unsigned long long o = shfl_up_u64(incl, d);
+      if (lane >= d) incl += o;
+    }
+    const unsigned long long reach = __ballot(incl >= rem);
+    const unsigned long long nonempty = __ballot(seg != 0ull);
+    const int fl = reach ? __builtin_ctzll(reach)
+                         : (nonempty ? 63 - __builtin_clzll(nonempty) : 0);
+    if (lane == fl) {
+      unsigned long long acc = incl - seg;
+      int chosen = -1, last_nonempty = hi;
+      for (int j = 0; j < per; ++j) {
+        const unsigned long long h = hist[hi - j];
+        if (h) last_nonempty = hi - j;
+        if (h && acc + h >= rem) {
+          chosen = hi - j;
+          break;
+        }
+        acc += h;
+      }
+      unsigned long long r2 = rem - acc;
+      if (chosen < 0) {
+        chosen = last_nonempty;
+        r2 = hist[chosen] ? hist[chosen] : 1ull;
+      }
+      sm.sel_bucket = (uint32_t)chosen;
+      sm.sel_rem = r2;
+    }
+  }
+  __syncthreads();
+}
+
+// Per-row context of the temperature path.
+template <int DT, bool VEC>
+struct Row {
+  const char* x;
+  int V;
+  float T, ymax;
+  bool has_k;
+  uint32_t kkey;  // top_k: key of the k-th largest value
+  int kcut;       // top_k: last index kept among the tokens with that key
+  __device__ bool kept(int i, uint32_t key) const {
+    return !has_k || key > kkey || (key == kkey && i <= kcut);
+  }
+};
+
+struct Sel {
+  uint32_t key;             // the selected key (all 32 bits)
+  unsigned long long rem;   // what is still needed inside its tie group
+  unsigned long long hist;  // the tie group's total (mass, or count)
+  unsigned long long cnt;   // the tie group's size
+  int minidx;               // its smallest index
+};
+
+// Second and third digits of a selection whose first-digit histogram is
+// sm.h1: COUNT counts every token, otherwise kept tokens' mass.
+template <bool COUNT, int DT, bool VEC>
+__device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long long target) {
+  const int tid = threadIdx.x;
+  scan_buckets(sm, sm.h1, kB1, target);
+  uint32_t prefix = sm.sel_bucket << 20;
+  unsigned long long rem = sm.sel_rem;
+  Sel out{};
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 10 : 0;
+    const uint32_t pmask = pass == 0 ? 0xfff00000u : 0xfffffc00u;
+    const bool last = pass == 1;
+    __syncthreads();  // every thread has read sm.sel_* before it is reused
+    for (int b = tid; b < kB2; b += kST) {
+      sm.h[b] = 0ull;
+      sm.cnt[b] = 0u;
+      sm.minidx[b] = INT_MAX;
+    }
+    __syncthreads();
+    for_each<DT, VEC>(rw.x, rw.V, [&](int i, float x) {
+      const float y = x / rw.T;
+      const uint32_t key = order_key(y);
+      if ((key & pmask) != prefix) return;
+      const uint32_t b = (key >> shift) & (uint32_t)(kB2 - 1);
+      if constexpr (COUNT) {
+        atomicAdd(&sm.h[b], 1ull);
+      } else {
+        if (!rw.kept(i, key)) return;
+        const unsigned long long m = mass_of(y - rw.ymax);
+        if (m == 0ull) return;
+        atomicAdd(&sm.h[b], m);
+      }
+      if (last) {
+        atomicAdd(&sm.cnt[b], 1u);
+        atomicMin(&sm.minidx[b], i);
+      }
+    });
+    __syncthreads();
+    scan_buckets(sm, sm.h, kB2, rem);
+    const uint32_t b = sm.sel_bucket;
+    rem = sm.sel_rem;
+    prefix |= b << shift;
+    if (last) {
+      out.hist = sm.h[b];
+      out.cnt = sm.cnt[b];
+      out.minidx = sm.minidx[b];
+    }
+  }
+  __syncthreads();
+  out.key = prefix;
+  out.rem = rem;
+  return out;
+}
+
+// Index of the n-th (1-based) token, in index order, whose key is `key` and
+// that the top_k filter keeps (FILTER); V - 1 if there is none.  Only used
+// when more than one token of a tie group is needed.
+template <bool FILTER, int DT, bool VEC>
+__device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
+                        unsigned long long n) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) sm.found = rw.V - 1;
+  __syncthreads();
+  unsigned long long base = 0;
+  for (int c = 0; c < rw.V; c += kST) {
+    const int i = c + tid;
+    bool f = false;
+    if (i < rw.V) {
+      const uint32_t k = order_key(logit<DT>(rw.x, i) / rw.T);
+      f = k == key && (!FILTER || rw.kept(i, k));
+    }
+    const unsigned long long bal = __ballot(f);
+    const int rank = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) sm.red_i[wv] = __popcll(bal);
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int w = 0; w < kSW; ++w) {
+      const int cw = sm.red_i[w];
+      off += w < wv ? cw : 0;
+      tot += cw;
+    }
+    if (f && base + (unsigned long long)(off + rank) == n - 1ull) sm.found = i;
+    __syncthreads();
+    base += (unsigned long long)tot;
+    if (base >= n) break;
+  }
+  const int r = sm.found;
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ unsigned long long clamp_target(double t, unsigned long long hi) {
+  unsigned long long v = t >= (double)hi ? hi : (unsigned long long)ceil(t > 0.0 ? t : 0.0);
+  return v < 1ull ? 1ull : (v > hi ? hi : v);
+}
+
+// How many tokens of the selected tie group the remaining mass needs.
+__device__ __forceinline__ unsigned long long ties_needed(const Sel& s) {
+  const unsigned long long per = s.cnt ? s.hist / s.cnt : s.hist;
+  unsigned long long n = per ? (s.rem + per - 1ull) / per : 1ull;
+  if (n > s.cnt) n = s.cnt;
+  return n < 1ull ? 1ull : n;
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+
+  if (T == 0.0f || V <= 1) {
+    // argmax: strictly greater values only, so the first maximum wins
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for_each<DT, VEC>(x, V, [&](int i, float v) {
+      if (v > bv) {
+        bv = v;
+        bi = i;
+      }
+    });
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, 64);
+      const int oi = __shfl_xor(bi, m, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      sm.red_f[wv] = bv;
+      sm.red_i[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < kSW; ++w) {
+        const float ov = sm.red_f[w];
+        const int oi = sm.red_i[w];
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    }
+    return;
+  }
+
+  Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
+  float ym = -INFINITY;
+  for_each<DT, VEC>(x, V, [&](int, float v) { ym = fmaxf(ym, v / T); });
+  rw.ymax = block_max(sm, ym);
+
+  if (a.top_k > 0 && a.top_k < V) {
+    // the k-th largest key, and how many of its ties the first k include
+    for (int b = tid; b < kB1; b += kST) sm.h1[b] = 0ull;
+    __syncthreads();
+    for_each<DT, VEC>(x, V, [&](int, float v) { atomicAdd(&sm.h1[order_key(v / T) >> 20], 1ull); });
+    __syncthreads();
+    const Sel s = select_low<true>(sm, rw, (unsigned long long)a.top_k);
+    rw.kkey = s.key;
+    rw.kcut = s.rem >= s.cnt ? V : (s.rem <= 1ull ? s.minidx : nth_tied<false>(sm, rw, s.key, s.rem));
+    rw.has_k = true;
+  }
+
+  // first digit of the mass histogram; its buckets add up to the total mass
+  for (int b = tid; b < kB1; b += kST) sm.h1[b] = 0ull;
+  __syncthreads();
+  for_each<DT, VEC>(x, V, [&](int i, float v) {
+    const float y = v / T;
+    const uint32_t key = order_key(y);
+    if (!rw.kept(i, key)) return;
+    const unsigned long long m = mass_of(y - rw.ymax);
+    if (m) atomicAdd(&sm.h1[key >> 20], m);
+  });
+  __syncthreads();
+  unsigned long long part = 0;
+  for (int b = tid; b < kB1; b += kST) part += sm.h1[b];
+  unsigned long long total = block_sum_u64(sm, part);
+
+  if (a.top_p < 1.0f) {
+    // the shortest sorted prefix whose mass reaches top_p of the total
+    const unsigned long long tp = clamp_target((double)a.top_p * (double)total, total);
+    const Sel s = select_low<false>(sm, rw, tp);
+    const unsigned long long per = s.cnt ? s.hist / s.cnt : s.hist;
+    total = tp - s.rem + ties_needed(s) * per;
+  }
+  const unsigned long long tr = clamp_target((double)a.r * (double)total, total);
+  const Sel s = select_low<false>(sm, rw, tr);
+  const unsigned long long n = ties_needed(s);
+  const int tok = n == 1ull ? (s.minidx == INT_MAX ? V - 1 : s.minidx)
+                            : nth_tied<true>(sm, rw, s.key, n);
+  if (tid == 0) a.tokens[row] = tok;
+}
+
+}  // namespace
+
+hipError_t launch_sample(const void* logits, int dtype, long long row_stride, int batch,
+                         int vocab, const float* temperatures, int top_k, float top_p,
+                         float r, int32_t* tokens, hipStream_t stream) {
+  const long long sb = row_stride * (long long)dtype_bytes(dtype);
+  SampleArgs a{static_cast<const char*>(logits), sb, vocab, temperatures, top_k, top_p, r,
+               tokens};
+  // 16-byte loads when every row starts on a 16-byte boundary
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (batch == 1 || sb % 16 == 0);
+  if (dtype == PKV_F32) {
+    if (vec) sample_kernel<PKV_F32, true><<<batch, kST, 0, stream>>>(a);
+    else sample_kernel<PKV_F32, false><<<batch, kST, 0, stream>>>(a);
+  } else if (dtype == PKV_BF16) {
+    if (vec) sample_kernel<PKV_BF16, true><<<batch, kST, 0, stream>>>(a);
+    else sample_kernel<PKV_BF16, false><<<batch, kST, 0, stream>>>(a);
+  } else {
+    if (vec) sample_kernel<PKV_F16, true><<<batch, kST, 0, stream>>>(a);
+    else sample_kernel<PKV_F16, false><<<batch, kST, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pkv

@@ -148,6 +148,38 @@ def rope_tables_host(rope_dim: int, freq_base: float, max_seq: int):
     return c, s
 
 
+def sample_draw(seed: int = 42) -> float:
+    """StdRng::seed_from_u64(seed).gen::<f32>() (sample.rs:41-42), the fixed
+    draw that sample() compares the cumulative probabilities with."""
+    return float(lib().pkv_sample_draw(seed))
+
+
+def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | None = None,
+           seed: int = 42, out=None, stream=None):
+    """Token per logits row on the device: argmax / sample() of sample.rs:12-55.
+    logits: (batch, vocab) f32/f16/bf16 with unit stride along vocab;
+    temperatures: (batch,) float32 on the device (None: all greedy).
+    Returns (batch,) int32 on the device."""
+    import torch
+    if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
+        raise ValueError("logits must be (batch, vocab) with unit stride along vocab")
+    B, V = logits.shape
+    dev = logits.device
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=dev)
+    t = None
+    if temperatures is not None:
+        t = torch.as_tensor(temperatures, dtype=torch.float32).to(dev).contiguous()
+        if t.numel() != B:
+            raise ValueError("temperatures must have one value per row")
+    check(lib().pkv_sample(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
+                           logits.stride(0) if B > 1 else V, B, V,
+                           _dev_ptr(t) if t is not None else None, top_k or 0,
+                           1.0 if top_p is None else float(top_p), seed, _dev_ptr(out),
+                           _stream_ptr(stream)), None)
+    return out
+
+
 class Rope:
     """The reference's Rope (rope.rs:6-33): cos/sin tables in device memory;
     apply() is apply_rope (rope.rs:38-42) with per-token positions."""

@@ -241,6 +241,31 @@ int pkv_decode_attention_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
                               const void* k_new, const void* v_new,
                               void* stream);
 
+/* ---- token selection (crates/ai-engine-runtime/src/sample.rs:12-55) --------
+ * The engine copies each logits row to the host and samples it with
+ * SamplingConfig {temperature of the request, top_p: None, top_k: None,
+ * seed: 42} (crates/ai-engine-candle/src/paged/engine.rs:58-60,145-162,226);
+ * this selects on the device and leaves one int32 per row.
+ *  logits: device, row b at logits + b * row_stride elements, `vocab` values
+ *  each, dtype PKV_F32 / PKV_F16 / PKV_BF16.  temperatures: device f32
+ *  [batch], or NULL (every row greedy).  tokens: device int32 [batch].
+ * Row b is argmax (first maximum; NaN never chosen; 0 when no value exceeds
+ * -inf) when temperatures[b] == 0 or vocab <= 1.  Otherwise sample(): y =
+ * logit / temperature sorted descending (ties in index order), the first
+ * top_k kept (top_k == 0: None), p = softmax over them, the shortest prefix
+ * whose cumulative p reaches top_p kept and renormalised (top_p >= 1 or NaN:
+ * None), and the first token at which the cumulative p reaches r =
+ * StdRng::seed_from_u64(seed).gen::<f32>() -- the same r on every call, as
+ * in the reference.  The token equals the reference's except where its f32
+ * running sums fall within their rounding of r or top_p.  Temperatures must
+ * be finite and logits of sampled rows free of NaN (the reference's sort is
+ * unspecified there).  Runs on the calling thread's current device. */
+int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
+               int vocab, const float* temperatures, int top_k, float top_p,
+               uint64_t seed, int32_t* tokens, void* stream);
+/* StdRng::seed_from_u64(seed).gen::<f32>() (sample.rs:41-42; host only). */
+float pkv_sample_draw(uint64_t seed);
+
 /* Kernel timing (instrumentation; no reference counterpart).  While enabled,
  * every pkv_decode_attention, pkv_prefill_attention, pkv_copy_blocks and
  * pkv_compact call records HIP events, owned by the pool, on its stream right

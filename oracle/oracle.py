@@ -79,6 +79,19 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_rope_table.restype = None
     L.orc_rope_apply.argtypes = [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P]
     L.orc_rope_apply.restype = None
+    L.orc_pcg32_output.argtypes = [ctypes.c_uint64]
+    L.orc_pcg32_output.restype = ctypes.c_uint32
+    L.orc_chacha_block.argtypes = [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _P]
+    L.orc_chacha_block.restype = None
+    L.orc_seed_from_u64.argtypes = [ctypes.c_uint64, _P]
+    L.orc_seed_from_u64.restype = None
+    L.orc_sample_draw.argtypes = [ctypes.c_uint64]
+    L.orc_sample_draw.restype = ctypes.c_float
+    L.orc_argmax.argtypes = [_P, _SZ]
+    L.orc_argmax.restype = ctypes.c_int64
+    L.orc_sample.argtypes = [_P, _SZ, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                             ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    L.orc_sample.restype = ctypes.c_int64
     L.orc_threads.argtypes = [ctypes.c_int]
     L.orc_threads.restype = ctypes.c_int
 
@@ -309,3 +322,47 @@ def rope_apply(x, cos_t, sin_t, positions) -> np.ndarray:
 
 def threads(requested: int = 0) -> int:
     return int(lib().orc_threads(int(requested)))
+
+
+# ---------------------------------------------------------------------------
+# token selection (crates/ai-engine-runtime/src/sample.rs:12-55)
+# ---------------------------------------------------------------------------
+def pcg32_output(state: int) -> int:
+    return int(lib().orc_pcg32_output(state))
+
+
+def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    assert k.size == 8
+    out = np.zeros(16, np.uint32)
+    lib().orc_chacha_block(_p(k), counter, stream, rounds, _p(out))
+    return out
+
+
+def seed_from_u64(seed: int) -> np.ndarray:
+    out = np.zeros(8, np.uint32)
+    lib().orc_seed_from_u64(seed, _p(out))
+    return out
+
+
+def sample_draw(seed: int) -> float:
+    """StdRng::seed_from_u64(seed).gen::<f32>() (sample.rs:41-42)."""
+    return float(lib().orc_sample_draw(seed))
+
+
+def argmax(logits) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(lib().orc_argmax(_p(x), x.size))
+
+
+def sample(logits, temperature: float, top_k: int | None = None, top_p: float | None = None,
+           seed: int = 42, precise: bool = False) -> tuple[int, float]:
+    """sample() of sample.rs:12-48 -> (token, margin of the decisive sums).
+    precise=False: the reference's f32 arithmetic; True: the same steps with
+    exp, normalisation and running sums in double."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    m = ctypes.c_double()
+    tok = lib().orc_sample(_p(x) if x.size else None, x.size, temperature, top_k or 0,
+                           0 if top_p is None else 1, 0.0 if top_p is None else top_p, seed,
+                           1 if precise else 0, ctypes.byref(m))
+    return int(tok), float(m.value)

@@ -40,6 +40,18 @@
  *   orc_rope_apply        - identity at position 0, pairwise norm
  *                           preservation, rotation composition, relative-
  *                           position invariance of q.k, float64 rotation.
+ *   orc_sample/argmax     - the reference's four KATs (ai-engine-runtime
+ *                           tests/sample.rs), closed forms (uniform logits
+ *                           pick floor(r * V), two-token logistic, top-k and
+ *                           top-p renormalisation), first-maximum and NaN
+ *                           rules of argmax.
+ *   orc_chacha_block      - the public ChaCha20 and ChaCha12 all-zero key
+ *                           test vectors; orc_pcg32_output - the pcg32
+ *                           reference demo sequence (initstate 42, initseq
+ *                           54).  orc_seed_from_u64's wiring (increment,
+ *                           advance before output) and the f32 conversion
+ *                           follow the crates' published source and are
+ *                           otherwise unpinned.
  */
 #include <math.h>
 #include <stdint.h>
@@ -658,4 +670,173 @@ int orc_threads(int requested) {
     (void)requested;
     return 1;
 #endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* token selection: sample() and argmax() of                                */
+/* crates/ai-engine-runtime/src/sample.rs:12-55, which the paged engine      */
+/* calls per row with SamplingConfig {temperature, top_p: None, top_k: None, */
+/* seed: 42} (crates/ai-engine-candle/src/paged/engine.rs:58-60,162,226).    */
+/*                                                                           */
+/* The draw r comes from rand 0.8.6 (Cargo.lock:5080-5083):                  */
+/* StdRng::seed_from_u64(seed).gen::<f32>().  StdRng is ChaCha12 (rand_chacha */
+/* 0.3.1); seed_from_u64 is rand_core 0.6.4's default: a PCG32 stream        */
+/* (multiplier 6364136223846793005, increment 11634580027462260723, state    */
+/* advanced before each output, XSH-RR output) fills the 32-byte key, eight  */
+/* little-endian words; the block counter and stream start at 0; gen::<f32>  */
+/* takes the first output word w and returns (w >> 8) * 2^-24.  None of      */
+/* these crates is in the reference tree; their published algorithms are    */
+/* restated here.                                                            */
+/* ------------------------------------------------------------------------ */
+static inline uint32_t orc_rotl32(uint32_t x, int n) { return (x << n) | (x >> (32 - n)); }
+
+/* PCG32 XSH-RR output of a 64-bit state. */
+uint32_t orc_pcg32_output(uint64_t state) {
+    uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+    uint32_t rot = (uint32_t)(state >> 59);
+    return (xs >> rot) | (xs << ((32u - rot) & 31u));
+}
+
+/* One ChaCha block: constants, 8 key words, 64-bit counter, 64-bit stream. */
+void orc_chacha_block(const uint32_t* key, uint64_t counter, uint64_t stream, int rounds,
+                      uint32_t* out) {
+    uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
+    for (int i = 0; i < 8; ++i) s[4 + i] = key[i];
+    s[12] = (uint32_t)counter;
+    s[13] = (uint32_t)(counter >> 32);
+    s[14] = (uint32_t)stream;
+    s[15] = (uint32_t)(stream >> 32);
+    uint32_t x[16];
+    memcpy(x, s, sizeof x);
+#define ORC_QR(a, b, c, d)                                   \
+    x[a] += x[b]; x[d] = orc_rotl32(x[d] ^ x[a], 16);         \
+    x[c] += x[d]; x[b] = orc_rotl32(x[b] ^ x[c], 12);         \
+    x[a] += x[b]; x[d] = orc_rotl32(x[d] ^ x[a], 8);          \
+    x[c] += x[d]; x[b] = orc_rotl32(x[b] ^ x[c], 7);
+    for (int r = 0; r < rounds; r += 2) {
+        ORC_QR(0, 4, 8, 12) ORC_QR(1, 5, 9, 13) ORC_QR(2, 6, 10, 14) ORC_QR(3, 7, 11, 15)
+        ORC_QR(0, 5, 10, 15) ORC_QR(1, 6, 11, 12) ORC_QR(2, 7, 8, 13) ORC_QR(3, 4, 9, 14)
+    }
+#undef ORC_QR
+    for (int i = 0; i < 16; ++i) out[i] = x[i] + s[i];
+}
+
+/* rand_core 0.6.4 SeedableRng::seed_from_u64 for a 32-byte seed. */
+void orc_seed_from_u64(uint64_t state, uint32_t* key) {
+    for (int i = 0; i < 8; ++i) {
+        state = state * 6364136223846793005ull + 11634580027462260723ull;
+        key[i] = orc_pcg32_output(state);
+    }
+}
+
+/* StdRng::seed_from_u64(seed).gen::<f32>() (sample.rs:41-42). */
+float orc_sample_draw(uint64_t seed) {
+    uint32_t key[8], blk[16];
+    orc_seed_from_u64(seed, key);
+    orc_chacha_block(key, 0, 0, 12, blk);
+    return (float)(blk[0] >> 8) * (1.0f / 16777216.0f);
+}
+
+/* argmax (sample.rs:50-55): fold from (0, -inf) keeping strictly greater
+ * values, so the first maximum wins and NaN never does. */
+int64_t orc_argmax(const float* x, size_t n) {
+    size_t bi = 0;
+    float bv = -INFINITY;
+    for (size_t i = 0; i < n; ++i)
+        if (x[i] > bv) { bi = i; bv = x[i]; }
+    return (int64_t)bi;
+}
+
+static const float* orc_sort_keys;
+/* sort_by(b.partial_cmp(a)) is a stable descending sort: equal values keep
+ * index order, and -0.0 equals +0.0 (NaN inputs are not supported). */
+static int orc_desc_cmp(const void* a, const void* b) {
+    size_t i = *(const size_t*)a, j = *(const size_t*)b;
+    float x = orc_sort_keys[i], y = orc_sort_keys[j];
+    if (x > y) return -1;
+    if (x < y) return 1;
+    return i < j ? -1 : (i > j ? 1 : 0);
+}
+
+/* sample (sample.rs:12-48).  precise = 0: the reference's arithmetic, f32
+ * throughout with libm expf and running sums in the sorted order.
+ * precise = 1: the same steps on the same f32 values y and y - max, with
+ * exp, the normalisation and the running sums in double -- the value the
+ * f32 version approximates, used to separate the reference's rounding from
+ * a wrong selection.  top_k <= 0 is None; has_top_p = 0 is None.  *margin
+ * gets the distance of the decisive running sums from their thresholds (r,
+ * and top_p when it cuts), in the mode's own arithmetic (0 when the
+ * fallback to the last token is taken). */
+int64_t orc_sample(const float* logits, size_t n, float temperature, int top_k, int has_top_p,
+                   float top_p, uint64_t seed, int precise, double* margin) {
+    if (margin) *margin = INFINITY;
+    if (temperature == 0.0f || n <= 1) return orc_argmax(logits, n);
+    float* y = malloc(n * sizeof(float));
+    size_t* idx = malloc(n * sizeof(size_t));
+    double* p = malloc(n * sizeof(double));
+    for (size_t i = 0; i < n; ++i) { y[i] = logits[i] / temperature; idx[i] = i; }
+    orc_sort_keys = y;
+    qsort(idx, n, sizeof(size_t), orc_desc_cmp);
+    size_t len = n;
+    if (top_k > 0 && (size_t)top_k < len) len = (size_t)top_k;
+    float max_x = y[idx[0]];
+    /* f32 mode keeps every intermediate in float (each value rounded to
+     * float on assignment); precise mode keeps doubles */
+    double sum = 0.0;
+    float sum32 = 0.0f;
+    for (size_t i = 0; i < len; ++i) {
+        float d = y[idx[i]] - max_x;
+        if (precise) { p[i] = exp((double)d); sum += p[i]; }
+        else { float e = expf(d); p[i] = e; sum32 += e; }
+    }
+    for (size_t i = 0; i < len; ++i) {
+        if (precise) p[i] /= sum;
+        else p[i] = (float)((float)p[i] / sum32);
+    }
+    double m = INFINITY;
+    if (has_top_p) {
+        double cum = 0.0;
+        float cum32 = 0.0f;
+        size_t cutoff = len;
+        for (size_t i = 0; i < len; ++i) {
+            double prev, now;
+            if (precise) { prev = cum; cum += p[i]; now = cum; }
+            else { prev = cum32; cum32 += (float)p[i]; now = cum32; }
+            if (precise ? now >= (double)top_p : cum32 >= top_p) {
+                cutoff = i + 1;
+                double d1 = (double)top_p - prev, d2 = now - top_p;
+                m = d1 < d2 ? d1 : d2;
+                break;
+            }
+        }
+        len = cutoff;
+        double s = 0.0;
+        float s32 = 0.0f;
+        for (size_t i = 0; i < len; ++i) { s += p[i]; s32 += (float)p[i]; }
+        for (size_t i = 0; i < len; ++i) {
+            if (precise) p[i] /= s;
+            else p[i] = (float)((float)p[i] / s32);
+        }
+    }
+    float r = orc_sample_draw(seed);
+    double acc = 0.0;
+    float acc32 = 0.0f;
+    int64_t tok = (int64_t)idx[len - 1];
+    double mr = 0.0;
+    for (size_t i = 0; i < len; ++i) {
+        double prev, now;
+        if (precise) { prev = acc; acc += p[i]; now = acc; }
+        else { prev = acc32; acc32 += (float)p[i]; now = acc32; }
+        if (precise ? (double)r <= now : r <= acc32) {
+            tok = (int64_t)idx[i];
+            double d1 = (double)r - prev, d2 = now - r;
+            mr = d1 < d2 ? d1 : d2;
+            break;
+        }
+    }
+    if (margin) *margin = m < mr ? m : mr;
+    free(y);
+    free(idx);
+    free(p);
+    return tok;
 }

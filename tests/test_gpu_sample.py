@@ -1,0 +1,131 @@
+"""GPU parity of token selection (pkv_sample) against the CPU oracle's
+restatement of sample() / argmax() (crates/ai-engine-runtime/src/sample.rs:
+12-55).  Greedy rows are exact.  The kernel sums probability mass exactly
+(integers), so sampled rows are compared with the oracle's restatement in
+exact arithmetic (float64 exp and running sums over the reference's f32
+values): the token must be equal unless that restatement's running sum lies
+within 1e-6 of r or top_p.  Against the oracle's f32 restatement (the
+reference's own rounding), a row may differ only where that rounding alone
+moves the pick, i.e. where the f32 and float64 restatements differ."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pagedkv
+
+pytestmark = pytest.mark.gpu
+
+TD = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+AMBIGUOUS = 1e-6
+
+
+def _logits(rng, kind, V):
+    if kind == "normal":
+        return rng.standard_normal(V).astype(np.float32) * rng.choice([0.5, 3.0, 10.0])
+    if kind == "ties":
+        return rng.integers(-3, 3, V).astype(np.float32)
+    if kind == "flat":
+        return np.full(V, 1.25, np.float32)
+    x = (rng.standard_normal(V) * 4).astype(np.float32)   # a few dominant tokens
+    x[rng.integers(0, V, 3)] = 9.0
+    return x
+
+
+def _check_rows(x32, temps, top_k, top_p, got, seed=42):
+    """Returns the rows where the kernel and the f32 restatement differ."""
+    differ = []
+    for b in range(x32.shape[0]):
+        t = float(temps[b])
+        exact, margin = oracle.sample(x32[b], t, top_k=top_k, top_p=top_p, seed=seed,
+                                      precise=True)
+        ref32, _ = oracle.sample(x32[b], t, top_k=top_k, top_p=top_p, seed=seed)
+        g = int(got[b])
+        if g != exact:
+            assert margin < AMBIGUOUS, (b, exact, g, margin)
+        if g != ref32:
+            assert ref32 != exact or margin < AMBIGUOUS, (b, ref32, exact, g)
+            differ.append(b)
+    return differ
+
+
+def test_reference_kats_on_device(gpu):
+    cases = [([0.1, 5.0, 2.0, -1.0], 0.0, None, None, 1),
+             ([1.0, 5.0, 2.0], 0.0, None, None, 1),
+             ([1.0, 1.0, 1.0, 1.0, 100.0], 1.0, 1, None, 4),
+             ([1.0, 1.0, 100.0, 1.0], 1.0, None, 0.5, 2)]
+    for x, t, k, p, want in cases:
+        lg = torch.tensor([x], dtype=torch.float32, device=gpu)
+        tok = pagedkv.sample(lg, torch.tensor([t]), top_k=k, top_p=p, seed=0)
+        assert int(tok.item()) == want
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("V", [2, 7, 1000, 32000, 128256])
+@pytest.mark.parametrize("top_k,top_p", [(None, None), (40, None), (None, 0.9), (5, 0.5)])
+def test_sample_matches_oracle(gpu, dt, V, top_k, top_p):
+    rng = np.random.default_rng(V + 7 * (top_k or 0) + int(100 * (top_p or 0)))
+    kinds = ["normal", "ties", "flat", "spiky"]
+    B = 24
+    x = np.stack([_logits(rng, kinds[b % 4], V) for b in range(B)])
+    lg = torch.from_numpy(x).to(gpu).to(TD[dt])
+    x32 = lg.float().cpu().numpy()          # the values the kernel sees
+    temps = np.array([[0.0, 0.7, 1.0, 1.6, -1.0, 0.3][b % 6] for b in range(B)], np.float32)
+    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
+    torch.cuda.synchronize()
+    _check_rows(x32, temps, top_k, top_p, got.cpu().numpy())
+
+
+def test_uniform_rows_closed_form(gpu):
+    # equal logits keep index order: the pick is floor(r V)
+    r = pagedkv.sample_draw(42)
+    for V in (10, 100, 1000, 4096, 50000):
+        lg = torch.zeros((3, V), dtype=torch.bfloat16, device=gpu)
+        tok = pagedkv.sample(lg, torch.tensor([1.0, 0.5, 2.0]))
+        assert tok.cpu().tolist() == [math.floor(r * V)] * 3
+    lg = torch.zeros((1, 1000), device=gpu)
+    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_k=10).item()) == math.floor(10 * r)
+    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_p=0.5).item()) == math.floor(500 * r)
+
+
+def test_greedy_rules_on_device(gpu):
+    nan, inf = math.nan, math.inf
+    rows = [[1.0, 5.0, 5.0, 2.0], [nan, 1.0, 3.0, 3.0], [-inf, -inf, -inf, -inf],
+            [nan, -inf, nan, nan], [2.0, nan, 2.0, 9.0]]
+    lg = torch.tensor(rows, device=gpu)
+    tok = pagedkv.sample(lg)                 # no temperatures: every row greedy
+    assert tok.cpu().tolist() == [oracle.argmax(r) for r in rows] == [1, 2, 0, 0, 3]
+    # one logit: argmax even when sampling; no logits: token 0
+    assert int(pagedkv.sample(torch.tensor([[4.0]], device=gpu), torch.tensor([1.0])).item()) == 0
+    assert int(pagedkv.sample(torch.zeros((1, 0), device=gpu)).item()) == 0
+    # a large greedy row: first maximum by index
+    x = torch.randn((4, 128256), device=gpu)
+    x[:, 77777] = 50.0
+    x[:, 99999] = 50.0
+    assert pagedkv.sample(x).cpu().tolist() == [77777] * 4
+
+
+def test_strided_rows_and_determinism(gpu):
+    rng = np.random.default_rng(3)
+    big = torch.from_numpy(rng.standard_normal((16, 40000)).astype(np.float32)).to(gpu)
+    lg = big[:, 1000:33000]                  # row stride 40000, vocab 32000
+    temps = torch.full((16,), 0.8)
+    a = pagedkv.sample(lg, temps)
+    b = pagedkv.sample(lg, temps)
+    assert torch.equal(a, b)
+    _check_rows(lg.cpu().numpy(), temps.numpy(), None, None, a.cpu().numpy())
+
+
+def test_seed_changes_draw(gpu):
+    lg = torch.zeros((1, 1000), device=gpu)
+    for seed in (0, 1, 42, 12345):
+        tok = int(pagedkv.sample(lg, torch.tensor([1.0]), seed=seed).item())
+        assert tok == math.floor(pagedkv.sample_draw(seed) * 1000)
+
+
+def test_invalid_arguments(gpu):
+    lg = torch.zeros((2, 10), device=gpu)
+    with pytest.raises(pagedkv.PagedKvError):
+        pagedkv.sample(lg, torch.ones(2), top_k=-1)
