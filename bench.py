@@ -59,7 +59,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg2", "cfg5"])
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample"])
+    ap.add_argument("--rope", action="store_true",
+                    help="decode configs: q and the new k/v arrive in f32 before the rotary "
+                         "embedding, which the decode kernel applies (pkv_decode_attention_rope)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="minimum layer passes of the CPU baseline sample (0 = skip it)")
@@ -96,6 +99,8 @@ def main() -> int:
         return churn(args, dev)
     if args.config == "cfg2":
         return mix(args, dev)
+    if args.config == "sample":
+        return sample_bench(args, dev)
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
     L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
@@ -116,10 +121,11 @@ def main() -> int:
     cache.fill_normal(args.seed)
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
+    idt = torch.float32 if args.rope else tdt  # the reference's activations are f32
     q = (torch.randn((L, B, H, hd), generator=g, device=dev, dtype=torch.float32)
-         / math.sqrt(hd)).to(tdt)
-    k_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(tdt)
-    v_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(tdt)
+         / math.sqrt(hd)).to(idt)
+    k_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(idt)
+    v_new = torch.randn((L, B, KVH, hd), generator=g, device=dev, dtype=torch.float32).to(idt)
     out = torch.empty((L, B, H * hd), dtype=tdt, device=dev)
     tables = torch.from_numpy(np.where(batch.tables < 0, 0, batch.tables).astype(np.int32)).to(dev)
     ctx_lens = torch.from_numpy(batch.context_lens).to(dev)
@@ -137,10 +143,24 @@ def main() -> int:
             for l in range(L)]
     tp, cp, mbps = tables.data_ptr(), ctx_lens.data_ptr(), tables.shape[1]
 
+    rope = None
+    if args.rope:
+        # Llama-3 rotary base; q/k rotated at position seq_len inside the kernel
+        rope = pagedkv.Rope(hd, 500000.0, max_ctx + 1)
+        e = 2 if tdt != torch.float32 else 4
+        # f32 q and new k/v read instead of the pool dtype, plus one cos/sin row
+        bytes_launch += B * (H + 2 * KVH) * hd * (4 - e) + B * hd * 4
+        bytes_step = bytes_launch * L
+
     def launch(l: int, r: int, s) -> None:
         qp, op, kp, vp = ptrs[l]
-        rc = lib.pkv_decode_attention(h, r * L + l, qp, op, odt, tp, mbps, cp, max_ctx, B, H,
-                                      scale, kp, vp, s)
+        if rope is not None:
+            rc = lib.pkv_decode_attention_rope(h, r * L + l, rope.handle, None, pagedkv.F32, qp,
+                                               op, odt, tp, mbps, cp, max_ctx, B, H, scale, kp,
+                                               vp, s)
+        else:
+            rc = lib.pkv_decode_attention(h, r * L + l, qp, op, odt, tp, mbps, cp, max_ctx, B, H,
+                                          scale, kp, vp, s)
         if rc:
             pagedkv._lib.check(rc, h)
 
@@ -221,7 +241,7 @@ def main() -> int:
             traffic = tr.get("bytes_per_launch")
 
     cpu = None
-    if args.cpu_layers > 0:
+    if args.cpu_layers > 0 and not args.rope:
         eager_step(0)  # out[0] = layer 0 of replica 0, the CPU sample's layer
         torch.cuda.synchronize()
         cpu = cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log)
@@ -239,7 +259,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": {wl.BF16: "bf16", wl.F16: "f16", wl.F32: "f32"}[shape.dtype],
         "data": "synthetic (seeded N(0,1) K/V/Q, random block tables)",
-        "config": {"workload": f"{args.config}: {desc}", "batch": B, "layers": L,
+        "config": {"workload": f"{args.config}: {desc}"
+                               + (" + fused RoPE (f32 q/k/v in)" if args.rope else ""),
+                   "batch": B, "layers": L,
                    "mean_context": round(float(batch.ctx.mean()), 1), "seed": args.seed,
                    "num_blocks": batch.num_blocks, "pool_replicas": reps,
                    "launch": "hip graph" if use_graph else "eager", "parallelism": "single GPU"},
@@ -253,6 +275,95 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     cache.close()
+    return 0
+
+
+def sample_bench(args, dev) -> int:
+    """Token selection on the device (pkv_sample; sample.rs:12-55 as the
+    engine calls it, engine.rs:145-162): 256 rows of Llama-3's 128,256-entry
+    vocabulary in bf16, every row sampled at temperature 0.8 (seed 42, no
+    top-k / top-p, as the engine's sample_cfg).  value = rows/s; roofline =
+    one read of the logits per launch against HBM peak (the kernel makes
+    several passes over each row, from L2 / the Infinity Cache); greedy rows
+    are timed beside it."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import pagedkv
+
+    B, V = 256, 128256
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    logits = (torch.randn((B, V), generator=g, device=dev) * 3.0).to(torch.bfloat16)
+    temps = torch.full((B,), 0.8, device=dev)
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    lib = pagedkv.lib()
+    sp = int(torch.cuda.current_stream(dev).cuda_stream) or None
+
+    def run(t):
+        rc = lib.pkv_sample(logits.data_ptr(), pagedkv.BF16, V, B, V,
+                            t.data_ptr() if t is not None else None, 0, 1.0, 42,
+                            out.data_ptr(), sp)
+        if rc:
+            pagedkv._lib.check(rc, None)
+
+    def time_it(t):
+        for _ in range(max(1, args.warmup)):
+            run(t)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            run(t)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms = time_it(temps)
+    got = out.cpu().numpy().copy()
+    ms_greedy = time_it(None)
+    greedy = out.cpu().numpy().copy()
+    x32 = logits.float().cpu().numpy()
+    # parity on a few rows: greedy exact; sampled equal to the exact-arithmetic
+    # restatement unless its running sum is within 1e-6 of r
+    ok = True
+    for b in range(0, B, 37):
+        ok &= int(greedy[b]) == oracle.argmax(x32[b])
+        tok, margin = oracle.sample(x32[b], 0.8, precise=True)
+        ok &= int(got[b]) == tok or margin < 1e-6
+    log(f"[bench] sample: {ms * 1e3:.1f} us sampled, {ms_greedy * 1e3:.1f} us greedy "
+        f"for {B} x {V} bf16 rows; oracle check {'ok' if ok else 'FAILED'}")
+    if not ok:
+        print(json.dumps({"error": "token selection differs from the oracle"}))
+        return 1
+    rbytes = B * V * 2 + B * 4
+    cpu = None
+    if args.cpu_layers > 0:
+        # the reference procedure (sort, f32 softmax, running sum) on host rows
+        rows = iter(range(1 << 30))
+        per, n, _ = timed_passes(lambda: oracle.sample(x32[next(rows) % B], 0.8), args)
+        cpu = {"value": round(1.0 / per, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"oracle sample() (stable sort + f32 softmax + running sum, as "
+                         f"sample.rs) of one {V}-entry row, {n} passes of {per * 1e3:.1f} ms"}
+    res = {
+        "metric": "on-device token selection rows/s (sample.rs at T=0.8), Llama-3 vocabulary, 1 GPU",
+        "value": round(B / (ms / 1e3), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0, 9) logits)",
+        "config": {"workload": f"sample: {B} rows x {V} logits, temperature 0.8, seed 42",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(rbytes / (ms / 1e3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(rbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "pkv::sample_kernel", "kernel_avg_us": round(ms * 1e3, 2),
+                     "algorithmic_bytes_per_launch": rbytes},
+        "greedy": {"us": round(ms_greedy * 1e3, 2),
+                   "GBps": round(rbytes / (ms_greedy / 1e3) / 1e9, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
     return 0
 
 
@@ -556,22 +667,39 @@ def churn(args, dev) -> int:
     surv = np.concatenate([np.array(t.blocks, np.int32) for t in survivors if len(t)])
     n_surv = surv.size
     remap = wl.permutation(args.seed ^ 0xC0DE, n_surv).astype(np.int32)
+    # warm-up: move one free block onto another (loads the kernel; no live data moves)
+    free_ids = np.setdiff1d(np.arange(N, dtype=np.int32), surv)
+    cache.compact(free_ids[:1], free_ids[1:2])
     torch.cuda.synchronize()
-    t0 = time.time()
-    e0.record()
-    cache.compact(surv, remap)
-    e1.record()
-    torch.cuda.synchronize()
-    comp_wall_ms = (time.time() - t0) * 1e3
-    comp_ms = e0.elapsed_time(e1)
-    comp_kms, _ = cache.profile_read()
+    cache.profile_read()
+    # compaction forward (survivors -> remap) and back, alternately: every
+    # call moves the same blocks; the average covers host planning, plan
+    # upload and kernel of one call
+    comp_reps = max(2, reps)
+    comp_ms = comp_wall_ms = 0.0
+    for k in range(comp_reps):
+        a_, b_ = (surv, remap) if k % 2 == 0 else (remap, surv)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        e0.record()
+        cache.compact(a_, b_)
+        e1.record()
+        torch.cuda.synchronize()
+        comp_wall_ms += (time.time() - t0) * 1e3
+        comp_ms += e0.elapsed_time(e1)
+    comp_ms /= comp_reps
+    comp_wall_ms /= comp_reps
+    comp_kms, comp_n = cache.profile_read()
+    comp_kms /= max(1, comp_n)
     cache.profile(False)
+    if comp_reps % 2:
+        cache.compact(remap, surv)  # leave the survivors where the tables say
     moved = int((surv != remap).sum())
     comp_bytes = 2 * moved * cache.block_bytes * 2 * L
     cache.check()
     step_ms = cow_ms + comp_ms
     log(f"[bench] cfg5: CoW {cow_ms:.3f} ms ({cow_bytes / (cow_ms / 1e3) / 1e9:.0f} GB/s), "
-        f"compaction {comp_ms:.2f} ms incl. plan upload, kernel {comp_kms:.2f} ms "
+        f"compaction {comp_ms:.2f} ms incl. host plan + upload, kernel {comp_kms:.2f} ms "
         f"({comp_bytes / (comp_kms / 1e3) / 1e9:.0f} GB/s)")
 
     traffic = None
@@ -604,7 +732,8 @@ def churn(args, dev) -> int:
                      "algorithmic_bytes_per_launch": comp_bytes},
         "cow": {"copies": 512, "ms": round(cow_ms, 4), "kernel_ms": round(cow_kms, 4),
                 "GBps": round(cow_bytes / (cow_ms / 1e3) / 1e9, 1)},
-        "compaction": {"moved_blocks": moved, "ms_device_incl_plan_upload": round(comp_ms, 3),
+        "compaction": {"moved_blocks": moved, "calls": comp_reps,
+                       "ms_incl_host_plan_and_upload": round(comp_ms, 3),
                        "ms_wall_incl_plan": round(comp_wall_ms, 3), "kernel_ms": round(comp_kms, 3),
                        "GBps": round(comp_bytes / (comp_ms / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,
