@@ -21,7 +21,9 @@
 //   registers, as B).  The accumulator puts in each lane the scores of 4
 //   keys per 16-key tile of ONE row (lane % 16): the per-lane k-slice of the
 //   B operand of O^T = V^T P^T, so P never leaves registers.  Online softmax
-//   per row in the exp2 domain, fp32 accumulation throughout.  P enters the
+//   per row in the exp2 domain, fp32 accumulation throughout; for 16-bit
+//   pools the row sums come from the P.V MFMA with an all-ones V^T tile (the
+//   same rounded P as the numerator, no VALU adds).  P enters the
 //   PV product as f16 for f16 pools (relative rounding 2^-12); for bf16 pools
 //   as a bf16 high part plus a bf16 residual (two MFMAs, ~16 significant
 //   bits); for f32 pools exactly, on v_mfma_f32_16x16x4f32.
@@ -38,7 +40,26 @@
 namespace pkv {
 namespace {
 
-constexpr int kPW = 4;   // waves per workgroup
+// Waves per workgroup (each owns 16 * NR rows).
+#ifndef PKV_PREFILL_WAVES
+#define PKV_PREFILL_WAVES 4
+#endif
+constexpr int kPW = PKV_PREFILL_WAVES;
+constexpr int kPT = kPW * 64;  // threads per workgroup
+
+// 16-row MFMA tiles per wave for 16-bit pools of head_dim <= 128.
+#ifndef PKV_PREFILL_NR
+#define PKV_PREFILL_NR 2
+#endif
+// Keys per tile for rows of at most 256 bytes.
+#ifndef PKV_PREFILL_KT
+#define PKV_PREFILL_KT 64
+#endif
+// 16-bit pools: softmax row sums taken by the P.V MFMA from an all-ones
+// operand instead of VALU adds.
+#ifndef PKV_PREFILL_MFMA_ROWSUM
+#define PKV_PREFILL_MFMA_ROWSUM 1
+#endif
 constexpr int kXcd = 8;  // XCDs; workgroups go round-robin over them
 
 template <int DT, int HD, int R>
@@ -46,11 +67,11 @@ struct PCfg {
   static constexpr int E = DT == PKV_F32 ? 4 : 2;
   static constexpr int RB = HD * E;                                // row bytes
   static constexpr int NF = RB / 64;                               // 16-B fragments per lane per row
-  static constexpr int NR = (DT != PKV_F32 && HD <= 128) ? 2 : 1;  // 16-row tiles per wave
+  static constexpr int NR = (DT != PKV_F32 && HD <= 128) ? PKV_PREFILL_NR : 1;  // 16-row tiles per wave
   static constexpr int RW = 16 * NR;                               // rows per wave
   static constexpr int ROWS = kPW * RW;                            // rows per workgroup
   static constexpr int ND = HD / 16;                               // 16-dim tiles of O^T
-  static constexpr int KT = RB >= 512 ? 32 : 64;                   // keys per tile
+  static constexpr int KT = RB >= 512 ? 32 : (RB >= 256 ? 64 : PKV_PREFILL_KT);  // keys per tile
   static constexpr int NKM = KT / 16;                              // 16-key MFMA tiles
   static constexpr int CH = RB / 16;                               // 16-B chunks per row
   static constexpr int EPC = 16 / E;                               // elements per chunk
@@ -59,13 +80,15 @@ struct PCfg {
   static constexpr int VP = RB + 32;                               // 16-bit: V row pitch in LDS
   static constexpr int KLDS = KT * KPITCH;
   static constexpr int STAGE = KLDS + (DT == PKV_F32 ? HD * VTP : KT * VP);
-  static constexpr int NKL = KT * CH / (kPW * kWave);              // K chunks per thread
-  static constexpr int NVP = (KT / 2) * CH / (kPW * kWave);        // V key-pair chunks per thread
+  static constexpr int NKL = KT * CH / kPT;                        // K chunks per thread
+  // V key-pair chunks per thread (f32 pools; 16-bit pools load V like K and
+  // keep NKL chunks in NVP x 2 registers)
+  static constexpr int NVP = DT == PKV_F32 ? (KT / 2) * CH / kPT : (NKL + 1) / 2;
   // register sets for tiles in flight: loads run NSET + 1 tiles ahead
   static constexpr int NSET = (NKL + 2 * NVP) <= 4 ? 2 : 1;
   static constexpr int D = NSET + 1;
   static_assert(NKL >= 1 && NVP >= 1, "tile too small for the workgroup");
-  static_assert(KT * CH % (kPW * kWave) == 0 && (KT / 2) * CH % (kPW * kWave) == 0, "");
+  static_assert(KT * CH % kPT == 0 && (DT != PKV_F32 || (KT / 2) * CH % kPT == 0), "");
 };
 
 struct PrefillKArgs {
@@ -121,7 +144,7 @@ __device__ __forceinline__ uint32_t cvt_pk16(float x0, float x1) {
 }
 
 template <int DT, int HD, int R>
-__global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
+__global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   using C = PCfg<DT, HD, R>;
   __shared__ __attribute__((aligned(16))) char lds[2 * C::STAGE];
 
@@ -192,8 +215,8 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
   }
 
   // ---- cooperative tile loads.  K chunk i of a thread: key
-  //      (tid + 256 i) / CH, bytes 16 (tid % CH); V pair chunk v: keys
-  //      2 ((tid + 256 v) / CH) and +1.  CH divides 64, so one wave's share
+  //      (tid + kPT i) / CH, bytes 16 (tid % CH); V pair chunk v: keys
+  //      2 ((tid + kPT v) / CH) and +1 (kPT = threads per workgroup).  CH divides 64, so one wave's share
   //      of a load covers at most 16 aligned keys -- one block (block_size
   //      >= 16): its block id is wave-uniform (a scalar load) and a lane
   //      adds a 32-bit offset.  Keys past n_keys are clamped to n_keys - 1.
@@ -216,10 +239,10 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
   int kb[2][C::NKL], vb[2][C::NVP];  // raw block ids, two sets by tile parity
   auto ids = [&](int t, int (&kbs)[C::NKL], int (&vbs)[C::NVP]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < C::NKL; ++i) kbs[i] = table_at(t * C::KT + wkey + 256 * i / C::CH);
+    for (int i = 0; i < C::NKL; ++i) kbs[i] = table_at(t * C::KT + wkey + kPT * i / C::CH);
     if constexpr (DT == PKV_F32) {  // 16-bit pools load V with K's keys and block ids
 #pragma unroll
-      for (int v = 0; v < C::NVP; ++v) vbs[v] = table_at(t * C::KT + 2 * (wkey + 256 * v / C::CH));
+      for (int v = 0; v < C::NVP; ++v) vbs[v] = table_at(t * C::KT + 2 * (wkey + kPT * v / C::CH));
     }
   };
   u32x4 kreg[C::NSET][C::NKL], vreg[C::NSET][C::NVP][2];
@@ -227,14 +250,14 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
                    const int (&kbs)[C::NKL], const int (&vbs)[C::NVP]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < C::NKL; ++i) {
-      const int key = min(t * C::KT + wkey + 256 * i / C::CH + lkey, n_keys - 1);
+      const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
       const char* base = kh + (size_t)checked(kbs[i]) * blk_stride;
       kr[i] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
     }
     if constexpr (DT == PKV_F32) {
 #pragma unroll
       for (int v = 0; v < C::NVP; ++v) {
-        const int k0 = t * C::KT + 2 * (wkey + 256 * v / C::CH + lkey);
+        const int k0 = t * C::KT + 2 * (wkey + kPT * v / C::CH + lkey);
         const char* base = vh + (size_t)checked(vbs[v]) * blk_stride;
         vr[v][0] = ld16(base + ((uint32_t)((min(k0, n_keys - 1) & tmask) * slot_stride) + lbyte));
         vr[v][1] = ld16(base + ((uint32_t)((min(k0 + 1, n_keys - 1) & tmask) * slot_stride) + lbyte));
@@ -242,7 +265,7 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
     } else {  // V chunk 2 v + h: the same key and bytes as K chunk 2 v + h
 #pragma unroll
       for (int i = 0; i < C::NKL; ++i) {
-        const int key = min(t * C::KT + wkey + 256 * i / C::CH + lkey, n_keys - 1);
+        const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
         const char* base = vh + (size_t)checked(kbs[i]) * blk_stride;
         vr[i >> 1][i & 1] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
       }
@@ -253,13 +276,13 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
     char* vl = kl + C::KLDS;
 #pragma unroll
     for (int i = 0; i < C::NKL; ++i) {
-      const int idx = tid + 256 * i;
+      const int idx = tid + kPT * i;
       st16(kl + (idx / C::CH) * C::KPITCH + 16 * (idx % C::CH), kr[i]);
     }
     if constexpr (DT == PKV_F32) {  // V^T: dim-major rows, keys in natural order
 #pragma unroll
       for (int v = 0; v < C::NVP; ++v) {
-        const int idx = tid + 256 * v;
+        const int idx = tid + kPT * v;
         char* dst = vl + C::EPC * (idx % C::CH) * C::VTP + 2 * (idx / C::CH) * 4;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -269,18 +292,27 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
     } else {  // V row-major like K; read transposed by ds_read_b64_tr_b16
 #pragma unroll
       for (int i = 0; i < C::NKL; ++i) {
-        const int idx = tid + 256 * i;
+        const int idx = tid + kPT * i;
         st16(vl + (idx / C::CH) * C::VP + 16 * (idx % C::CH), vr[i >> 1][i & 1]);
       }
     }
   };
 
+  // Row sums: lane-partial VALU sums, or (16-bit pools) the P.V MFMA against
+  // an all-ones V^T tile, which leaves the full sum of row 16 rn + col in
+  // every register of lacc[rn].
+  constexpr bool kRowSum = PKV_PREFILL_MFMA_ROWSUM && DT != PKV_F32;
+  const uint32_t one2 = DT == PKV_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4 ones = u32x4{one2, one2, one2, one2};
+  (void)ones;
+  f32x4 lacc[C::NR];
   float m[C::NR], lsum[C::NR];
   f32x4 o[C::ND][C::NR];
 #pragma unroll
   for (int rn = 0; rn < C::NR; ++rn) {
     m[rn] = -INFINITY;
     lsum[rn] = 0.0f;
+    lacc[rn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int dm = 0; dm < C::ND; ++dm) o[dm][rn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
@@ -360,15 +392,17 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           p[km][rn][j] = fast_exp2(fmaf(sacc[km][rn][j], a.scale_log2, nm));
-          ssum += p[km][rn][j];
+          if constexpr (!kRowSum) ssum += p[km][rn][j];
         }
-      lsum[rn] = fmaf(lsum[rn], alpha[rn], ssum);  // lane-partial over its keys
+      if constexpr (!kRowSum) lsum[rn] = fmaf(lsum[rn], alpha[rn], ssum);  // lane-partial
     }
     if (__builtin_amdgcn_ballot_w64(moved)) {  // wave-uniform
 #pragma unroll
-      for (int rn = 0; rn < C::NR; ++rn)
+      for (int rn = 0; rn < C::NR; ++rn) {
 #pragma unroll
         for (int dm = 0; dm < C::ND; ++dm) o[dm][rn] *= alpha[rn];
+        if constexpr (kRowSum) lacc[rn] *= alpha[rn];
+      }
     }
     // ---- O^T += V^T P^T ----
     if constexpr (DT == PKV_F32) {
@@ -407,6 +441,14 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
           for (int rn = 0; rn < C::NR; ++rn) {
             mfma_frag<DT>(va, phi[rn], o[dm][rn]);
             if constexpr (DT == PKV_BF16) mfma_frag<DT>(va, plo[rn], o[dm][rn]);
+          }
+        }
+        if constexpr (kRowSum) {
+          // every row of the all-ones operand sums the row's weights
+#pragma unroll
+          for (int rn = 0; rn < C::NR; ++rn) {
+            mfma_frag<DT>(ones, phi[rn], lacc[rn]);
+            if constexpr (DT == PKV_BF16) mfma_frag<DT>(ones, plo[rn], lacc[rn]);
           }
         }
       }
@@ -456,9 +498,14 @@ __global__ void __launch_bounds__(kPW * kWave) prefill_kernel(PrefillKArgs a) {
   // ---- epilogue: lane holds O^T[dims 16 dm + 4 G + j][row 16 rn + col] ----
 #pragma unroll
   for (int rn = 0; rn < C::NR; ++rn) {
-    float l = lsum[rn];
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
+    float l;
+    if constexpr (kRowSum) {
+      l = lacc[rn][0];
+    } else {
+      l = lsum[rn];
+      l += shfl_xor_f(l, 16);
+      l += shfl_xor_f(l, 32);
+    }
     const int r = roww + 16 * rn + col;
     if (r >= n_rows) continue;
     const float inv = 1.0f / l;
@@ -493,7 +540,7 @@ hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
     k.per_xcd = (int)per;
     grid = per * kXcd;
   }
-  prefill_kernel<DT, HD, R><<<(unsigned)grid, kPW * kWave, 0, s>>>(k);
+  prefill_kernel<DT, HD, R><<<(unsigned)grid, kPT, 0, s>>>(k);
   return hipGetLastError();
 }
 
