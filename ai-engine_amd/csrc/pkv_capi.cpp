@@ -69,8 +69,9 @@ int check_layer(pkv_pool* p, int layer) {
   return PKV_OK;
 }
 
-// Ensure the decode workspace holds `counter_bytes` of counters followed by
-// `total - counter_bytes` of partials.  Counters are zeroed on (re)allocation
+// Ensure the pool workspace (split-context partials of decode and of split
+// prefill; calls on the pool's stream use it in turn) holds `counter_bytes`
+// of counters followed by `total - counter_bytes` of partials.  Counters are zeroed on (re)allocation
 // and the kernels leave them zero.
 int ensure_workspace(pkv_pool* p, size_t total, size_t counter_bytes) {
   size_t part_need = total - counter_bytes;
@@ -557,6 +558,13 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
   if (out_dtype != PKV_F32 && out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   DeviceGuard dg(p->device);
+  {
+    int pk = 0, mp = 0;
+    size_t need = 0;
+    pkv::prefill_plan(p, n_seqs, n_head, max_q_len, max_context_len, &pk, &mp, &need);
+    if (need)
+      if (int rc = ensure_workspace(p, p->ws_counter_bytes + need, p->ws_counter_bytes)) return rc;
+  }
   pkv::PrefillArgs a{q, out, out_dtype, cu_q_lens, context_lens, block_tables,
                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale};
   hipEvent_t eb = nullptr, ee = nullptr;
@@ -564,6 +572,27 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
   hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "prefill launch");
   return PKV_OK;
+}
+
+size_t pkv_prefill_workspace_bytes(const pkv_pool* p, int n_seqs, int n_head, int max_q_len,
+                                   int max_context_len) {
+  if (!p || n_seqs <= 0 || max_q_len <= 0 || n_head <= 0 || n_head % p->n_kv_head) return 0;
+  int pk = 0, mp = 0;
+  size_t need = 0;
+  pkv::prefill_plan(p, n_seqs, n_head, max_q_len, max_context_len, &pk, &mp, &need);
+  return need;
+}
+
+int pkv_pool_reserve_prefill(pkv_pool* p, int n_seqs, int n_head, int max_q_len,
+                             int max_context_len) {
+  CHECK_POOL(p);
+  if (n_seqs < 0 || max_q_len < 0 || n_head <= 0 || n_head % p->n_kv_head)
+    return fail(p, PKV_ERR_INVALID, "reserve_prefill: n_seqs %d, max_q_len %d, n_head %d",
+                n_seqs, max_q_len, n_head);
+  size_t need = pkv_prefill_workspace_bytes(p, n_seqs, n_head, max_q_len, max_context_len);
+  if (!need) return PKV_OK;
+  DeviceGuard dg(p->device);
+  return ensure_workspace(p, p->ws_counter_bytes + need, p->ws_counter_bytes);
 }
 
 int pkv_pool_profile(pkv_pool* p, int enable) {

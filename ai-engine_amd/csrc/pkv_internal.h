@@ -154,6 +154,11 @@ struct PrefillArgs {
   float scale;
 };
 bool prefill_supported(const pkv_pool* p, int n_head);
+// Split of long key ranges for launches with few row blocks: keys per part,
+// parts per row block at most, and the workspace the partials need (0: no
+// split).
+void prefill_plan(const pkv_pool* p, int n_seqs, int n_head, int max_q_len, int max_context_len,
+                  int* part_keys, int* max_parts, size_t* ws_bytes);
 hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
                           hipStream_t stream, hipEvent_t ev_begin = nullptr,
                           hipEvent_t ev_end = nullptr);

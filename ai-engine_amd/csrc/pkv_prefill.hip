@@ -55,6 +55,17 @@ constexpr int kPT = kPW * 64;  // threads per workgroup
 #ifndef PKV_PREFILL_KT
 #define PKV_PREFILL_KT 64
 #endif
+// Keys per part of a long key range: row blocks whose prior context exceeds
+// it are split into parts that run as separate workgroups and are merged
+// afterwards (when the launch has few row blocks; see prefill_plan).
+#ifndef PKV_PREFILL_PART_KEYS
+#define PKV_PREFILL_PART_KEYS 1024
+#endif
+// Splitting stops at this many row blocks (enough to fill the GPU), and
+// parts are lengthened to keep at most kSplitMaxItems partial items.
+#ifndef PKV_PREFILL_SPLIT_MAX_BLOCKS
+#define PKV_PREFILL_SPLIT_MAX_BLOCKS 256
+#endif
 // 16-bit pools: softmax row sums taken by the P.V MFMA from an all-ones
 // operand instead of VALU adds.
 #ifndef PKV_PREFILL_MFMA_ROWSUM
@@ -108,10 +119,22 @@ struct PrefillKArgs {
   int max_q_len;
   int max_context_len;
   int row_blocks;  // ceil(max_q_len * R / ROWS)
+  int part_keys;   // keys per part: a multiple of two tiles
+  int max_parts;   // parts per row block at most (1 + (max_context_len - 1) / part_keys)
   int per_xcd;     // workgroup slots per XCD (affinity mapping), 0 = plain order
   float scale_log2;
+  float* part_ml;  // split key ranges: (m, l) per (item, row)
+  float* part_o;   //   and the unnormalised O row
   uint32_t* err;
 };
+
+// Parts of a row block whose rows have prior context `prior`: every part but
+// the last covers part_keys keys below the prior (visible to all rows, no
+// mask, at least one key per row); the last one runs from there to the
+// block's last key.
+__device__ __forceinline__ int n_parts_of(int prior, int part_keys) {
+  return 1 + prior / part_keys;
+}
 
 template <int DT>
 __device__ __forceinline__ uint32_t to16(float x) {
@@ -154,19 +177,26 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const int G = lane >> 4;
   const int col = lane & 15;
 
-  // ---- work item: (sequence, kv head) pair sg, row block rb ----
+  // ---- work item: (sequence, kv head) pair sg, row block rb, key part ----
+  // Row blocks run last (longest) first, each with its parts in order.
   const int n_sg = a.n_seqs * a.kvh;
-  int sg, rb;
-  if (a.per_xcd > 0) {
-    const int x = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
-    const int nx = (n_sg - x + kXcd - 1) / kXcd;  // pairs of this XCD
-    if (slot >= nx * a.row_blocks) return;
-    rb = a.row_blocks - 1 - slot / nx;
-    sg = x + kXcd * (slot % nx);
-  } else {
-    if ((int)blockIdx.x >= n_sg * a.row_blocks) return;
-    rb = a.row_blocks - 1 - (int)blockIdx.x / n_sg;
-    sg = (int)blockIdx.x % n_sg;
+  const int rbp = a.row_blocks * a.max_parts;
+  int sg, rb, part;
+  {
+    int u;
+    if (a.per_xcd > 0) {
+      const int x = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
+      const int nx = (n_sg - x + kXcd - 1) / kXcd;  // pairs of this XCD
+      if (slot >= nx * rbp) return;
+      u = slot / nx;
+      sg = x + kXcd * (slot % nx);
+    } else {
+      if ((int)blockIdx.x >= n_sg * rbp) return;
+      u = (int)blockIdx.x / n_sg;
+      sg = (int)blockIdx.x % n_sg;
+    }
+    rb = a.row_blocks - 1 - u / a.max_parts;
+    part = u % a.max_parts;
   }
   const int g = sg % a.kvh;
   const int s = sg / a.kvh;
@@ -194,9 +224,13 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const char* vh = a.v_pool + (size_t)g * C::RB;
   const int32_t* table = a.block_tables + (size_t)s * a.mbps;
 
-  // keys the workgroup needs: 0 .. prior + its last token
+  // keys the workgroup needs: 0 .. prior + its last token, in parts
   const int n_keys = prior + min(row0 + C::ROWS - 1, n_rows - 1) / R + 1;
-  const int n_tiles = (n_keys + C::KT - 1) / C::KT;
+  const int nparts = n_parts_of(prior, a.part_keys);
+  if (part >= nparts) return;  // uniform over the workgroup
+  const int k_hi = part + 1 < nparts ? (part + 1) * a.part_keys : n_keys;
+  const int t_lo = part * (a.part_keys / C::KT);
+  const int n_tiles = (k_hi + C::KT - 1) / C::KT;  // tiles t_lo .. n_tiles - 1
 
   // ---- this wave's rows (B operand / output): row 16 rn + col ----
   const int roww = row0 + wave * C::RW;
@@ -465,35 +499,68 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   // memory operations run unconditionally: the in-order wait counts stay
   // exact across the loop.  Iterations run in pairs (register sets and LDS
   // stages alternate); a tile past the end computes nothing.
+  // Tile indices are absolute (keys t * KT ..); a part starts at an even
+  // tile (part_keys is a multiple of two tiles), so parities, LDS stages and
+  // register sets follow t as in a whole range.
   constexpr int NS = C::NSET, D = C::D;
-  ids(0, kb[0], vb[0]);
-  loads(0, kreg[0], vreg[0], kb[0], vb[0]);
+  ids(t_lo, kb[0], vb[0]);
+  loads(t_lo, kreg[0], vreg[0], kb[0], vb[0]);
   if constexpr (D > 2) {
-    ids(1, kb[1], vb[1]);
-    loads(1, kreg[1 % NS], vreg[1 % NS], kb[1], vb[1]);
+    ids(t_lo + 1, kb[1], vb[1]);
+    loads(t_lo + 1, kreg[1 % NS], vreg[1 % NS], kb[1], vb[1]);
   }
   store(0, kreg[0], vreg[0]);
-  ids(D - 1, kb[(D - 1) & 1], vb[(D - 1) & 1]);
-  ids(D, kb[D & 1], vb[D & 1]);
-  loads(D - 1, kreg[(D - 1) % NS], vreg[(D - 1) % NS], kb[(D - 1) & 1], vb[(D - 1) & 1]);
+  ids(t_lo + D - 1, kb[(D - 1) & 1], vb[(D - 1) & 1]);
+  ids(t_lo + D, kb[D & 1], vb[D & 1]);
+  loads(t_lo + D - 1, kreg[(D - 1) % NS], vreg[(D - 1) % NS], kb[(D - 1) & 1], vb[(D - 1) & 1]);
   __syncthreads();
 
   auto iter = [&](int t, auto parity) __attribute__((always_inline)) {
     constexpr int P = decltype(parity)::value;  // t & 1
     const int k0 = t * C::KT;
-    if (has_rows && k0 <= klim_hi)  // wave-uniform: some row sees a key of this tile
+    // wave-uniform: the tile is in this part and some row sees one of its keys
+    if (has_rows && k0 < k_hi && k0 <= klim_hi)
       compute(t, k0 + C::KT - 1 > klim_lo);
     store((P + 1) & 1, kreg[(P + 1) % NS], vreg[(P + 1) % NS]);
     ids(t + D + 1, kb[(P + D + 1) & 1], vb[(P + D + 1) & 1]);
     loads(t + D, kreg[(P + D) % NS], vreg[(P + D) % NS], kb[(P + D) & 1], vb[(P + D) & 1]);
     __syncthreads();
   };
-  for (int t = 0; t < n_tiles; t += 2) {
+  for (int t = t_lo; t < n_tiles; t += 2) {
     iter(t, std::integral_constant<int, 0>{});
     iter(t + 1, std::integral_constant<int, 1>{});
   }
   if (bad_block && lane == 0) atomicOr(a.err, PKV_EBIT_BLOCK);
   if (!has_rows) return;
+
+  if (nparts > 1) {
+    // ---- partial result of this part: (m, l) and the unnormalised O row
+    //      (lane holds O^T[dims 16 dm + 4 G + j][row 16 rn + col]) ----
+    const size_t item = ((size_t)sg * a.row_blocks + rb) * a.max_parts + part;
+#pragma unroll
+    for (int rn = 0; rn < C::NR; ++rn) {
+      float l;
+      if constexpr (kRowSum) {
+        l = lacc[rn][0];
+      } else {
+        l = lsum[rn];
+        l += shfl_xor_f(l, 16);
+        l += shfl_xor_f(l, 32);
+      }
+      const int r = roww + 16 * rn + col;
+      if (r >= n_rows) continue;
+      const size_t pr = item * C::ROWS + (r - row0);
+      float* po = a.part_o + pr * HD;
+#pragma unroll
+      for (int dm = 0; dm < C::ND; ++dm)
+        *reinterpret_cast<f32x4*>(po + 16 * dm + 4 * G) = o[dm][rn];
+      if (G == 0) {
+        a.part_ml[2 * pr] = m[rn];
+        a.part_ml[2 * pr + 1] = l;
+      }
+    }
+    return;
+  }
 
   // ---- epilogue: lane holds O^T[dims 16 dm + 4 G + j][row 16 rn + col] ----
 #pragma unroll
@@ -525,18 +592,76 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   }
 }
 
+// Merge of a split row block (sequence s, kv head g, row block rb): per row,
+// M = max_p m_p, L = sum_p l_p 2^(m_p - M), O = sum_p O_p 2^(m_p - M) / L
+// (exp2 domain of the main kernel), four output elements per thread.  The
+// validity checks repeat the main kernel's (which reports the errors).
+template <int HD>
+__global__ void __launch_bounds__(256)
+    prefill_merge_kernel(PrefillKArgs a, int R, int rows_per_block, int out_dt) {
+  const int sg = (int)blockIdx.x / a.row_blocks;
+  const int rb = (int)blockIdx.x % a.row_blocks;
+  if (sg >= a.n_seqs * a.kvh) return;
+  const int g = sg % a.kvh, s = sg / a.kvh;
+  const int q0 = a.cu_q_lens[s];
+  const int q_len = min(a.cu_q_lens[s + 1] - q0, a.max_q_len);
+  const int ctx = a.context_lens[s];
+  if (ctx > a.max_context_len || ctx > a.mbps * (1 << a.bs_log2) || ctx < q_len || q_len < 0)
+    return;
+  const int nparts = n_parts_of(ctx - q_len, a.part_keys);
+  const int n_rows = q_len * R;
+  const int row0 = rb * rows_per_block;
+  if (nparts <= 1 || row0 >= n_rows) return;
+  const int nr = min(rows_per_block, n_rows - row0);
+  const size_t item0 = ((size_t)sg * a.row_blocks + rb) * a.max_parts;
+  const size_t pstride = (size_t)rows_per_block;  // rows between parts
+  const int H = a.kvh * R;
+  constexpr int Q4 = HD / 4;
+  for (int task = threadIdx.x; task < nr * Q4; task += 256) {
+    const int rr = task / Q4;
+    const int d4 = (task - rr * Q4) * 4;
+    const size_t pr0 = item0 * pstride + rr;
+    float M = -INFINITY;
+    for (int j = 0; j < nparts; ++j) M = fmaxf(M, a.part_ml[2 * (pr0 + j * pstride)]);
+    float L = 0.0f;
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < nparts; ++j) {
+      const size_t pr = pr0 + j * pstride;
+      const float w = fast_exp2(a.part_ml[2 * pr] - M);
+      L = fmaf(w, a.part_ml[2 * pr + 1], L);
+      const f32x4 ov = *reinterpret_cast<const f32x4*>(a.part_o + pr * HD + d4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, ov[i], acc[i]);
+    }
+    const float inv = 1.0f / L;
+    const int r = row0 + rr;
+    const size_t eo = ((size_t)(q0 + r / R) * H + g * R + r % R) * HD + d4;
+    if (a.out_f32) {
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) =
+          f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = out_dt == PKV_BF16 ? f32_to_bf16_bits(acc[i] * inv) : f32_to_f16_bits(acc[i] * inv);
+      *reinterpret_cast<uint64_t*>(reinterpret_cast<uint16_t*>(a.out) + eo) =
+          (uint64_t)(w[0] | (w[1] << 16)) | ((uint64_t)(w[2] | (w[3] << 16)) << 32);
+    }
+  }
+}
+
 template <int DT, int HD, int R>
 hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
   using C = PCfg<DT, HD, R>;
   k.row_blocks = (k.max_q_len * R + C::ROWS - 1) / C::ROWS;
   const long long n_sg = (long long)k.n_seqs * k.kvh;
-  const long long items = n_sg * k.row_blocks;
+  const long long items = n_sg * k.row_blocks * k.max_parts;
   if (items <= 0) return hipSuccess;
   if (items >= (1ll << 31)) return hipErrorInvalidValue;
   long long grid = items;
   k.per_xcd = 0;
   if (n_sg >= kXcd) {
-    const long long per = ((n_sg + kXcd - 1) / kXcd) * k.row_blocks;
+    const long long per = ((n_sg + kXcd - 1) / kXcd) * k.row_blocks * k.max_parts;
     k.per_xcd = (int)per;
     grid = per * kXcd;
   }
@@ -567,13 +692,63 @@ hipError_t plaunch_hd(int HD, int R, const PrefillKArgs& k, hipStream_t s) {
   }
 }
 
+template <int HD>
+hipError_t pmerge(const PrefillKArgs& k, int R, int rows, int out_dt, hipStream_t s) {
+  const long long blocks = (long long)k.n_seqs * k.kvh * k.row_blocks;
+  if (blocks <= 0) return hipSuccess;
+  prefill_merge_kernel<HD><<<(unsigned)blocks, 256, 0, s>>>(k, R, rows, out_dt);
+  return hipGetLastError();
+}
+
 int ilog2p(int x) {
   int r = 0;
   while ((1 << r) < x) ++r;
   return r;
 }
 
+// Keys per tile and rows per workgroup of the kernel instantiated for a
+// pool's dtype and head_dim (host mirror of PCfg).
+void prefill_shape(int dt, int hd, int* kt, int* rows) {
+  const int rbytes = hd * (dt == PKV_F32 ? 4 : 2);
+  *kt = rbytes >= 512 ? 32 : (rbytes >= 256 ? 64 : PKV_PREFILL_KT);
+  *rows = kPW * 16 * ((dt != PKV_F32 && hd <= 128) ? PKV_PREFILL_NR : 1);
+}
+
+constexpr long long kSplitMaxItems = 4096;  // partial items at most
+
 }  // namespace
+
+void prefill_plan(const pkv_pool* p, int n_seqs, int n_head, int max_q_len, int max_context_len,
+                  int* part_keys, int* max_parts, size_t* ws_bytes) {
+  int kt = 0, rows = 0;
+  prefill_shape(p->dtype, p->head_dim, &kt, &rows);
+  const long long R = n_head / p->n_kv_head;
+  const long long blocks =
+      (long long)n_seqs * p->n_kv_head * (((long long)max_q_len * R + rows - 1) / rows);
+  const int mcl = max_context_len > 0 ? max_context_len : 1;
+  const int unit = 2 * kt;
+  auto round_up = [&](long long x) { return (int)((x + unit - 1) / unit * unit); };
+  int pk = round_up(PKV_PREFILL_PART_KEYS);
+  int mp = 1 + (mcl - 1) / pk;
+  if (blocks >= PKV_PREFILL_SPLIT_MAX_BLOCKS || blocks <= 0) {
+    // enough row blocks to fill the GPU: no split
+    pk = round_up(mcl);
+    mp = 1;
+  } else {
+    while (mp > 1 && blocks * mp > kSplitMaxItems) {
+      pk = round_up(2LL * pk);
+      mp = 1 + (mcl - 1) / pk;
+    }
+  }
+  *part_keys = pk;
+  *max_parts = mp;
+  size_t bytes = 0;
+  if (mp > 1) {
+    const size_t n = (size_t)blocks * mp * rows;  // partial rows
+    bytes = ((n * 2 * 4 + 255) / 256) * 256 + n * (size_t)p->head_dim * 4;
+  }
+  if (ws_bytes) *ws_bytes = bytes;
+}
 
 bool prefill_supported(const pkv_pool* p, int n_head) {
   if (n_head <= 0 || n_head % p->n_kv_head != 0) return false;
@@ -603,6 +778,20 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
   k.max_context_len = a.max_context_len;
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.err = p->err;
+  size_t ws = 0;
+  prefill_plan(p, a.n_seqs, a.n_head, a.max_q_len, a.max_context_len, &k.part_keys,
+               &k.max_parts, &ws);
+  if (k.max_parts > 1) {
+    // the split's partials live in the pool workspace (sized by the caller)
+    if (!p->ws || p->ws_bytes - p->ws_counter_bytes < ws) return hipErrorInvalidValue;
+    int kt = 0, rows = 0;
+    prefill_shape(p->dtype, p->head_dim, &kt, &rows);
+    const int R = a.n_head / p->n_kv_head;
+    const size_t n = (size_t)a.n_seqs * p->n_kv_head *
+                     (((size_t)a.max_q_len * R + rows - 1) / rows) * k.max_parts * rows;
+    k.part_ml = reinterpret_cast<float*>(p->ws + p->ws_counter_bytes);
+    k.part_o = reinterpret_cast<float*>(p->ws + p->ws_counter_bytes + ((n * 2 * 4 + 255) / 256) * 256);
+  }
   int R = a.n_head / p->n_kv_head;
   hipError_t e = hipSuccess;
   if (ev_begin) e = hipEventRecord(ev_begin, stream);
@@ -613,7 +802,15 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
     default: e = plaunch_hd<PKV_BF16>(p->head_dim, R, k, stream); break;
   }
   if (e == hipSuccess && ev_end) e = hipEventRecord(ev_end, stream);
-  return e;
+  if (e != hipSuccess || k.max_parts <= 1) return e;
+  int kt = 0, rows = 0;
+  prefill_shape(p->dtype, p->head_dim, &kt, &rows);
+  k.row_blocks = (a.max_q_len * R + rows - 1) / rows;
+  switch (p->head_dim) {
+    case 64: return pmerge<64>(k, R, rows, p->dtype, stream);
+    case 128: return pmerge<128>(k, R, rows, p->dtype, stream);
+    default: return pmerge<256>(k, R, rows, p->dtype, stream);
+  }
 }
 
 }  // namespace pkv

@@ -317,6 +317,16 @@ class PagedKvCache:
     def reserve_decode(self, batch: int, n_head: int, max_context_len: int) -> None:
         check(lib().pkv_pool_reserve_decode(self._h, batch, n_head, max_context_len), self._h)
 
+    def prefill_workspace_bytes(self, n_seqs: int, n_head: int, max_q_len: int,
+                                max_context_len: int) -> int:
+        return int(lib().pkv_prefill_workspace_bytes(self._h, n_seqs, n_head, max_q_len,
+                                                     max_context_len))
+
+    def reserve_prefill(self, n_seqs: int, n_head: int, max_q_len: int,
+                        max_context_len: int) -> None:
+        check(lib().pkv_pool_reserve_prefill(self._h, n_seqs, n_head, max_q_len,
+                                             max_context_len), self._h)
+
     # raw byte access (synchronous), for tests and checkpoints
     def read_bytes(self, layer: int, which: int, offset: int = 0, nbytes: int | None = None):
         import numpy as np

@@ -51,6 +51,8 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_prefill_attention": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                    ctypes.c_float, _P]),
     "pkv_pool_check": (_I, [_P]),
+    "pkv_prefill_workspace_bytes": (_SZ, [_P, _I, _I, _I, _I]),
+    "pkv_pool_reserve_prefill": (_I, [_P, _I, _I, _I, _I]),
     "pkv_rope_tables_host": (_I, [_I, ctypes.c_float, _I, _P, _P]),
     "pkv_rope_create": (_I, [ctypes.POINTER(_P), _I, ctypes.c_float, _I, _I]),
     "pkv_rope_destroy": (_I, [_P]),

@@ -189,6 +189,16 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_seqs, int max_q_len, int max_context_len,
                           int n_head, float scale, void* stream);
 
+/* Workspace of pkv_prefill_attention for the given launch shape: launches
+ * with few row blocks (fewer than can fill the GPU) split long key ranges
+ * into parts that are merged afterwards, with partial results in the pool's
+ * workspace (0: no split).  The pool grows the workspace on demand;
+ * callers that must not allocate later reserve it up front. */
+size_t pkv_prefill_workspace_bytes(const pkv_pool* pool, int n_seqs, int n_head,
+                                   int max_q_len, int max_context_len);
+int pkv_pool_reserve_prefill(pkv_pool* pool, int n_seqs, int n_head,
+                             int max_q_len, int max_context_len);
+
 /* ---- rotary position embedding (crates/ai-engine-candle/src/paged/rope.rs,
  * applied per row in the decode step, transformer.rs:252-269) ---------------
  * Tables as Rope::new (rope.rs:14-23): theta_i = 1 / freq_base^(2 i / rope_dim)

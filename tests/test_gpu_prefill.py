@@ -179,3 +179,35 @@ def test_tinyllama_chunked_prefill_shape(gpu):
     c = PCase(gpu, wl.F16, 32, 4, 64, 16, priors, [256] * 4, seed=77)
     _close(c.run(out_dtype=torch.float16), c.reference(), "tinyllama prefill")
     c.close()
+
+
+@pytest.mark.parametrize("dt,hd,R", [(wl.F16, 64, 8), (wl.BF16, 128, 4), (wl.BF16, 256, 2),
+                                     (wl.F32, 64, 4), (wl.F32, 128, 1), (wl.BF16, 64, 2)])
+def test_long_prior_split_into_parts(gpu, dt, hd, R):
+    # Priors beyond the part length split a row block's keys into parts run
+    # by separate workgroups and merged afterwards (launches with few row
+    # blocks); parts end on the prior, so the causal diagonal stays in the
+    # last part.  Priors on and next to part boundaries, one-token chunks,
+    # chunks of several row blocks, and a short sequence that is not split.
+    KVH = 2
+    priors = [4100, 1023, 1024, 2048, 1500, 20, 2600]
+    chunks = [37, 1, 130, 64, 7, 90, 1]
+    c = PCase(gpu, dt, R * KVH, KVH, hd, 16, priors, chunks, seed=hd + R + dt)
+    pool_bytes = c.cache.prefill_workspace_bytes(len(priors), R * KVH, max(chunks),
+                                                 int(c.ctx.max()))
+    assert pool_bytes > 0  # this launch is split
+    out_dtype = torch.float32 if dt == wl.F32 else TD[dt]
+    _close(c.run(out_dtype=out_dtype), c.reference(), f"split dt={dt} hd={hd} R={R}")
+    c.close()
+
+
+def test_split_workspace_reserved_up_front(gpu):
+    # a reserved workspace is used as is (no growth inside the call), and a
+    # launch with many row blocks is not split at all
+    c = PCase(gpu, wl.BF16, 8, 2, 128, 16, [3000, 700], [50, 20], seed=3)
+    need = c.cache.prefill_workspace_bytes(2, 8, 50, int(c.ctx.max()))
+    c.cache.reserve_prefill(2, 8, 50, int(c.ctx.max()))
+    _close(c.run(), c.reference(), "reserved split")
+    assert c.cache.prefill_workspace_bytes(512, 8, 2048, 8192) == 0
+    assert need > 0
+    c.close()
