@@ -405,11 +405,32 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     agree = bool(np.all(np.abs(gpu0 - res) <= 1e-3 + 2e-2 * np.abs(res)))
     log(f"[bench] cpu baseline: {dt:.2f} s/layer -> {batch.batch / step_s:.1f} tok/s "
         f"(gpu/cpu layer-0 agreement: {agree})")
-    return {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads,
+    res_cpu = {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
+                          f"{passes} passes of {dt * 1e3:.1f} ms, scaled x{shape.n_layers} layers"),
+               "agrees_with_gpu": agree}
+    # The reference's own costs where they fit in a bounded sample: an f32
+    # pool, a full K and V pool copy per appended row (slice_assign), then
+    # gather / pad / GQA repeat / masked SDPA, one thread.
+    if kp.size * 4 <= (256 << 20):
+        kf = wl.widen(kp, shape.dtype).reshape(shp).astype(np.float32)
+        vf = wl.widen(vp, shape.dtype).reshape(shp).astype(np.float32)
+        qf, knf, vnf = (wl.widen(x, shape.dtype).astype(np.float32) for x in (qh, knh, vnh))
+        seq = (cl - 1).astype(np.int64)
+        fdt, fpasses, _ = timed_passes(
+            lambda: oracle.decode_step_faithful_f32(kf, vf, shape.block_size, tables, seq, seq,
+                                                    qf, knf, vnf, scale), args)
+        fstep = fdt * shape.n_layers
+        log(f"[bench] cpu reference-faithful: {fdt:.2f} s/layer -> "
+            f"{batch.batch / fstep:.2f} tok/s")
+        res_cpu["reference_faithful"] = {
+            "value": round(batch.batch / fstep, 3), "unit": "tok/s", "cores": 1,
             "kind": "port",
-            "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
-                       f"{passes} passes of {dt * 1e3:.1f} ms, scaled x{shape.n_layers} layers"),
-            "agrees_with_gpu": agree}
+            "sample": (f"layer 0, f32 pool of {kp.size * 4 >> 20} MiB per K, a full K and V pool "
+                       f"copy per appended row (slice_assign) then gather/pad/mask/sdpa, "
+                       f"{fpasses} passes of {fdt * 1e3:.0f} ms, scaled x{shape.n_layers} layers")}
+    return res_cpu
 
 
 def mix(args, dev) -> int:

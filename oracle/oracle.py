@@ -57,6 +57,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_decode_step_f32.argtypes = [_P, _P, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P, _P, _P,
                                       _SZ, _SZ, ctypes.c_float, _P]
     L.orc_decode_step_f32.restype = ctypes.c_int
+    L.orc_decode_step_faithful_f32.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P,
+                                               _P, _P, _SZ, _SZ, ctypes.c_float, _P]
+    L.orc_decode_step_faithful_f32.restype = ctypes.c_int
     L.orc_paged_attention_f64.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P,
                                           _SZ, _SZ, ctypes.c_double, _P]
     L.orc_paged_attention_f64.restype = None
@@ -185,6 +188,30 @@ def sdpa_f32(q, k, v, mask, n_head: int, n_kv_head: int, scale: float | None = N
     out = np.empty((B, Lq, H * hd), dtype=np.float32)
     lib().orc_sdpa_f32(_p(q), _p(k), _p(v), _p(mask), B, H, n_kv_head, Lq, kv, hd,
                        float(scale), _p(out))
+    return out
+
+
+def decode_step_faithful_f32(k_pool, v_pool, block_size: int, tables, seq_lens, positions,
+                             q, k_new, v_new, scale: float | None = None) -> np.ndarray:
+    """decode_step_f32 with the reference's cost: every appended row copies
+    the whole K and V pool first (slice_assign, attention.rs:73-80)."""
+    assert k_pool.dtype == np.float32 and v_pool.dtype == np.float32
+    NB, KVH, hd = k_pool.shape[0], k_pool.shape[2], k_pool.shape[3]
+    tables = np.ascontiguousarray(tables, dtype=np.uint32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int64)
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k_new = np.ascontiguousarray(k_new, dtype=np.float32)
+    v_new = np.ascontiguousarray(v_new, dtype=np.float32)
+    B, H = q.shape[0], q.shape[1]
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.empty((B, H * hd), dtype=np.float32)
+    rc = lib().orc_decode_step_faithful_f32(_p(k_pool), _p(v_pool), NB, block_size, KVH, hd,
+                                            _p(tables), tables.shape[1], _p(sl), _p(pos), _p(q),
+                                            _p(k_new), _p(v_new), B, H, float(scale), _p(out))
+    if rc:
+        raise IndexError("position beyond block table" if rc == -1 else "allocation failed")
     return out
 
 

@@ -28,7 +28,8 @@
  *                           dominant key -> its V row), mutation checks.
  *   orc_decode_step_f32   - equals orc_paged_attention_f64 on ragged inputs
  *                           (padding invariance) and orc_sdpa_f32 on the
- *                           gathered inputs.
+ *                           gathered inputs; orc_decode_step_faithful_f32
+ *                           gives the same bits (it only adds the copies).
  *   orc_prefill_*         - reduces to the reference prefill mask (P = 0), to
  *                           decode (one query), chunk-split invariance, and
  *                           brute-force torch float64 on tiny inputs.
@@ -270,6 +271,49 @@ int orc_decode_step_f32(float* k_pool, float* v_pool, size_t bs, size_t KVH,
     free(v_all);
     free(gk);
     free(gv);
+    return rc;
+}
+
+/* The reference's cost model (CPU baseline variant "reference-faithful"):
+ * KvPool::write assigns each row with candle's slice_assign, which builds a
+ * new full pool tensor (attention.rs:73-80), so every appended row first
+ * copies the whole K pool and the whole V pool.  The copies go to a second
+ * buffer that then becomes the pool; the attention is orc_decode_step_f32's
+ * (write -> gather -> pad -> mask -> sdpa).  The pools hold the result. */
+int orc_decode_step_faithful_f32(float* k_pool, float* v_pool, size_t num_blocks,
+                                 size_t bs, size_t KVH, size_t hd,
+                                 const uint32_t* tables, size_t max_nb,
+                                 const int64_t* seq_lens, const int64_t* positions,
+                                 const float* q, const float* k_new,
+                                 const float* v_new, size_t B, size_t H,
+                                 float scale, float* out) {
+    const size_t bytes = num_blocks * bs * KVH * hd * sizeof(float);
+    float* kbuf = (float*)malloc(bytes);
+    float* vbuf = (float*)malloc(bytes);
+    if (!kbuf || !vbuf) {
+        free(kbuf);
+        free(vbuf);
+        return -2;
+    }
+    float *kc = k_pool, *vc = v_pool, *ko = kbuf, *vo = vbuf;
+    const size_t row = KVH * hd;
+    int rc = 0;
+    for (size_t b = 0; b < B && rc == 0; b++) {
+        float* t;
+        memcpy(ko, kc, bytes);
+        t = kc; kc = ko; ko = t;
+        memcpy(vo, vc, bytes);
+        t = vc; vc = vo; vo = t;
+        rc = orc_kv_write(kc, vc, 4, bs, KVH, hd, tables + b * max_nb, max_nb,
+                          (size_t)seq_lens[b], k_new + b * row, v_new + b * row, 1);
+    }
+    if (rc == 0)
+        rc = orc_decode_step_f32(kc, vc, bs, KVH, hd, tables, max_nb, seq_lens, positions,
+                                 q, k_new, v_new, B, H, scale, out);
+    if (kc != k_pool) memcpy(k_pool, kc, bytes);
+    if (vc != v_pool) memcpy(v_pool, vc, bytes);
+    free(kbuf);
+    free(vbuf);
     return rc;
 }
 

@@ -242,6 +242,22 @@ def test_decode_step_f32_matches_closed_form(B, H, KVH, hd, bs):
     np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)
 
 
+def test_decode_step_faithful_equals_in_place():
+    # the reference-faithful cost model (a full pool copy per appended row)
+    # leaves the same pool bytes and output bits as the in-place restatement
+    B, H, KVH, hd, bs = 4, 8, 2, 16, 16
+    ctx, tables, kp, vp = _random_paged(21, B, KVH, hd, bs, 90)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((B, H, hd)).astype(np.float32)
+    kn = rng.standard_normal((B, KVH, hd)).astype(np.float32)
+    vn = rng.standard_normal((B, KVH, hd)).astype(np.float32)
+    k2, v2 = kp.copy(), vp.copy()
+    a = oracle.decode_step_f32(kp, vp, bs, tables, ctx, ctx, q, kn, vn)
+    b = oracle.decode_step_faithful_f32(k2, v2, bs, tables, ctx, ctx, q, kn, vn)
+    assert np.array_equal(a, b)
+    assert np.array_equal(kp, k2) and np.array_equal(vp, v2)
+
+
 def test_paged_attention_f64_matches_torch_on_gathered():
     B, H, KVH, hd, bs = 3, 8, 2, 16, 16
     ctx, tables, kp, vp = _random_paged(5, B, KVH, hd, bs, 50, wl.BF16)
