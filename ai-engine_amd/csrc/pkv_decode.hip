@@ -691,6 +691,19 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int c = lane % LPR;  // 16-byte chunk of the row
   const float* pob = a.part_o + ((size_t)pair * a.max_parts * R + h) * HD + 4 * c;
 
+  // The first PPI * kMergeUnroll partial rows are loaded together with the
+  // (m, l) pairs, before the reductions that weight them: one memory round
+  // trip for the partition counts of small launches instead of two.
+  f32x4 ov0[kMergeUnroll];
+  float mv0[kMergeUnroll];
+#pragma unroll
+  for (int u = 0; u < kMergeUnroll; ++u) {
+    const int pp = u * PPI + q;
+    const bool ok = pp < n_parts;
+    ov0[u] = ok ? *reinterpret_cast<const f32x4*>(pob + (size_t)pp * pstride_o)
+                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    mv0[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
+  }
   float M = -INFINITY;
   for (int p0 = 0; p0 < n_parts; p0 += kWave)
     if (p0 + lane < n_parts) M = fmaxf(M, mlb[(size_t)(p0 + lane) * pstride_ml]);
@@ -706,7 +719,13 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   L = wave_sum_f(L);
 
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int p0 = 0; p0 < n_parts; p0 += PPI * kMergeUnroll) {
+#pragma unroll
+  for (int u = 0; u < kMergeUnroll; ++u) {
+    const float w = fast_exp2(mv0[u] - M);  // 0 for absent rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, ov0[u][i], acc[i]);
+  }
+  for (int p0 = PPI * kMergeUnroll; p0 < n_parts; p0 += PPI * kMergeUnroll) {
     f32x4 ov[kMergeUnroll];
     float mv[kMergeUnroll];
 #pragma unroll
