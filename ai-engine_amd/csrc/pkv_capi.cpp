@@ -733,6 +733,8 @@ int pkv_sample(const void* logits, int dtype, long long row_stride, int batch, i
     return fail(nullptr, PKV_ERR_INVALID, "sample: row_stride %lld < vocab %d", row_stride, vocab);
   if (reinterpret_cast<uintptr_t>(logits) % pkv::dtype_bytes(dtype))
     return fail(nullptr, PKV_ERR_INVALID, "sample: logits not aligned to the element size");
+  if ((reinterpret_cast<uintptr_t>(temperatures) | reinterpret_cast<uintptr_t>(tokens)) % 4)
+    return fail(nullptr, PKV_ERR_INVALID, "sample: temperatures and tokens must be 4-byte aligned");
   if (top_k < 0)
     return fail(nullptr, PKV_ERR_INVALID, "sample: top_k %d < 0 (0 is None)", top_k);
   hipError_t e = pkv::launch_sample(logits, dtype, row_stride, batch, vocab, temperatures,

@@ -149,6 +149,31 @@ __device__ __forceinline__ uint32_t order_key(float y) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// The float whose order_key is k (keys of +0 map back to +0).
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Logits x whose y = fl(x / T) can have a key in [kmin, kmax]: y then lies
+// within one ulp of [ya, yb], so x / T does too, and x lies in the product of
+// that range with T (exact in double), rounded outwards to float.  A test
+// against the interval rejects other elements without the division; the
+// few it admits are checked exactly.
+struct XRange {
+  float lo, hi;
+};
+__device__ __forceinline__ XRange x_range(uint32_t kmin, uint32_t kmax, float T) {
+  const float ya = nextafterf(key_value(kmin), -INFINITY);
+  const float yb = nextafterf(key_value(kmax), INFINITY);
+  double a = (double)ya * (double)T, b = (double)yb * (double)T;
+  if (a > b) {
+    const double t = a;
+    a = b;
+    b = t;
+  }
+  return XRange{nextafterf((float)a, -INFINITY), nextafterf((float)b, INFINITY)};
+}
+
 // exp(d) for d = y - max y <= 0, in 2^-40 units.
 __device__ __forceinline__ unsigned long long mass_of(float d) {
   const float e = expf(d);
@@ -293,7 +318,9 @@ __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long 
       sm.minidx[b] = INT_MAX;
     }
     __syncthreads();
+    const XRange xr = x_range(prefix, prefix | ~pmask, rw.T);
     for_each<DT, VEC>(rw.x, rw.V, [&](int i, float x) {
+      if (!(x >= xr.lo && x <= xr.hi)) return;
       const float y = x / rw.T;
       const uint32_t key = order_key(y);
       if ((key & pmask) != prefix) return;
@@ -425,9 +452,15 @@ __global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
   }
 
   Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
-  float ym = -INFINITY;
-  for_each<DT, VEC>(x, V, [&](int, float v) { ym = fmaxf(ym, v / T); });
-  rw.ymax = block_max(sm, ym);
+  // max of fl(x / T): correctly rounded division is monotone in x, so it is
+  // the largest logit (T > 0) or the smallest (T < 0) divided by T
+  float xm = -INFINITY;
+  if (T > 0.0f)
+    for_each<DT, VEC>(x, V, [&](int, float v) { xm = fmaxf(xm, v); });
+  else
+    for_each<DT, VEC>(x, V, [&](int, float v) { xm = fmaxf(xm, -v); });
+  xm = block_max(sm, xm);
+  rw.ymax = (T > 0.0f ? xm : -xm) / T;
 
   if (a.top_k > 0 && a.top_k < V) {
     // the k-th largest key, and how many of its ties the first k include
