@@ -59,7 +59,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample"])
+    ap.add_argument("--config", default="cfg3",
+                    choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample", "gather"])
     ap.add_argument("--rope", action="store_true",
                     help="decode configs: q and the new k/v arrive in f32 before the rotary "
                          "embedding, which the decode kernel applies (pkv_decode_attention_rope)")
@@ -101,6 +102,8 @@ def main() -> int:
         return mix(args, dev)
     if args.config == "sample":
         return sample_bench(args, dev)
+    if args.config == "gather":
+        return gather_bench(args, dev)
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
     L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
@@ -274,6 +277,106 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    cache.close()
+    return 0
+
+
+def gather_bench(args, dev) -> int:
+    """KvPool::gather_seq (attention.rs:85-97), the per-row gather of the
+    reference's decode step (transformer.rs:277), on cfg3's layer shape: the
+    K and V rows of each of the 256 sequences (ctx + 1 tokens) copied out of
+    the pool in table order by pkv_gather_seq, one call per sequence, the
+    256 calls replayed as a HIP graph.  value = GB/s of read + written bytes;
+    checked bit-exact against the oracle on a sample of sequences."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import pagedkv
+    from pagedkv import workload as wl
+
+    shape = wl.CFG3
+    B, bs, KVH, hd = 256, shape.block_size, shape.n_kv_head, shape.head_dim
+    batch = wl.decode_batch(shape, B, 512, 4096, args.seed)
+    cache = pagedkv.PagedKvCache(1, batch.num_blocks, bs, KVH, hd, torch.bfloat16)
+    cache.fill_normal(args.seed)
+    lens = (batch.ctx + 1).astype(np.int64)
+    tables = [torch.from_numpy(np.ascontiguousarray(batch.tables[b, :-(-int(lens[b]) // bs)]))
+              .to(dev) for b in range(B)]
+    outs = [(torch.empty((int(n), KVH, hd), dtype=torch.bfloat16, device=dev),
+             torch.empty((int(n), KVH, hd), dtype=torch.bfloat16, device=dev)) for n in lens]
+    lib = pagedkv.lib()
+    h = cache.handle
+
+    def calls(sp):
+        for b in range(B):
+            rc = lib.pkv_gather_seq(h, 0, tables[b].data_ptr(), int(lens[b]),
+                                    outs[b][0].data_ptr(), outs[b][1].data_ptr(), sp)
+            if rc:
+                pagedkv._lib.check(rc, h)
+
+    cap = torch.cuda.Stream(dev)
+    gr = torch.cuda.CUDAGraph()
+    calls(int(torch.cuda.current_stream(dev).cuda_stream) or None)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr, stream=cap):
+        calls(int(torch.cuda.current_stream(dev).cuda_stream))
+    for _ in range(max(1, args.warmup)):
+        gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    cache.check()
+    ms = e0.elapsed_time(e1) / args.steps
+    row = KVH * hd * 2
+    gbytes = int(lens.sum()) * row * 2 * 2  # K and V rows, read and written
+    # bit-exact against the oracle's closed form on a sample of sequences
+    nd = np.uint16
+    kp = cache.read_bytes(0, pagedkv.K).view(nd).reshape(batch.num_blocks, bs, KVH, hd)
+    vp = cache.read_bytes(0, pagedkv.V).view(nd).reshape(batch.num_blocks, bs, KVH, hd)
+    ok = True
+    for b in range(0, B, 51):
+        rk, rv = oracle.gather_seq(kp, vp, bs, batch.tables[b].astype(np.uint32), int(lens[b]))
+        gk = outs[b][0].cpu().view(torch.int16).numpy().view(np.uint16)
+        gv = outs[b][1].cpu().view(torch.int16).numpy().view(np.uint16)
+        ok &= np.array_equal(gk, rk) and np.array_equal(gv, rv)
+    log(f"[bench] gather: {B} sequences, {int(lens.sum())} rows, {ms * 1e3:.1f} us per step "
+        f"({gbytes / (ms / 1e3) / 1e9:.0f} GB/s), oracle bit-exact: {ok}")
+    if not ok:
+        print(json.dumps({"error": "gather differs from the oracle"}))
+        return 1
+    cpu = None
+    if args.cpu_layers > 0:
+        tb = batch.tables.astype(np.uint32)
+        rows = iter(range(1 << 30))
+        per, n, _ = timed_passes(
+            lambda: [oracle.gather_seq(kp, vp, bs, tb[b], int(lens[b]))
+                     for b in [next(rows) % B]], args)
+        mean_b = gbytes / B
+        cpu = {"value": round(mean_b / per / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"oracle gather_seq (closed-form index copy) of one sequence per pass, "
+                         f"{n} passes of {per * 1e3:.2f} ms"}
+    res = {
+        "metric": "KvPool::gather_seq GB/s (read + written), Llama-3-8B layer shape, 1 GPU",
+        "value": round(gbytes / (ms / 1e3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool, random block tables)",
+        "config": {"workload": f"gather: {B} sequences of cfg3 (ctx U[512, 4096]), one layer, "
+                               f"8 kv heads x hd 128, bs 16, one call per sequence in a HIP graph",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbytes / (ms / 1e3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "pkv::gather_kernel", "kernel_avg_us": round(ms * 1e3 / B, 2),
+                     "algorithmic_bytes_per_launch": gbytes // B},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
     cache.close()
     return 0
 
