@@ -89,6 +89,7 @@ class Scheduler:
         _check(lib().pkv_sched_create(ctypes.byref(h), ctypes.byref(cfg)))
         self._h = h
         self.block_size = block_size
+        self.kv_cache_blocks = kv_cache_blocks
 
     def __del__(self) -> None:
         h = getattr(self, "_h", None)
@@ -135,7 +136,8 @@ class Scheduler:
         return int(c.value)
 
     def compact(self):
-        n_cap = 1 << 20
+        """Renumber live blocks to [0, live) -> (src, dst) moves for pkv_compact."""
+        n_cap = max(1, self.kv_cache_blocks)  # at most one move per block
         src = np.zeros(n_cap, np.int32)
         dst = np.zeros(n_cap, np.int32)
         n = ctypes.c_int()

@@ -293,3 +293,31 @@ def test_compact_moves_live_blocks_to_prefix():
         s.complete([30] * p.n_producing)
         p = s.step()
     assert s.table(nid)[0] == [len(live)]
+
+
+def test_api_misuse_is_reported():
+    from pagedkv import PagedKvError
+    with pytest.raises(PagedKvError):
+        Scheduler(0, 16, 8, 100, EOS)             # no sequences allowed
+    s = Scheduler(2, 16, 8, 100, EOS)
+    with pytest.raises(PagedKvError):
+        s.complete([1])                           # no plan is open
+    with pytest.raises(PagedKvError):
+        s.submit(-1, 4)
+    a = s.submit(5, 4)
+    p = s.step()
+    with pytest.raises(PagedKvError):
+        s.step()                                  # the open plan must be completed first
+    with pytest.raises(PagedKvError):
+        s.fork(a, 3)                              # not while a plan is open
+    with pytest.raises(PagedKvError):
+        s.complete([1, 2])                        # one token per producing row
+    s.complete([9] * p.n_producing)
+    with pytest.raises(PagedKvError):
+        s.fork(12345, 3)                          # not a live sequence
+    b = s.fork(a, 3)
+    with pytest.raises(PagedKvError):
+        s.fork(a, 3)                              # max_num_seqs reached
+    with pytest.raises(PagedKvError):
+        s.table(999)
+    assert s.counts()[0] == 2 and b != a
