@@ -364,6 +364,39 @@ int pkv_append(pkv_pool* p, int layer, const void* k, const void* v,
   return PKV_OK;
 }
 
+int pkv_append_rope(pkv_pool* p, int layer, const pkv_rope* rope, const int32_t* positions,
+                    int in_dtype, const void* k, const void* v, const int32_t* slot_mapping,
+                    int n_tokens, const void* q, void* q_out, int n_head, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (!rope) return fail(p, PKV_ERR_INVALID, "rope is NULL");
+  if (rope->rope_dim != p->head_dim)
+    return fail(p, PKV_ERR_INVALID, "rope_dim %d != head_dim %d", rope->rope_dim, p->head_dim);
+  if (rope->device != p->device)
+    return fail(p, PKV_ERR_INVALID, "rope tables on device %d, pool on device %d", rope->device,
+                p->device);
+  if (in_dtype != PKV_F32 && in_dtype != PKV_F16 && in_dtype != PKV_BF16)
+    return fail(p, PKV_ERR_INVALID, "in_dtype %d", in_dtype);
+  if (n_tokens < 0) return fail(p, PKV_ERR_INVALID, "n_tokens %d < 0", n_tokens);
+  if (!q != !q_out) return fail(p, PKV_ERR_INVALID, "q and q_out must both be given or both NULL");
+  if (q && (n_head <= 0 || n_head % p->n_kv_head != 0))
+    return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head,
+                p->n_kv_head);
+  if (q && q == q_out && in_dtype != p->dtype)
+    return fail(p, PKV_ERR_INVALID, "q_out may alias q only when in_dtype is the pool dtype");
+  if (n_tokens == 0) return PKV_OK;
+  if (!k || !v || !slot_mapping || !positions)
+    return fail(p, PKV_ERR_INVALID, "k, v, slot_mapping and positions must be non-NULL");
+  if (!aligned16(k) || !aligned16(v) || (q && (!aligned16(q) || !aligned16(q_out))))
+    return fail(p, PKV_ERR_INVALID, "k, v, q and q_out must be 16-byte aligned");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_append_rope(p, layer, rope, positions, in_dtype, k, v, slot_mapping,
+                                         n_tokens, q, q_out, n_head,
+                                         static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "append_rope launch");
+  return PKV_OK;
+}
+
 int pkv_gather_seq(pkv_pool* p, int layer, const int32_t* block_table, int len,
                    void* out_k, void* out_v, void* stream) {
   CHECK_POOL(p);

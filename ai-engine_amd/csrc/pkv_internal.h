@@ -104,6 +104,10 @@ void rope_tables_host(int rope_dim, float freq_base, int max_seq, float* cos_t,
 hipError_t launch_rope_apply(const pkv_rope* r, const void* x, int in_dtype,
                              void* out, int out_dtype, const int32_t* positions,
                              int n_tokens, int n_head, hipStream_t stream);
+hipError_t launch_append_rope(const pkv_pool* p, int layer, const pkv_rope* r,
+                              const int32_t* positions, int in_dtype, const void* k,
+                              const void* v, const int32_t* slots, int n_tokens,
+                              const void* q, void* q_out, int n_head, hipStream_t stream);
 
 struct DecodeArgs {
   const void* q;

@@ -96,7 +96,100 @@ __global__ void __launch_bounds__(kRopeThreads)
   store4(orow, e + half, out_dt, o2);
 }
 
+// Prefill glue in one pass (prefill_seq, transformer.rs:160-174): rows of
+// token t are its n_kv k rows (rotated, stored at pool slot slots[t]), its
+// n_kv v rows (stored as they are) and, when q is given, its n_head q rows
+// (rotated, stored to q_out); all converted from in_dt to the pool dtype.
+// One thread per (token, row, 4 element pairs).  slots[t] < 0 is a padding
+// token: its k/v rows are skipped, its q rows still rotated.
+__global__ void __launch_bounds__(kRopeThreads)
+    append_rope_kernel(const char* __restrict__ k, const char* __restrict__ v,
+                       const char* q, char* q_out, int in_dt, char* __restrict__ kp,
+                       char* __restrict__ vp, int pool_dt, const int32_t* __restrict__ slots,
+                       long long n_slots, const float* __restrict__ cos_t,
+                       const float* __restrict__ sin_t, const int32_t* __restrict__ positions,
+                       int n_tokens, int n_kv, int n_q, int d, int max_seq, uint32_t* err) {
+  const int half = d / 2;
+  const int groups = half / 4;
+  const int rows = 2 * n_kv + n_q;
+  const long long i = (long long)blockIdx.x * kRopeThreads + threadIdx.x;
+  if (i >= (long long)n_tokens * rows * groups) return;
+  const int gi = (int)(i % groups);
+  const long long tr = i / groups;
+  const int t = (int)(tr / rows);
+  const int r = (int)(tr - (long long)t * rows);
+  const int e = 4 * gi;
+  const size_t ib = in_dt == PKV_F32 ? 4 : 2, pb = pool_dt == PKV_F32 ? 4 : 2;
+  const char* src;
+  char* dst;
+  bool rotate = true;
+  if (r < 2 * n_kv) {
+    const int s = slots[t];
+    if (s < 0) return;
+    if (s >= n_slots) {
+      if (gi == 0) atomicOr(err, PKV_EBIT_SLOT);
+      return;
+    }
+    const int h = r < n_kv ? r : r - n_kv;
+    const size_t in_row = (size_t)t * n_kv + h;
+    const size_t pool_row = (size_t)s * n_kv + h;
+    if (r < n_kv) {
+      src = k + in_row * d * ib;
+      dst = kp + pool_row * d * pb;
+    } else {
+      src = v + in_row * d * ib;
+      dst = vp + pool_row * d * pb;
+      rotate = false;
+    }
+  } else {
+    const size_t row = (size_t)t * n_q + (r - 2 * n_kv);
+    src = q + row * d * ib;
+    dst = q_out + row * d * pb;
+  }
+  f32x4 x1 = load4(src, e, in_dt);
+  f32x4 x2 = load4(src, e + half, in_dt);
+  if (rotate) {
+    const int pos = positions[t];
+    if (pos < 0 || pos >= max_seq) {
+      if (gi == 0) atomicOr(err, PKV_EBIT_POSITION);
+      return;
+    }
+    const f32x4 c = *reinterpret_cast<const f32x4*>(cos_t + (size_t)pos * half + e);
+    const f32x4 s = *reinterpret_cast<const f32x4*>(sin_t + (size_t)pos * half + e);
+    f32x4 o1, o2;
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o1[j] = x1[j] * c[j] - x2[j] * s[j];
+        o2[j] = x1[j] * s[j] + x2[j] * c[j];
+      }
+    }
+    x1 = o1;
+    x2 = o2;
+  }
+  store4(dst, e, pool_dt, x1);
+  store4(dst, e + half, pool_dt, x2);
+}
+
 }  // namespace
+
+hipError_t launch_append_rope(const pkv_pool* p, int layer, const pkv_rope* r,
+                              const int32_t* positions, int in_dtype, const void* k,
+                              const void* v, const int32_t* slots, int n_tokens, const void* q,
+                              void* q_out, int n_head, hipStream_t stream) {
+  const int n_q = q ? n_head : 0;
+  const long long threads =
+      (long long)n_tokens * (2 * p->n_kv_head + n_q) * (p->head_dim / 8);
+  if (threads <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((threads + kRopeThreads - 1) / kRopeThreads);
+  append_rope_kernel<<<grid, kRopeThreads, 0, stream>>>(
+      static_cast<const char*>(k), static_cast<const char*>(v), static_cast<const char*>(q),
+      static_cast<char*>(q_out), in_dtype, p->layer_k(layer), p->layer_v(layer), p->dtype, slots,
+      (long long)p->num_blocks * p->block_size, r->cos, r->sin, positions, n_tokens,
+      p->n_kv_head, n_q, p->head_dim, r->max_seq, p->err);
+  return hipGetLastError();
+}
 
 hipError_t launch_rope_apply(const pkv_rope* r, const void* x, int in_dtype, void* out,
                              int out_dtype, const int32_t* positions, int n_tokens, int n_head,

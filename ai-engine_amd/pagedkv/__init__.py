@@ -371,6 +371,43 @@ class KvPool:
         check(lib().pkv_append(self._h, self.layer_index, _dev_ptr(k), _dev_ptr(v),
                                _dev_ptr(sm), k.shape[0], _stream_ptr(stream)), self._h)
 
+    def append_rope(self, rope: "Rope", k, v, slot_mapping, positions, q=None, q_out=None,
+                    stream=None):
+        """prefill_seq's glue (transformer.rs:160-174) in one launch: rotate k
+        (n, n_kv, hd) by `positions`, store it and v at `slot_mapping`, and,
+        with q (n, H, hd), return q rotated into the pool dtype (into q_out if
+        given).  k, v, q share one dtype: float32 or the pool dtype."""
+        import torch
+        c = self.cache
+        n = int(k.shape[0])
+        if q is not None and q.dtype != k.dtype:
+            raise TypeError("q must have k's dtype")
+        if k.dtype not in (torch.float32, c.dtype) or v.dtype != k.dtype:
+            raise TypeError("k and v must be float32 or the pool dtype, and equal")
+        for t, name in ((k, "k"), (v, "v")):
+            if t.shape != (n, c.n_kv_head, c.head_dim) or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous ({n}, {c.n_kv_head}, {c.head_dim})")
+        sm = _i32(slot_mapping, c.device)
+        pos = _i32(positions, c.device)
+        if sm.numel() != n or pos.numel() != n:
+            raise ValueError("slot_mapping / positions / k lengths differ")
+        H = 0
+        if q is not None:
+            if q.dim() != 3 or q.shape[0] != n or q.shape[2] != c.head_dim:
+                raise ValueError(f"q must be ({n}, H, {c.head_dim})")
+            q = q.contiguous()
+            H = int(q.shape[1])
+            if q_out is None:
+                q_out = torch.empty(q.shape, dtype=c.dtype, device=c.device)
+            if q_out.dtype != c.dtype or q_out.shape != q.shape or not q_out.is_contiguous():
+                raise ValueError("q_out must be contiguous, q's shape, in the pool dtype")
+        check(lib().pkv_append_rope(
+            self._h, self.layer_index, rope.handle, _dev_ptr(pos), pkv_dtype(k.dtype),
+            _dev_ptr(k), _dev_ptr(v), _dev_ptr(sm), n,
+            _dev_ptr(q) if q is not None else None,
+            _dev_ptr(q_out) if q is not None else None, H, _stream_ptr(stream)), self._h)
+        return q_out if q is not None else None
+
     # -- KvPool::gather_seq (attention.rs:85-97) ----------------------------
     def gather_seq(self, table, length: int, stream=None):
         import torch

@@ -62,8 +62,10 @@ def main() -> int:
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample", "gather"])
     ap.add_argument("--rope", action="store_true",
-                    help="decode configs: q and the new k/v arrive in f32 before the rotary "
-                         "embedding, which the decode kernel applies (pkv_decode_attention_rope)")
+                    help="decode configs and cfg2: q and the new k/v arrive in f32 before the "
+                         "rotary embedding, which the decode kernel applies "
+                         "(pkv_decode_attention_rope) and the chunk store applies to k and q "
+                         "(pkv_append_rope)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="minimum layer passes of the CPU baseline sample (0 = skip it)")
@@ -569,8 +571,13 @@ def mix(args, dev) -> int:
         return (torch.randn(shp, generator=g, device=dev, dtype=torch.float32) * sc).to(tdt)
 
     sc = 1.0 / math.sqrt(hd)
+    # with --rope the inputs are the f32 projections before rotation (the
+    # reference's activations) and the rotary embedding is part of the step
     qp, kc, vc = rnd(L, T, H, hd, sc=sc), rnd(L, T, KVH, hd), rnd(L, T, KVH, hd)
     qd, kd, vd = rnd(L, ND, H, hd, sc=sc), rnd(L, ND, KVH, hd), rnd(L, ND, KVH, hd)
+    if args.rope:
+        qp, kc, vc, qd, kd, vd = (t.float() for t in (qp, kc, vc, qd, kd, vd))
+        qrot = torch.empty((T, H, hd), dtype=tdt, device=dev)
     outp = torch.empty((L, T, H * hd), dtype=tdt, device=dev)
     outd = torch.empty((L, ND, H * hd), dtype=tdt, device=dev)
     tables = np.where(m.tables < 0, 0, m.tables).astype(np.int32)
@@ -584,6 +591,11 @@ def mix(args, dev) -> int:
     max_p, max_d = int(pctx_np.max()), int(dctx_np.max())
     mbps = tables.shape[1]
     cache.reserve_decode(ND, H, max_d)
+    rope = None
+    if args.rope:
+        rope = pagedkv.Rope(hd, 10000.0, max(max_p, max_d) + 1)
+        ppos = torch.from_numpy(np.concatenate(
+            [np.arange(p, p + c, dtype=np.int32) for p, c in zip(m.prior, m.chunk)])).to(dev)
     torch.cuda.synchronize()
 
     lib = pagedkv.lib()
@@ -594,21 +606,33 @@ def mix(args, dev) -> int:
     chk = pagedkv._lib.check
 
     def append(l):
-        rc = lib.pkv_append(h, l, kc[l].data_ptr(), vc[l].data_ptr(), slots.data_ptr(), T, sp)
+        if rope is not None:   # k rotated + stored, v stored, q rotated: one launch
+            rc = lib.pkv_append_rope(h, l, rope.handle, ppos.data_ptr(), pagedkv.F32,
+                                     kc[l].data_ptr(), vc[l].data_ptr(), slots.data_ptr(), T,
+                                     qp[l].data_ptr(), qrot.data_ptr(), H, sp)
+        else:
+            rc = lib.pkv_append(h, l, kc[l].data_ptr(), vc[l].data_ptr(), slots.data_ptr(), T, sp)
         if rc:
             chk(rc, h)
 
     def prefill(l):
-        rc = lib.pkv_prefill_attention(h, l, qp[l].data_ptr(), outp[l].data_ptr(), odt,
+        q = qrot if rope is not None else qp[l]
+        rc = lib.pkv_prefill_attention(h, l, q.data_ptr(), outp[l].data_ptr(), odt,
                                        cu.data_ptr(), pctx.data_ptr(), ptab.data_ptr(), mbps, NP, C,
                                        max_p, H, sc, sp)
         if rc:
             chk(rc, h)
 
     def decode(l):
-        rc = lib.pkv_decode_attention(h, l, qd[l].data_ptr(), outd[l].data_ptr(), odt,
-                                      dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND, H, sc,
-                                      kd[l].data_ptr(), vd[l].data_ptr(), sp)
+        if rope is not None:
+            rc = lib.pkv_decode_attention_rope(h, l, rope.handle, None, pagedkv.F32,
+                                               qd[l].data_ptr(), outd[l].data_ptr(), odt,
+                                               dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND,
+                                               H, sc, kd[l].data_ptr(), vd[l].data_ptr(), sp)
+        else:
+            rc = lib.pkv_decode_attention(h, l, qd[l].data_ptr(), outd[l].data_ptr(), odt,
+                                          dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND, H,
+                                          sc, kd[l].data_ptr(), vd[l].data_ptr(), sp)
         if rc:
             chk(rc, h)
 
@@ -656,7 +680,11 @@ def mix(args, dev) -> int:
     flops = wl.prefill_flops(shape, m.prior, m.chunk)
     pbytes = wl.prefill_bytes(shape, m.prior, m.chunk)
     dbytes = wl.decode_bytes(shape, m.ctx, 1)
-    abytes = 2 * T * KVH * hd * 2 * 2 + 4 * T
+    # chunk append: k and v read and written (+ q read and written with --rope)
+    ib = 4 if rope is not None else 2
+    abytes = T * KVH * hd * 2 * (ib + 2) + 4 * T
+    if rope is not None:
+        abytes += T * H * hd * (ib + 2) + 4 * T
     tflops = flops / (pre_ms / 1e3) / 1e12
     dec_gbps = dbytes / (dec_ms / 1e3) / 1e9
     tok_s = (T + ND) / (ms_step / 1e3)
@@ -665,7 +693,7 @@ def mix(args, dev) -> int:
         f"chunk append {app_ms * 1e3:.1f} us")
 
     cpu = None
-    if args.cpu_layers > 0:
+    if args.cpu_layers > 0 and rope is None:
         import oracle
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         shp = (m.num_blocks, bs, KVH, hd)
@@ -703,7 +731,9 @@ def mix(args, dev) -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) K/V/Q, random block tables)",
         "config": {"workload": "cfg2: 22 layers, 32q/4kv heads, hd 64, bs 16, f16 KV; 8 chunked "
-                               "prefills of 256 over prior U[0,1024] + 56 decodes, ctx U[256,2048]",
+                               "prefills of 256 over prior U[0,1024] + 56 decodes, ctx U[256,2048]"
+                               + (" + RoPE (f32 q/k/v in: pkv_append_rope, "
+                                  "pkv_decode_attention_rope)" if rope is not None else ""),
                    "priors": m.prior.tolist(), "mean_decode_context": round(float(m.ctx.mean()), 1),
                    "seed": args.seed, "num_blocks": m.num_blocks, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
@@ -715,10 +745,13 @@ def mix(args, dev) -> int:
                             "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
                             "kernel": "pkv::decode_kernel", "kernel_avg_us": round(dec_ms * 1e3, 2),
                             "algorithmic_bytes_per_launch": dbytes},
-        "append": {"us": round(app_ms * 1e3, 2), "GBps": round(abytes / (app_ms / 1e3) / 1e9, 1)},
+        "append": {"us": round(app_ms * 1e3, 2), "GBps": round(abytes / (app_ms / 1e3) / 1e9, 1),
+                   "rope": rope is not None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+    if rope is not None:
+        rope.close()
     cache.close()
     return 0
 

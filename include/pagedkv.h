@@ -251,6 +251,24 @@ int pkv_decode_attention_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
                               const void* k_new, const void* v_new,
                               void* stream);
 
+/* The prefill step's glue in one launch (prefill_seq, transformer.rs:
+ * 160-174: apply_rope to q and k, then KvPool::write of every token's k and
+ * v, attention.rs:57-83): k rows rotated by positions[t] and v rows stored
+ * at slot_mapping[t], as pkv_append; with q (not NULL), its rows rotated
+ * into q_out for pkv_prefill_attention.
+ *  k, v: [n_tokens][n_kv_head][head_dim], q: [n_tokens][n_head][head_dim],
+ *  all in in_dtype (PKV_F32, PKV_F16 or PKV_BF16), 16-byte aligned; the
+ *  stored rows and q_out are in the pool dtype (q_out may alias q when
+ *  in_dtype is the pool dtype).  positions, slot_mapping: device int32
+ *  [n_tokens]; slot < 0 skips that token's k/v (its q is still rotated).
+ *  Rotation and rounding as pkv_rope_apply.  A position outside
+ *  [0, max_seq) leaves that token's rotated rows unwritten and a slot
+ *  beyond the pool its k/v; pkv_pool_check() reports either. */
+int pkv_append_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
+                    const int32_t* positions, int in_dtype, const void* k,
+                    const void* v, const int32_t* slot_mapping, int n_tokens,
+                    const void* q, void* q_out, int n_head, void* stream);
+
 /* ---- token selection (crates/ai-engine-runtime/src/sample.rs:12-55) --------
  * The engine copies each logits row to the host and samples it with
  * SamplingConfig {temperature of the request, top_p: None, top_k: None,

@@ -197,3 +197,130 @@ def test_decode_attention_rope_rejects_mismatch(gpu):
                                     torch.ones(1, dtype=torch.int32, device=gpu), rope=rope)
     c.close()
     rope.close()
+
+
+# -- prefill glue: pkv_append_rope (transformer.rs:160-174) --------------------
+def _slot_case(seed, n, nb, bs):
+    slots = wl.permutation(seed, nb * bs)[:n].astype(np.int32)
+    slots[::7] = -1                                        # padding tokens
+    return slots
+
+
+@pytest.mark.parametrize("dt,in_dt,hd,KVH,R", [(wl.BF16, wl.F32, 128, 8, 4),
+                                               (wl.BF16, wl.BF16, 128, 8, 4),
+                                               (wl.F16, wl.F32, 64, 4, 8),
+                                               (wl.F16, wl.F16, 64, 2, 1),
+                                               (wl.F32, wl.F32, 256, 2, 2),
+                                               (wl.BF16, wl.F32, 256, 1, 8)])
+def test_append_rope_bit_exact(gpu, dt, in_dt, hd, KVH, R):
+    n, nb, bs, H, max_seq = 203, 40, 16, KVH * R, 3000
+    seed = hd + KVH + R + 3 * dt + in_dt
+    kp0 = wl.normal_storage(seed + 1, (nb, bs, KVH, hd), dt)
+    vp0 = wl.normal_storage(seed + 2, (nb, bs, KVH, hd), dt)
+    k = wl.normal_storage(seed + 3, (n, KVH, hd), in_dt)
+    v = wl.normal_storage(seed + 4, (n, KVH, hd), in_dt)
+    q = wl.normal_storage(seed + 5, (n, H, hd), in_dt)
+    slots = _slot_case(seed, n, nb, bs)
+    pos = wl.randint(seed + 6, n, 0, max_seq - 1).astype(np.int32)
+    pos[:3] = [0, max_seq - 1, 1]
+    c = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, TD[dt])
+    c.write_bytes(0, pagedkv.K, kp0)
+    c.write_bytes(0, pagedkv.V, vp0)
+    rope = pagedkv.Rope(hd, 500000.0, max_seq)
+    qo = c.layer(0).append_rope(rope, _dev(k, in_dt, gpu), _dev(v, in_dt, gpu),
+                                torch.from_numpy(slots).to(gpu), torch.from_numpy(pos).to(gpu),
+                                q=_dev(q, in_dt, gpu))
+    torch.cuda.synchronize()
+    c.check()
+    cs, sn = oracle.rope_table(hd, 500000.0, max_seq)
+    kr = wl.to_storage(oracle.rope_apply(wl.widen(k, in_dt), cs, sn, pos), dt)
+    vr = wl.to_storage(wl.widen(v, in_dt), dt)
+    qr = wl.to_storage(oracle.rope_apply(wl.widen(q, in_dt), cs, sn, pos), dt)
+    kp, vp = kp0.copy().reshape(nb * bs, KVH, hd), vp0.copy().reshape(nb * bs, KVH, hd)
+    live = slots >= 0
+    kp[slots[live]] = kr[live]
+    vp[slots[live]] = vr[live]
+    assert np.array_equal(c.read_bytes(0, pagedkv.K), kp.view(np.uint8).reshape(-1))
+    assert np.array_equal(c.read_bytes(0, pagedkv.V), vp.view(np.uint8).reshape(-1))
+    nd = np.uint32 if dt == wl.F32 else np.uint16
+    assert np.array_equal(_bits(qo), qr.view(nd))
+    c.close()
+    rope.close()
+
+
+def test_append_rope_equals_separate_passes(gpu):
+    # one launch == rope_apply(k) + pkv_append + rope_apply(q), byte for byte
+    n, nb, bs, KVH, hd, H = 96, 12, 16, 4, 128, 32
+    k = torch.randn((n, KVH, hd), device=gpu)
+    v = torch.randn((n, KVH, hd), device=gpu)
+    q = torch.randn((n, H, hd), device=gpu)
+    slots = torch.from_numpy(_slot_case(9, n, nb, bs)).to(gpu)
+    pos = torch.arange(500, 500 + n, dtype=torch.int32, device=gpu)
+    rope = pagedkv.Rope(hd, 500000.0, 1024)
+    a = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, torch.bfloat16)
+    b = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, torch.bfloat16)
+    qa = a.layer(0).append_rope(rope, k, v, slots, pos, q=q)
+    kb = rope.apply(k, pos, out_dtype=torch.bfloat16)
+    b.layer(0).append(kb, v.to(torch.bfloat16), slots)
+    qb = rope.apply(q, pos, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    for which in (pagedkv.K, pagedkv.V):
+        assert np.array_equal(a.read_bytes(0, which), b.read_bytes(0, which))
+    assert torch.equal(qa.view(torch.int16), qb.view(torch.int16))
+    a.close()
+    b.close()
+    rope.close()
+
+
+def test_append_rope_in_place_q_and_no_q(gpu):
+    n, nb, bs, KVH, hd, H = 20, 4, 16, 2, 64, 4
+    rope = pagedkv.Rope(hd, 10000.0, 256)
+    c = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, torch.float16)
+    k = torch.randn((n, KVH, hd), device=gpu).half()
+    v = torch.randn((n, KVH, hd), device=gpu).half()
+    q = torch.randn((n, H, hd), device=gpu).half()
+    ref_q = rope.apply(q, torch.arange(n, dtype=torch.int32, device=gpu))
+    slots = torch.arange(n, dtype=torch.int32, device=gpu)
+    pos = torch.arange(n, dtype=torch.int32, device=gpu)
+    out = c.layer(0).append_rope(rope, k, v, slots, pos, q=q, q_out=q)
+    assert out is q
+    assert c.layer(0).append_rope(rope, k, v, slots, pos) is None
+    torch.cuda.synchronize()
+    assert torch.equal(q, ref_q)
+    kg, vg = c.layer(0).gather_seq(list(range(nb)), n)
+    assert torch.equal(kg, rope.apply(k, pos))
+    assert torch.equal(vg, v)
+    c.close()
+    rope.close()
+
+
+def test_append_rope_bad_position_and_slot(gpu):
+    n, nb, bs, KVH, hd, H = 4, 2, 16, 2, 128, 4
+    rope = pagedkv.Rope(hd, 10000.0, 100)
+    c = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, torch.bfloat16)
+    k = torch.randn((n, KVH, hd), device=gpu)
+    v = torch.randn((n, KVH, hd), device=gpu)
+    q = torch.randn((n, H, hd), device=gpu)
+    qo = torch.zeros((n, H, hd), dtype=torch.bfloat16, device=gpu)
+    before_k = c.read_bytes(0, pagedkv.K)
+    slots = torch.tensor([0, 1, 2, nb * bs], dtype=torch.int32, device=gpu)
+    pos = torch.tensor([0, 100, 5, 6], dtype=torch.int32, device=gpu)
+    c.layer(0).append_rope(rope, k, v, slots, pos, q=q, q_out=qo)
+    torch.cuda.synchronize()
+    with pytest.raises(pagedkv.PagedKvError):
+        c.check()
+    row = KVH * hd * 2
+    after_k = c.read_bytes(0, pagedkv.K)
+    assert np.array_equal(after_k[row:2 * row], before_k[row:2 * row])   # position 100: unwritten
+    assert not np.array_equal(after_k[:row], before_k[:row])
+    assert torch.count_nonzero(qo[1]) == 0 and torch.count_nonzero(qo[0]) > 0
+    c.check()   # cleared
+    # at the C boundary: q without q_out is rejected before any launch
+    rc = pagedkv.lib().pkv_append_rope(c.handle, 0, rope.handle, pos.data_ptr(), pagedkv.F32,
+                                       k.data_ptr(), v.data_ptr(), slots.data_ptr(), n,
+                                       q.data_ptr(), None, H, None)
+    assert rc != 0 and b"q_out" in pagedkv.lib().pkv_last_error(c.handle)
+    with pytest.raises(ValueError):
+        c.layer(0).append_rope(rope, k, v, slots[:3], pos)
+    c.close()
+    rope.close()
