@@ -338,7 +338,6 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   constexpr bool kRowSum = PKV_PREFILL_MFMA_ROWSUM && DT != PKV_F32;
   const uint32_t one2 = DT == PKV_BF16 ? 0x3F803F80u : 0x3C003C00u;
   const u32x4 ones = u32x4{one2, one2, one2, one2};
-  (void)ones;
   f32x4 lacc[C::NR];
   float m[C::NR], lsum[C::NR];
   f32x4 o[C::ND][C::NR];
@@ -367,12 +366,9 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
     const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
     return u32x4{l2.x, l2.y, h2.x, h2.y};
   };
-  auto compute = [&](int t, bool masked) __attribute__((always_inline)) {
-    const char* kl = lds + (t & 1) * C::STAGE;
-    const char* vl = kl + C::KLDS;
-    const int k0 = t * C::KT;
-    // ---- S^T = K Q^T: sacc[km][rn][j] = S[key k0 + 16 km + 4 G + j][row] ----
-    f32x4 sacc[C::NKM][C::NR];
+  // ---- S^T = K Q^T: sacc[km][rn][j] = S[key k0 + 16 km + 4 G + j][row] ----
+  typedef f32x4 STile[C::NKM][C::NR];
+  auto qk = [&](const char* kl, STile& sacc) __attribute__((always_inline)) {
 #pragma unroll
     for (int km = 0; km < C::NKM; ++km) {
 #pragma unroll
@@ -384,27 +380,27 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
         for (int rn = 0; rn < C::NR; ++rn) mfma_frag<DT>(kf, qf[rn][f], sacc[km][rn]);
       }
     }
-    // ---- causal mask + online softmax per row (rows along lane % 16) ----
-    // Causal mask (wave-uniform branch): scores of keys past a row's
-    // position become -inf in place, so the shared softmax below gives them
-    // weight exactly 0 and a row's arithmetic does not depend on which rows
-    // share its wave or workgroup.
-    if (masked) {
+  };
+  // Causal mask: scores of keys past a row's position become -inf in place,
+  // so the shared softmax below gives them weight exactly 0 and a row's
+  // arithmetic does not depend on which rows share its wave or workgroup.
+  auto mask = [&](int k0, STile& sacc) __attribute__((always_inline)) {
 #pragma unroll
-      for (int km = 0; km < C::NKM; ++km)
+    for (int km = 0; km < C::NKM; ++km)
 #pragma unroll
-        for (int rn = 0; rn < C::NR; ++rn)
+      for (int rn = 0; rn < C::NR; ++rn)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (k0 + 16 * km + 4 * G + j > lim[rn]) sacc[km][rn][j] = -INFINITY;
-    }
-    // Online softmax with a lazily raised reference max m (log2 domain): m
-    // moves only when a tile's row max exceeds it by more than kTau, so
-    // weights stay <= 2^kTau and the O/l rescale is skipped whenever no row
-    // of the wave moved.  Scores enter the exponent through one fma.
-    float p[C::NKM][C::NR][4];
+        for (int j = 0; j < 4; ++j)
+          if (k0 + 16 * km + 4 * G + j > lim[rn]) sacc[km][rn][j] = -INFINITY;
+  };
+  // Online softmax per row (rows along lane % 16) with a lazily raised
+  // reference max m (log2 domain): m moves only when a tile's row max exceeds
+  // it by more than kTau, so weights stay <= 2^kTau and the O/l rescale is
+  // skipped whenever no row of the wave moved.  Scores enter the exponent
+  // through one fma; the weights replace the scores in sacc.  Returns
+  // whether this lane's rows moved (alpha: their rescale factors).
+  auto softmax = [&](STile& sacc, float (&alpha)[C::NR]) __attribute__((always_inline)) {
     bool moved = false;
-    float alpha[C::NR];
 #pragma unroll
     for (int rn = 0; rn < C::NR; ++rn) {
       float tmax = -INFINITY;
@@ -425,11 +421,14 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
       for (int km = 0; km < C::NKM; ++km)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          p[km][rn][j] = fast_exp2(fmaf(sacc[km][rn][j], a.scale_log2, nm));
-          if constexpr (!kRowSum) ssum += p[km][rn][j];
+          sacc[km][rn][j] = fast_exp2(fmaf(sacc[km][rn][j], a.scale_log2, nm));
+          if constexpr (!kRowSum) ssum += sacc[km][rn][j];
         }
       if constexpr (!kRowSum) lsum[rn] = fmaf(lsum[rn], alpha[rn], ssum);  // lane-partial
     }
+    return moved;
+  };
+  auto rescale = [&](bool moved, const float (&alpha)[C::NR]) __attribute__((always_inline)) {
     if (__builtin_amdgcn_ballot_w64(moved)) {  // wave-uniform
 #pragma unroll
       for (int rn = 0; rn < C::NR; ++rn) {
@@ -438,54 +437,79 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
         if constexpr (kRowSum) lacc[rn] *= alpha[rn];
       }
     }
-    // ---- O^T += V^T P^T ----
-    if constexpr (DT == PKV_F32) {
-      // k-step (km, j): lane group G supplies key 16 km + 4 G + j
+  };
+  // 16-bit pools: the weights as the B operand of the P.V MFMA, k-step ks
+  // (32 keys): lane group G supplies keys 32 ks + {4G..4G+3, 16+4G..16+4G+3};
+  // bf16 as a high part plus the bf16 residual (two MFMAs).
+  constexpr int NKS = C::KT / 32;
+  typedef u32x4 PTile[NKS][C::NR];
+  auto pack = [&](const STile& p, PTile& phi, PTile& plo) __attribute__((always_inline)) {
 #pragma unroll
-      for (int dm = 0; dm < C::ND; ++dm)
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int km = 0; km < C::NKM; ++km) {
-          const u32x4 va = ld16(vl + (16 * dm + col) * C::VTP + (16 * km + 4 * G) * 4);
+      for (int rn = 0; rn < C::NR; ++rn)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int rn = 0; rn < C::NR; ++rn)
-              o[dm][rn] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(va[j]),
-                                                               p[km][rn][j], o[dm][rn], 0, 0, 0);
+        for (int w = 0; w < 4; ++w) {
+          const float x0 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2];
+          const float x1 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2 + 1];
+          phi[ks][rn][w] = cvt_pk16<DT>(x0, x1);
+          if constexpr (DT == PKV_BF16)
+            plo[ks][rn][w] = cvt_pk16<DT>(x0 - bf16lo(phi[ks][rn][w]), x1 - bf16hi(phi[ks][rn][w]));
         }
-    } else {
-      // k-step ks (32 keys): lane group G supplies keys 32 ks + {4G..4G+3, 16+4G..16+4G+3}
+  };
+  // ---- O^T += V^T P^T ----
+  auto pv16 = [&](const char* vl, const PTile& phi, const PTile& plo) __attribute__((always_inline)) {
 #pragma unroll
-      for (int ks = 0; ks < C::KT / 32; ++ks) {
-        u32x4 phi[C::NR], plo[C::NR];
+    for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
-        for (int rn = 0; rn < C::NR; ++rn)
+      for (int dm = 0; dm < C::ND; ++dm) {
+        const u32x4 va = v_frag(vl, ks, dm);
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const float x0 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2];
-            const float x1 = p[2 * ks + (w >> 1)][rn][(w & 1) * 2 + 1];
-            phi[rn][w] = cvt_pk16<DT>(x0, x1);
-            if constexpr (DT == PKV_BF16)
-              plo[rn][w] = cvt_pk16<DT>(x0 - bf16lo(phi[rn][w]), x1 - bf16hi(phi[rn][w]));
-          }
-#pragma unroll
-        for (int dm = 0; dm < C::ND; ++dm) {
-          const u32x4 va = v_frag(vl, ks, dm);
-#pragma unroll
-          for (int rn = 0; rn < C::NR; ++rn) {
-            mfma_frag<DT>(va, phi[rn], o[dm][rn]);
-            if constexpr (DT == PKV_BF16) mfma_frag<DT>(va, plo[rn], o[dm][rn]);
-          }
-        }
-        if constexpr (kRowSum) {
-          // every row of the all-ones operand sums the row's weights
-#pragma unroll
-          for (int rn = 0; rn < C::NR; ++rn) {
-            mfma_frag<DT>(ones, phi[rn], lacc[rn]);
-            if constexpr (DT == PKV_BF16) mfma_frag<DT>(ones, plo[rn], lacc[rn]);
-          }
+        for (int rn = 0; rn < C::NR; ++rn) {
+          mfma_frag<DT>(va, phi[ks][rn], o[dm][rn]);
+          if constexpr (DT == PKV_BF16) mfma_frag<DT>(va, plo[ks][rn], o[dm][rn]);
         }
       }
+      if constexpr (kRowSum) {
+        // every row of the all-ones operand sums the row's weights
+#pragma unroll
+        for (int rn = 0; rn < C::NR; ++rn) {
+          mfma_frag<DT>(ones, phi[ks][rn], lacc[rn]);
+          if constexpr (DT == PKV_BF16) mfma_frag<DT>(ones, plo[ks][rn], lacc[rn]);
+        }
+      }
+    }
+  };
+  auto pv32 = [&](const char* vl, const STile& p) __attribute__((always_inline)) {
+    // k-step (km, j): lane group G supplies key 16 km + 4 G + j
+#pragma unroll
+    for (int dm = 0; dm < C::ND; ++dm)
+#pragma unroll
+      for (int km = 0; km < C::NKM; ++km) {
+        const u32x4 va = ld16(vl + (16 * dm + col) * C::VTP + (16 * km + 4 * G) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int rn = 0; rn < C::NR; ++rn)
+            o[dm][rn] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(va[j]),
+                                                             p[km][rn][j], o[dm][rn], 0, 0, 0);
+      }
+  };
+  auto compute = [&](int t, bool masked) __attribute__((always_inline)) {
+    const char* kl = lds + (t & 1) * C::STAGE;
+    const char* vl = kl + C::KLDS;
+    STile sacc;
+    qk(kl, sacc);
+    if (masked) mask(t * C::KT, sacc);  // wave-uniform branch
+    float alpha[C::NR];
+    const bool moved = softmax(sacc, alpha);
+    rescale(moved, alpha);
+    if constexpr (DT == PKV_F32) {
+      pv32(vl, sacc);
+    } else {
+      PTile phi, plo;
+      pack(sacc, phi, plo);
+      pv16(vl, phi, plo);
     }
   };
 
