@@ -357,24 +357,58 @@ __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long 
 
 // Index of the n-th (1-based) token, in index order, whose key is `key` and
 // that the top_k filter keeps (FILTER); V - 1 if there is none.  Only used
-// when more than one token of a tie group is needed.
+// when more than one token of a tie group is needed.  Each step gives every
+// thread a contiguous chunk of kTE elements (64 bytes: four 16-byte loads
+// when the row is aligned), marks the matches in a bit mask (the logit
+// interval of the key rejects most elements before the division), and a
+// block-wide exclusive scan of the per-thread counts, in index order, finds
+// the thread holding the n-th match.
 template <bool FILTER, int DT, bool VEC>
 __device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
                         unsigned long long n) {
+  constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
+  constexpr int kTE = 64 / E;               // elements per thread per step
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const XRange xr = x_range(key, key, rw.T);
   if (tid == 0) sm.found = rw.V - 1;
   __syncthreads();
   unsigned long long base = 0;
-  for (int c = 0; c < rw.V; c += kST) {
-    const int i = c + tid;
-    bool f = false;
-    if (i < rw.V) {
-      const uint32_t k = order_key(logit<DT>(rw.x, i) / rw.T);
-      f = k == key && (!FILTER || rw.kept(i, k));
+  for (int c = 0; c < rw.V; c += kST * kTE) {
+    const int i0 = c + tid * kTE;
+    float xs[kTE];
+    if (VEC && i0 + kTE <= rw.V) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 w = ld16(rw.x + (size_t)i0 * E + 16 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (DT == PKV_F32) {
+            xs[4 * q + j] = __uint_as_float(w[j]);
+          } else {
+            xs[8 * q + 2 * j] = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
+            xs[8 * q + 2 * j + 1] = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kTE; ++e) xs[e] = i0 + e < rw.V ? logit<DT>(rw.x, i0 + e) : NAN;
     }
-    const unsigned long long bal = __ballot(f);
-    const int rank = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) sm.red_i[wv] = __popcll(bal);
+    uint32_t mask = 0u;
+#pragma unroll
+    for (int e = 0; e < kTE; ++e) {
+      const float x = xs[e];  // NaN (past the end) fails the interval test
+      if (!(x >= xr.lo && x <= xr.hi)) continue;
+      const uint32_t k = order_key(x / rw.T);
+      if (k == key && (!FILTER || rw.kept(i0 + e, k))) mask |= 1u << e;
+    }
+    const int cnt = __popc(mask);
+    int incl = cnt;  // inclusive scan over the wave, in lane (= index) order
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) sm.red_i[wv] = incl;
     __syncthreads();
     int off = 0, tot = 0;
     for (int w = 0; w < kSW; ++w) {
@@ -382,7 +416,12 @@ __device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
       off += w < wv ? cw : 0;
       tot += cw;
     }
-    if (f && base + (unsigned long long)(off + rank) == n - 1ull) sm.found = i;
+    const unsigned long long before = base + (unsigned long long)(off + incl - cnt);
+    if (cnt > 0 && before < n && n <= before + (unsigned long long)cnt) {
+      uint32_t m = mask;
+      for (unsigned long long k = n - before; k > 1ull; --k) m &= m - 1u;  // drop lower matches
+      sm.found = i0 + __builtin_ctz(m);
+    }
     __syncthreads();
     base += (unsigned long long)tot;
     if (base >= n) break;
