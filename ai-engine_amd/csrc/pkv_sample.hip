@@ -32,6 +32,10 @@
 // last one records each bucket's size and smallest index, which settles a
 // tie without another pass unless several tied tokens are needed; three more
 // passes for top_k) -- and stays in L2 / the Infinity Cache between passes.
+// Batches of at most 128 rows without top_k / top_p split each row over
+// several workgroups instead (one launch per pass, partial histograms in a
+// stream-ordered allocation), which gives the same tokens.
+#include <algorithm>
 #include <climits>
 #include <cmath>
 
@@ -78,6 +82,7 @@ constexpr int kB1 = 4096;                 // first digit: key bits 31..20
 constexpr int kB2 = 1024;                 // second / third: bits 19..10, 9..0
 constexpr float kFix = 1099511627776.0f;  // 2^40
 constexpr unsigned long long kOne = 1ull << 40;
+constexpr int kSplitMinChunk = 4096;      // split path: elements per workgroup at least
 
 struct SampleArgs {
   const char* logits;
@@ -98,6 +103,7 @@ struct SampleSmem {
   unsigned long long red_u[kSW];
   float red_f[kSW];
   int red_i[kSW];
+  int red_j[kSW];
   unsigned int sel_bucket;
   unsigned long long sel_rem;
   int found;
@@ -114,15 +120,16 @@ __device__ __forceinline__ float logit(const char* row, int i) {
   }
 }
 
-// Calls f(i, logit) for this thread's elements of the row, in increasing i:
-// 16-byte vectors (VEC: the row is 16-byte aligned), then the tail.
+// Calls f(i, logit) for this thread's elements of row[lo, hi), in
+// increasing i: 16-byte vectors (VEC: the row is 16-byte aligned and lo is
+// a multiple of a vector's elements), then the tail past the last vector.
 template <int DT, bool VEC, class F>
-__device__ __forceinline__ void for_each(const char* row, int V, F&& f) {
-  int done = 0;
+__device__ __forceinline__ void for_range(const char* row, int lo, int hi, F&& f) {
+  int done = lo;
   if constexpr (VEC) {
     constexpr int E = DT == PKV_F32 ? 4 : 8;
-    const int nv = V / E;
-    for (int v = threadIdx.x; v < nv; v += kST) {
+    const int vend = hi / E;
+    for (int v = lo / E + (int)threadIdx.x; v < vend; v += kST) {
       const u32x4 w = ld16(row + (size_t)v * 16);
       if constexpr (DT == PKV_F32) {
 #pragma unroll
@@ -130,16 +137,20 @@ __device__ __forceinline__ void for_each(const char* row, int V, F&& f) {
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float lo = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
-          const float hi = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
-          f(v * 8 + 2 * j, lo);
-          f(v * 8 + 2 * j + 1, hi);
+          const float lo16 = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
+          const float hi16 = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
+          f(v * 8 + 2 * j, lo16);
+          f(v * 8 + 2 * j + 1, hi16);
         }
       }
     }
-    done = nv * E;
+    done = max(lo, vend * E);
   }
-  for (int i = done + (int)threadIdx.x; i < V; i += kST) f(i, logit<DT>(row, i));
+  for (int i = done + (int)threadIdx.x; i < hi; i += kST) f(i, logit<DT>(row, i));
+}
+template <int DT, bool VEC, class F>
+__device__ __forceinline__ void for_each(const char* row, int V, F&& f) {
+  for_range<DT, VEC>(row, 0, V, static_cast<F&&>(f));
 }
 
 // Larger y -> larger key; -0.0 and +0.0 compare equal, as partial_cmp has them.
@@ -226,52 +237,62 @@ __device__ int block_min_i(SampleSmem& sm, int v) {
   return r;
 }
 
-// Wave 0 walks the histogram hist[0..nb) from the top bucket down and
-// records in sm.sel_bucket the first bucket where the running total reaches
-// rem, and in sm.sel_rem what is still needed inside it.  Lane L sums the
-// segment of buckets nb-1-L*per down to nb-(L+1)*per (starting at a
-// lane-dependent offset so that the lanes hit different LDS banks), a wave
-// prefix scan finds the segment, and its lane walks it in order.  The
+// Finds in hist[0..nb) (nb = 4096 or 1024), walking from the top bucket
+// down, the first bucket where the running total reaches rem, and records
+// it in sm.sel_bucket and what is still needed inside it in sm.sel_rem.
+// Thread t owns the nb / kST buckets from nb-1-t*per down; a block-wide
+// inclusive scan of the threads' sums finds the first thread whose running
+// total reaches rem, and that thread walks its buckets in order.  The
 // histograms always hold at least rem below the digits chosen so far; if
 // that ever failed, the smallest non-empty bucket is taken so that the row
 // still ends with a token.  Call from all threads; ends with a barrier.
 __device__ void scan_buckets(SampleSmem& sm, const unsigned long long* hist, int nb,
                              unsigned long long rem) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  if (wv == 0) {
-    const int per = nb / 64;
-    const int hi = nb - 1 - lane * per;
-    unsigned long long seg = 0;
-    for (int j = 0; j < per; ++j) seg += hist[hi - ((j + lane) & (per - 1))];
-    unsigned long long incl = seg;
-    for (int d = 1; d < 64; d <<= 1) {
-      const unsigned long long o = shfl_up_u64(incl, d);
-      if (lane >= d) incl += o;
-    }
-    const unsigned long long reach = __ballot(incl >= rem);
-    const unsigned long long nonempty = __ballot(seg != 0ull);
-    const int fl = reach ? __builtin_ctzll(reach)
-                         : (nonempty ? 63 - __builtin_clzll(nonempty) : 0);
-    if (lane == fl) {
-      unsigned long long acc = incl - seg;
-      int chosen = -1, last_nonempty = hi;
-      for (int j = 0; j < per; ++j) {
-        const unsigned long long h = hist[hi - j];
-        if (h) last_nonempty = hi - j;
-        if (h && acc + h >= rem) {
-          chosen = hi - j;
-          break;
-        }
-        acc += h;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int per = nb / kST;
+  const int hi = nb - 1 - tid * per;
+  unsigned long long seg = 0;
+  for (int j = 0; j < per; ++j) seg += hist[hi - j];
+  unsigned long long incl = seg;  // inclusive scan over the wave
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned long long o = shfl_up_u64(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) sm.red_u[wv] = incl;
+  __syncthreads();
+  for (int w = 0; w < wv; ++w) incl += sm.red_u[w];
+  const unsigned long long reach = __ballot(incl >= rem);
+  const unsigned long long nonempty = __ballot(seg != 0ull);
+  if (lane == 0) {
+    sm.red_i[wv] = reach ? __builtin_ctzll(reach) : -1;                   // first reaching lane
+    sm.red_j[wv] = nonempty ? 63 - __builtin_clzll(nonempty) : -1;        // last non-empty lane
+  }
+  __syncthreads();
+  int chosen_t = -1, last_t = -1;
+  for (int w = 0; w < kSW; ++w) {
+    if (chosen_t < 0 && sm.red_i[w] >= 0) chosen_t = w * 64 + sm.red_i[w];
+    if (sm.red_j[w] >= 0) last_t = w * 64 + sm.red_j[w];
+  }
+  const int ft = chosen_t >= 0 ? chosen_t : (last_t >= 0 ? last_t : 0);
+  if (tid == ft) {
+    unsigned long long acc = incl - seg;
+    int chosen = -1, last_nonempty = hi;
+    for (int j = 0; j < per; ++j) {
+      const unsigned long long h = hist[hi - j];
+      if (h) last_nonempty = hi - j;
+      if (h && acc + h >= rem) {
+        chosen = hi - j;
+        break;
       }
-      unsigned long long r2 = rem - acc;
-      if (chosen < 0) {
-        chosen = last_nonempty;
-        r2 = hist[chosen] ? hist[chosen] : 1ull;
-      }
-      sm.sel_bucket = (uint32_t)chosen;
-      sm.sel_rem = r2;
+      acc += h;
     }
+    unsigned long long r2 = rem - acc;
+    if (chosen < 0) {
+      chosen = last_nonempty;
+      r2 = hist[chosen] ? hist[chosen] : 1ull;
+    }
+    sm.sel_bucket = (uint32_t)chosen;
+    sm.sel_rem = r2;
   }
   __syncthreads();
 }
@@ -298,11 +319,48 @@ struct Sel {
   int minidx;               // its smallest index
 };
 
+// One digit of a selection over row[lo, hi): sm.h gets the histogram of
+// key bits shift..shift+9 among the tokens whose key equals `prefix` under
+// `pmask` (COUNT: every token; otherwise kept tokens' mass) and, for the
+// last digit, sm.cnt / sm.minidx each bucket's size and smallest index.
+// Elements whose logit lies outside the prefix's logit interval are
+// rejected before the division.  Call from all threads; ends with a barrier.
+template <bool COUNT, int DT, bool VEC>
+__device__ void digit_pass(SampleSmem& sm, const Row<DT, VEC>& rw, int lo, int hi,
+                           uint32_t prefix, uint32_t pmask, int shift, bool last) {
+  for (int b = threadIdx.x; b < kB2; b += kST) {
+    sm.h[b] = 0ull;
+    sm.cnt[b] = 0u;
+    sm.minidx[b] = INT_MAX;
+  }
+  __syncthreads();
+  const XRange xr = x_range(prefix, prefix | ~pmask, rw.T);
+  for_range<DT, VEC>(rw.x, lo, hi, [&](int i, float x) {
+    if (!(x >= xr.lo && x <= xr.hi)) return;
+    const float y = x / rw.T;
+    const uint32_t key = order_key(y);
+    if ((key & pmask) != prefix) return;
+    const uint32_t b = (key >> shift) & (uint32_t)(kB2 - 1);
+    if constexpr (COUNT) {
+      atomicAdd(&sm.h[b], 1ull);
+    } else {
+      if (!rw.kept(i, key)) return;
+      const unsigned long long m = mass_of(y - rw.ymax);
+      if (m == 0ull) return;
+      atomicAdd(&sm.h[b], m);
+    }
+    if (last) {
+      atomicAdd(&sm.cnt[b], 1u);
+      atomicMin(&sm.minidx[b], i);
+    }
+  });
+  __syncthreads();
+}
+
 // Second and third digits of a selection whose first-digit histogram is
 // sm.h1: COUNT counts every token, otherwise kept tokens' mass.
 template <bool COUNT, int DT, bool VEC>
 __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long long target) {
-  const int tid = threadIdx.x;
   scan_buckets(sm, sm.h1, kB1, target);
   uint32_t prefix = sm.sel_bucket << 20;
   unsigned long long rem = sm.sel_rem;
@@ -312,33 +370,7 @@ __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long 
     const uint32_t pmask = pass == 0 ? 0xfff00000u : 0xfffffc00u;
     const bool last = pass == 1;
     __syncthreads();  // every thread has read sm.sel_* before it is reused
-    for (int b = tid; b < kB2; b += kST) {
-      sm.h[b] = 0ull;
-      sm.cnt[b] = 0u;
-      sm.minidx[b] = INT_MAX;
-    }
-    __syncthreads();
-    const XRange xr = x_range(prefix, prefix | ~pmask, rw.T);
-    for_each<DT, VEC>(rw.x, rw.V, [&](int i, float x) {
-      if (!(x >= xr.lo && x <= xr.hi)) return;
-      const float y = x / rw.T;
-      const uint32_t key = order_key(y);
-      if ((key & pmask) != prefix) return;
-      const uint32_t b = (key >> shift) & (uint32_t)(kB2 - 1);
-      if constexpr (COUNT) {
-        atomicAdd(&sm.h[b], 1ull);
-      } else {
-        if (!rw.kept(i, key)) return;
-        const unsigned long long m = mass_of(y - rw.ymax);
-        if (m == 0ull) return;
-        atomicAdd(&sm.h[b], m);
-      }
-      if (last) {
-        atomicAdd(&sm.cnt[b], 1u);
-        atomicMin(&sm.minidx[b], i);
-      }
-    });
-    __syncthreads();
+    digit_pass<COUNT>(sm, rw, 0, rw.V, prefix, pmask, shift, last);
     scan_buckets(sm, sm.h, kB2, rem);
     const uint32_t b = sm.sel_bucket;
     rem = sm.sel_rem;
@@ -444,62 +476,90 @@ __device__ __forceinline__ unsigned long long ties_needed(const Sel& s) {
   return n < 1ull ? 1ull : n;
 }
 
+// First maximum of row[lo, hi) (strictly greater values only, so the first
+// maximum wins; NaN is never taken): (value, index), index INT_MAX when no
+// value exceeds -inf.  The result is valid in thread 0.
 template <int DT, bool VEC>
-__global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
-  __shared__ SampleSmem sm;
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const char* x = a.logits + (long long)row * a.stride_bytes;
-  const int V = a.vocab;
-  const float T = a.temps ? a.temps[row] : 0.0f;
-
-  if (T == 0.0f || V <= 1) {
-    // argmax: strictly greater values only, so the first maximum wins
-    float bv = -INFINITY;
-    int bi = INT_MAX;
-    for_each<DT, VEC>(x, V, [&](int i, float v) {
-      if (v > bv) {
-        bv = v;
-        bi = i;
-      }
-    });
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
+__device__ void block_argmax(SampleSmem& sm, const char* x, int lo, int hi, float& bv, int& bi) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  bv = -INFINITY;
+  bi = INT_MAX;
+  for_range<DT, VEC>(x, lo, hi, [&](int i, float v) {
+    if (v > bv) {
+      bv = v;
+      bi = i;
+    }
+  });
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sm.red_f[wv] = bv;
+    sm.red_i[wv] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kSW; ++w) {
+      const float ov = sm.red_f[w];
+      const int oi = sm.red_i[w];
       if (ov > bv || (ov == bv && oi < bi)) {
         bv = ov;
         bi = oi;
       }
     }
-    if (lane == 0) {
-      sm.red_f[wv] = bv;
-      sm.red_i[wv] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < kSW; ++w) {
-        const float ov = sm.red_f[w];
-        const int oi = sm.red_i[w];
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      a.tokens[row] = bi == INT_MAX ? 0 : bi;
-    }
+  }
+}
+
+// The largest x (T > 0) or -x (T < 0) of row[lo, hi), in every thread.
+// max of fl(x / T) needs no division: correctly rounded division is
+// monotone in x, so it is that value divided by T (ymax_of).
+template <int DT, bool VEC>
+__device__ float block_xmax(SampleSmem& sm, const char* x, int lo, int hi, float T) {
+  float xm = -INFINITY;
+  if (T > 0.0f)
+    for_range<DT, VEC>(x, lo, hi, [&](int, float v) { xm = fmaxf(xm, v); });
+  else
+    for_range<DT, VEC>(x, lo, hi, [&](int, float v) { xm = fmaxf(xm, -v); });
+  return block_max(sm, xm);
+}
+__device__ __forceinline__ float ymax_of(float xm, float T) { return (T > 0.0f ? xm : -xm) / T; }
+
+// First digit of the mass histogram over row[lo, hi), added to sm.h1.
+template <int DT, bool VEC>
+__device__ void mass_pass(SampleSmem& sm, const Row<DT, VEC>& rw, int lo, int hi) {
+  for_range<DT, VEC>(rw.x, lo, hi, [&](int i, float v) {
+    const float y = v / rw.T;
+    const uint32_t key = order_key(y);
+    if (!rw.kept(i, key)) return;
+    const unsigned long long m = mass_of(y - rw.ymax);
+    if (m) atomicAdd(&sm.h1[key >> 20], m);
+  });
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+
+  if (T == 0.0f || V <= 1) {
+    float bv;
+    int bi;
+    block_argmax<DT, VEC>(sm, x, 0, V, bv, bi);
+    if (tid == 0) a.tokens[row] = bi == INT_MAX ? 0 : bi;
     return;
   }
 
   Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
-  // max of fl(x / T): correctly rounded division is monotone in x, so it is
-  // the largest logit (T > 0) or the smallest (T < 0) divided by T
-  float xm = -INFINITY;
-  if (T > 0.0f)
-    for_each<DT, VEC>(x, V, [&](int, float v) { xm = fmaxf(xm, v); });
-  else
-    for_each<DT, VEC>(x, V, [&](int, float v) { xm = fmaxf(xm, -v); });
-  xm = block_max(sm, xm);
-  rw.ymax = (T > 0.0f ? xm : -xm) / T;
+  rw.ymax = ymax_of(block_xmax<DT, VEC>(sm, x, 0, V, T), T);
 
   if (a.top_k > 0 && a.top_k < V) {
     // the k-th largest key, and how many of its ties the first k include
@@ -516,13 +576,7 @@ __global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
   // first digit of the mass histogram; its buckets add up to the total mass
   for (int b = tid; b < kB1; b += kST) sm.h1[b] = 0ull;
   __syncthreads();
-  for_each<DT, VEC>(x, V, [&](int i, float v) {
-    const float y = v / T;
-    const uint32_t key = order_key(y);
-    if (!rw.kept(i, key)) return;
-    const unsigned long long m = mass_of(y - rw.ymax);
-    if (m) atomicAdd(&sm.h1[key >> 20], m);
-  });
+  mass_pass<DT, VEC>(sm, rw, 0, V);
   __syncthreads();
   unsigned long long part = 0;
   for (int b = tid; b < kB1; b += kST) part += sm.h1[b];
@@ -543,6 +597,242 @@ __global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
   if (tid == 0) a.tokens[row] = tok;
 }
 
+// ---- small batches: each row split over G workgroups -----------------------
+// Without top_k / top_p, a row's selection needs its max, the first-digit
+// mass histogram and two more digit histograms; each is a sum over the row,
+// so G workgroups (blockIdx.x) can each take a contiguous chunk and add
+// their part in global memory, one launch per pass (the launch boundary
+// orders the passes; no workgroup waits for another).  The masses are the
+// same integers as in sample_kernel and integer sums do not depend on their
+// order, so the token is the same as sample_kernel's.  Launches: max (which
+// also clears the histograms), mass, second digit, third digit, finish (one
+// workgroup per row: the last scan, a tie walk when needed, the token).
+constexpr int kMaxG = 32;
+static_assert(kB1 % kST == 0 && kB2 == kST && kMaxG <= kST, "split-path loads");
+struct SplitWs {  // per row
+  float pmax[kMaxG];  // per workgroup: max x / -x (sampled), max x (greedy)
+  int pidx[kMaxG];    // greedy: index of that max (INT_MAX: none)
+  unsigned long long h1[kB1];
+  unsigned long long h2[kB2];
+  unsigned long long h3[kB2];
+  unsigned int cnt3[kB2];
+  int min3[kB2];
+};
+
+// Workgroup blockIdx.x's chunk of a row: multiples of 8 elements (whole
+// 16-byte vectors for every dtype), the last one ending at V.
+__device__ __forceinline__ void split_chunk(int V, int& lo, int& hi) {
+  const int G = (int)gridDim.x;
+  const int ce = (((V + G - 1) / G) + 7) / 8 * 8;
+  lo = min(V, (int)blockIdx.x * ce);
+  hi = min(V, lo + ce);
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) split_max_kernel(SampleArgs a, SplitWs* ws) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.y, g = blockIdx.x, G = gridDim.x, tid = threadIdx.x;
+  SplitWs& w = ws[row];
+  for (int i = g * kST + tid; i < kB1; i += G * kST) w.h1[i] = 0ull;
+  for (int i = g * kST + tid; i < kB2; i += G * kST) {
+    w.h2[i] = 0ull;
+    w.h3[i] = 0ull;
+    w.cnt3[i] = 0u;
+    w.min3[i] = INT_MAX;
+  }
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  int lo, hi;
+  split_chunk(a.vocab, lo, hi);
+  if (T == 0.0f || a.vocab <= 1) {
+    float bv;
+    int bi;
+    block_argmax<DT, VEC>(sm, x, lo, hi, bv, bi);
+    if (tid == 0) {
+      w.pmax[g] = bv;
+      w.pidx[g] = bi;
+    }
+    return;
+  }
+  const float xm = block_xmax<DT, VEC>(sm, x, lo, hi, T);
+  if (tid == 0) w.pmax[g] = xm;
+}
+
+// The row's global histograms as the later passes read them, loaded with
+// one round trip at the start of a launch: thread t's first-digit buckets
+// t + kST j, its second- and third-digit bucket t, and the per-workgroup
+// maxima (threads below G).
+struct SplitLoad {
+  unsigned long long h1[kB1 / kST];
+  unsigned long long h2, h3;
+  unsigned int cnt3;
+  int min3;
+  float pmax;
+};
+__device__ __forceinline__ SplitLoad split_load(const SplitWs& w, int G, int digits) {
+  const int tid = threadIdx.x;
+  SplitLoad l;
+#pragma unroll
+  for (int j = 0; j < kB1 / kST; ++j) l.h1[j] = digits >= 1 ? w.h1[tid + j * kST] : 0ull;
+  l.h2 = digits >= 2 ? w.h2[tid] : 0ull;
+  l.h3 = digits >= 3 ? w.h3[tid] : 0ull;
+  l.cnt3 = digits >= 3 ? w.cnt3[tid] : 0u;
+  l.min3 = digits >= 3 ? w.min3[tid] : INT_MAX;
+  l.pmax = tid < G ? w.pmax[tid] : -INFINITY;
+  return l;
+}
+
+// From the loaded histograms: the selection target r * total and the first
+// `digits` (1 or 2) digits chosen so far; sm.h1 holds the first-digit
+// histogram afterwards.
+__device__ void split_prefix(SampleSmem& sm, const SplitLoad& l, float r, int digits,
+                             uint32_t& prefix, unsigned long long& rem) {
+  const int tid = threadIdx.x;
+  unsigned long long part = 0;
+#pragma unroll
+  for (int j = 0; j < kB1 / kST; ++j) {
+    sm.h1[tid + j * kST] = l.h1[j];
+    part += l.h1[j];
+  }
+  if (digits == 2) sm.h[tid] = l.h2;
+  const unsigned long long total = block_sum_u64(sm, part);  // barriers: LDS complete
+  scan_buckets(sm, sm.h1, kB1, clamp_target((double)r * (double)total, total));
+  prefix = sm.sel_bucket << 20;
+  rem = sm.sel_rem;
+  if (digits == 2) {
+    __syncthreads();  // every thread has read sm.sel_*
+    scan_buckets(sm, sm.h, kB2, rem);
+    prefix |= sm.sel_bucket << 10;
+    rem = sm.sel_rem;
+  }
+  __syncthreads();  // every thread has read sm.sel_*
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) split_mass_kernel(SampleArgs a, SplitWs* ws) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const SplitWs& w = ws[row];
+  const float pm = tid < (int)gridDim.x ? w.pmax[tid] : -INFINITY;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || a.vocab <= 1) return;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  for (int b = tid; b < kB1; b += kST) sm.h1[b] = 0ull;
+  Row<DT, VEC> rw{x, a.vocab, T, ymax_of(block_max(sm, pm), T), false, 0u, a.vocab};
+  int lo, hi;
+  split_chunk(a.vocab, lo, hi);
+  mass_pass<DT, VEC>(sm, rw, lo, hi);
+  __syncthreads();
+  for (int b = tid; b < kB1; b += kST)
+    if (sm.h1[b]) atomicAdd(&ws[row].h1[b], sm.h1[b]);
+}
+
+template <int DT, bool VEC, bool LAST>
+__global__ void __launch_bounds__(kST) split_digit_kernel(SampleArgs a, SplitWs* ws) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const SplitLoad l = split_load(ws[row], gridDim.x, LAST ? 2 : 1);
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || a.vocab <= 1) return;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  Row<DT, VEC> rw{x, a.vocab, T, ymax_of(block_max(sm, l.pmax), T), false, 0u, a.vocab};
+  uint32_t prefix;
+  unsigned long long rem;
+  split_prefix(sm, l, a.r, LAST ? 2 : 1, prefix, rem);
+  int lo, hi;
+  split_chunk(a.vocab, lo, hi);
+  digit_pass<false>(sm, rw, lo, hi, prefix, LAST ? 0xfffffc00u : 0xfff00000u, LAST ? 0 : 10,
+                    LAST);
+  SplitWs& w = ws[row];
+  for (int b = tid; b < kB2; b += kST) {
+    if (!sm.h[b]) continue;
+    atomicAdd(LAST ? &w.h3[b] : &w.h2[b], sm.h[b]);
+    if (LAST) {
+      atomicAdd(&w.cnt3[b], sm.cnt[b]);
+      atomicMin(&w.min3[b], sm.minidx[b]);
+    }
+  }
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs* ws, int G) {
+  __shared__ SampleSmem sm;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const SplitWs& w = ws[row];
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || V <= 1) {
+    if (tid == 0) {  // chunks in index order: strictly greater keeps the first maximum
+      float bv = -INFINITY;
+      int bi = INT_MAX;
+      for (int g = 0; g < G; ++g) {
+        if (w.pmax[g] > bv) {
+          bv = w.pmax[g];
+          bi = w.pidx[g];
+        }
+      }
+      a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    }
+    return;
+  }
+  const SplitLoad l = split_load(w, G, 3);
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  Row<DT, VEC> rw{x, V, T, ymax_of(block_max(sm, l.pmax), T), false, 0u, V};
+  uint32_t prefix;
+  unsigned long long rem;
+  split_prefix(sm, l, a.r, 2, prefix, rem);
+  sm.h[tid] = l.h3;
+  sm.cnt[tid] = l.cnt3;
+  sm.minidx[tid] = l.min3;
+  __syncthreads();
+  scan_buckets(sm, sm.h, kB2, rem);
+  const uint32_t b = sm.sel_bucket;
+  Sel s;
+  s.key = prefix | b;
+  s.rem = sm.sel_rem;
+  s.hist = sm.h[b];
+  s.cnt = sm.cnt[b];
+  s.minidx = sm.minidx[b];
+  __syncthreads();
+  const unsigned long long n = ties_needed(s);
+  const int tok = n == 1ull ? (s.minidx == INT_MAX ? V - 1 : s.minidx)
+                            : nth_tied<true>(sm, rw, s.key, n);
+  if (tid == 0) a.tokens[row] = tok;
+}
+
+// Workgroups per row for the split path (1: one workgroup per row).  Rows
+// without temperatures are all greedy: one pass, one launch.
+int split_groups(int batch, int vocab, const float* temps, int top_k, float top_p) {
+  if (!temps || (top_k > 0 && top_k < vocab) || top_p < 1.0f || batch <= 0) return 1;
+  int g = 256 / batch;                                 // fill the CUs
+  g = std::min(g, kMaxG);
+  g = std::min(g, (vocab + kSplitMinChunk - 1) / kSplitMinChunk);  // chunks worth a workgroup
+  return std::max(g, 1);
+}
+
+template <int DT, bool VEC>
+hipError_t launch_dt(const SampleArgs& a, int batch, hipStream_t stream) {
+  const int G = split_groups(batch, a.vocab, a.temps, a.top_k, a.top_p);
+  if (G > 1) {
+    void* p = nullptr;
+    if (hipMallocAsync(&p, (size_t)batch * sizeof(SplitWs), stream) == hipSuccess) {
+      SplitWs* ws = static_cast<SplitWs*>(p);
+      const dim3 grid(G, batch);
+      split_max_kernel<DT, VEC><<<grid, kST, 0, stream>>>(a, ws);
+      split_mass_kernel<DT, VEC><<<grid, kST, 0, stream>>>(a, ws);
+      split_digit_kernel<DT, VEC, false><<<grid, kST, 0, stream>>>(a, ws);
+      split_digit_kernel<DT, VEC, true><<<grid, kST, 0, stream>>>(a, ws);
+      split_finish_kernel<DT, VEC><<<batch, kST, 0, stream>>>(a, ws, G);
+      const hipError_t e = hipGetLastError();
+      const hipError_t f = hipFreeAsync(p, stream);
+      return e != hipSuccess ? e : f;
+    }
+    (void)hipGetLastError();  // allocation failed: one workgroup per row
+  }
+  sample_kernel<DT, VEC><<<batch, kST, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_sample(const void* logits, int dtype, long long row_stride, int batch,
@@ -553,17 +843,12 @@ hipError_t launch_sample(const void* logits, int dtype, long long row_stride, in
                tokens};
   // 16-byte loads when every row starts on a 16-byte boundary
   const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (batch == 1 || sb % 16 == 0);
-  if (dtype == PKV_F32) {
-    if (vec) sample_kernel<PKV_F32, true><<<batch, kST, 0, stream>>>(a);
-    else sample_kernel<PKV_F32, false><<<batch, kST, 0, stream>>>(a);
-  } else if (dtype == PKV_BF16) {
-    if (vec) sample_kernel<PKV_BF16, true><<<batch, kST, 0, stream>>>(a);
-    else sample_kernel<PKV_BF16, false><<<batch, kST, 0, stream>>>(a);
-  } else {
-    if (vec) sample_kernel<PKV_F16, true><<<batch, kST, 0, stream>>>(a);
-    else sample_kernel<PKV_F16, false><<<batch, kST, 0, stream>>>(a);
-  }
-  return hipGetLastError();
+  if (dtype == PKV_F32) return vec ? launch_dt<PKV_F32, true>(a, batch, stream)
+                                   : launch_dt<PKV_F32, false>(a, batch, stream);
+  if (dtype == PKV_BF16) return vec ? launch_dt<PKV_BF16, true>(a, batch, stream)
+                                    : launch_dt<PKV_BF16, false>(a, batch, stream);
+  return vec ? launch_dt<PKV_F16, true>(a, batch, stream)
+             : launch_dt<PKV_F16, false>(a, batch, stream);
 }
 
 }  // namespace pkv

@@ -129,3 +129,55 @@ def test_invalid_arguments(gpu):
     lg = torch.zeros((2, 10), device=gpu)
     with pytest.raises(pagedkv.PagedKvError):
         pagedkv.sample(lg, torch.ones(2), top_k=-1)
+
+
+# -- batches of at most 128 rows split each row over several workgroups --------
+def _rows(rng, B, V):
+    kinds = ["normal", "ties", "flat", "spiky"]
+    return np.stack([_logits(rng, kinds[b % 4], V) for b in range(B)])
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_split_rows_equal_one_workgroup_rows(gpu, dt):
+    # 16 rows go through the split path; the same rows repeated to 256 rows
+    # (one workgroup per row) must give the same tokens, bit for bit: both
+    # add the same integer masses
+    rng = np.random.default_rng(5)
+    V, B = 128256, 16
+    x = _rows(rng, B, V)
+    temps = np.array([[0.0, 0.7, 1.0, 1.6, -1.0, 0.3, 0.8, 2.0][b % 8] for b in range(B)],
+                     np.float32)
+    lg = torch.from_numpy(x).to(gpu).to(TD[dt])
+    small = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu))
+    big = pagedkv.sample(lg.repeat(16, 1), torch.from_numpy(np.tile(temps, 16)).to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(big.view(16, B), small.view(1, B).expand(16, B))
+    _check_rows(lg.float().cpu().numpy(), temps, None, None, small.cpu().numpy())
+
+
+@pytest.mark.parametrize("B", [1, 3, 8, 64, 128])
+def test_split_ragged_vocab_and_strides(gpu, B):
+    # a vocabulary that is not a multiple of the 16-byte vector, rows at an
+    # odd stride (element loads), and batch sizes on both sides of the limit
+    rng = np.random.default_rng(B)
+    V = 50001
+    big = torch.from_numpy(_rows(rng, B, V + 3)).to(gpu).to(torch.bfloat16)
+    lg = big[:, 1:V + 1]                       # row stride V + 3, misaligned start
+    temps = np.array([[0.9, 0.0, 1.3, 0.6][b % 4] for b in range(B)], np.float32)
+    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu))
+    torch.cuda.synchronize()
+    _check_rows(lg.float().cpu().numpy(), temps, None, None, got.cpu().numpy())
+
+
+@pytest.mark.parametrize("with_temps", [False, True])
+def test_split_greedy_rows(gpu, with_temps):
+    # greedy rows: without temperatures (one launch) and with zero
+    # temperatures (the split path's per-chunk maxima); first maximum by
+    # index across chunk borders
+    B, V = 6, 128256
+    x = torch.randn((B, V), device=gpu)
+    for b, pos in enumerate([0, 4095, 4096, 65000, 128255, 100]):
+        x[b, pos] = 40.0
+    x[5, 90000] = 40.0                         # a later equal maximum loses
+    temps = torch.zeros(B, device=gpu) if with_temps else None
+    assert pagedkv.sample(x, temps).cpu().tolist() == [0, 4095, 4096, 65000, 128255, 100]
