@@ -443,6 +443,35 @@ def sample_bench(args, dev) -> int:
         print(json.dumps({"error": "token selection differs from the oracle"}))
         return 1
     rbytes = B * V * 2 + B * 4
+    # small batches (the split path: each row over several workgroups), the
+    # first rows of the same logits; checked against the full batch's tokens
+    small = {}
+    for sb in (1, 8, 32):
+        o2 = torch.empty(sb, dtype=torch.int32, device=dev)
+
+        def run_small(sb=sb, o2=o2):
+            rc = lib.pkv_sample(logits.data_ptr(), pagedkv.BF16, V, sb, V, temps.data_ptr(), 0,
+                                1.0, 42, o2.data_ptr(), sp)
+            if rc:
+                pagedkv._lib.check(rc, None)
+        for _ in range(max(1, args.warmup)):
+            run_small()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            run_small()
+        e1.record()
+        torch.cuda.synchronize()
+        same = bool(np.array_equal(o2.cpu().numpy(), got[:sb]))
+        small[str(sb)] = {"us": round(e0.elapsed_time(e1) / args.steps * 1e3, 2),
+                          "same_tokens_as_full_batch": same}
+        ok &= same
+    log(f"[bench] sample, small batches (us): "
+        + ", ".join(f"{k} rows {v['us']}" for k, v in small.items()))
+    if not ok:
+        print(json.dumps({"error": "small-batch tokens differ from the full batch's"}))
+        return 1
     cpu = None
     if args.cpu_layers > 0:
         # the reference procedure (sort, f32 softmax, running sum) on host rows
@@ -466,6 +495,7 @@ def sample_bench(args, dev) -> int:
                      "algorithmic_bytes_per_launch": rbytes},
         "greedy": {"us": round(ms_greedy * 1e3, 2),
                    "GBps": round(rbytes / (ms_greedy / 1e3) / 1e9, 1)},
+        "small_batches_sampled": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

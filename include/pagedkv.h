@@ -287,7 +287,12 @@ int pkv_append_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
  * in the reference.  The token equals the reference's except where its f32
  * running sums fall within their rounding of r or top_p.  Temperatures must
  * be finite and logits of sampled rows free of NaN (the reference's sort is
- * unspecified there).  Runs on the calling thread's current device. */
+ * unspecified there).  Runs on the calling thread's current device.  Batches
+ * of at most 128 rows with temperatures and no top_k / top_p split each row
+ * over several workgroups, with ~56 KB per row of partial histograms in a
+ * stream-ordered allocation on `stream` (hipMallocAsync / hipFreeAsync,
+ * capturable in a HIP graph); if that allocation fails, one workgroup per
+ * row.  Both give the same tokens. */
 int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
                int vocab, const float* temperatures, int top_k, float top_p,
                uint64_t seed, int32_t* tokens, void* stream);

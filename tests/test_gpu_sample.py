@@ -181,3 +181,32 @@ def test_split_greedy_rows(gpu, with_temps):
     x[5, 90000] = 40.0                         # a later equal maximum loses
     temps = torch.zeros(B, device=gpu) if with_temps else None
     assert pagedkv.sample(x, temps).cpu().tolist() == [0, 4095, 4096, 65000, 128255, 100]
+
+
+def test_split_path_replays_in_a_graph(gpu):
+    # captured in a HIP graph (the split path's stream-ordered allocation and
+    # its five launches become graph nodes) and replayed several times, with
+    # eager work between the replays: every replay gives the eager tokens
+    rng = np.random.default_rng(9)
+    B, V = 8, 128256
+    lg = torch.from_numpy(_rows(rng, B, V)).to(gpu).to(torch.bfloat16)
+    temps = torch.full((B,), 0.9, device=gpu)
+    ref = pagedkv.sample(lg, temps).clone()
+    out = torch.empty(B, dtype=torch.int32, device=gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):               # warm-up on a side stream
+        pagedkv.sample(lg, temps, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pagedkv.sample(lg, temps, out=out)
+    for i in range(4):
+        out.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        eager = pagedkv.sample(lg[:3], temps[:3])
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref[:3])
