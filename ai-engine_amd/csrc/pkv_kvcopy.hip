@@ -71,7 +71,8 @@ __global__ void __launch_bounds__(kCopyThreads)
 // stores.  A grid of long-lived workgroups (a few per CU) moves the 2 GiB of
 // cfg5's 512 copies 1.45x faster than one short workgroup per item.
 constexpr int kVecPerThread = 8;
-constexpr int kCopyGrid = 4096;  // workgroups of the copy: 16 per CU
+constexpr int kCopyGrid = 4096;       // workgroups of the copy: 16 per CU
+constexpr int kCompactGrid = 16384;   // of the compaction (its items are shorter)
 
 __global__ void __launch_bounds__(kCopyThreads)
     copy_blocks_kernel(char* __restrict__ base, size_t layer_bytes, int block_vec,
@@ -106,52 +107,60 @@ __global__ void __launch_bounds__(kCopyThreads)
   }
 }
 
-// In-place compaction.  grid.x = chain, grid.y = 2 * n_layers, grid.z =
-// chunk of a block.  Each thread owns the same byte range of every block in
+// In-place compaction.  Items (chain, K/V slab of a layer, chunk of a
+// block), chunk fastest; each workgroup takes items blockIdx.x, + gridDim.x,
+// ...  (cfg5's chains average under two moves, so one workgroup per item
+// would be short-lived: long-lived workgroups took its compaction from 24.2
+// to 20.5-21.2 ms).  Each thread owns the same byte range of every block in
 // its chain and performs the chain's moves in order, so a block's old bytes
 // are read (by the same thread, same address) before they are overwritten;
 // no cross-thread ordering is needed.  A cycle's first move parks one block
 // in registers (dst == -1) and its last move writes it back (src == -1).
 // The next move's source is loaded before this move's stores: the blocks of
 // a chain are distinct and each is read before it is written, so that read
-// never sees a byte this move writes (cfg5: 25.1 -> 24.2 ms).
+// never sees a byte this move writes (25.1 -> 24.2 ms).
 __global__ void __launch_bounds__(kCopyThreads)
     compact_kernel(char* __restrict__ base, size_t layer_bytes, int block_vec,
-                   const int32_t* __restrict__ ops,
-                   const int32_t* __restrict__ chain_start) {
-  int c = blockIdx.x;
-  int o0 = chain_start[c], o1 = chain_start[c + 1];
-  char* slab = base + (size_t)blockIdx.y * layer_bytes;
-  u32x4* pool = reinterpret_cast<u32x4*>(slab);
-  int v0 = blockIdx.z * (kCopyThreads * kVecPerThread) + threadIdx.x;
-  u32x4 held[kVecPerThread];
-  u32x4 ra[kVecPerThread], rb[kVecPerThread];
-  auto load_src = [&](int o, u32x4 (&r)[kVecPerThread]) __attribute__((always_inline)) {
-    const int s = ops[2 * o];
-    if (s < 0) return;  // the write-back of a cycle comes from `held`
+                   const int32_t* __restrict__ ops, const int32_t* __restrict__ chain_start,
+                   int n_chains, int n_slabs, int chunks) {
+  const long long items = (long long)n_chains * n_slabs * chunks;
+  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int chunk = (int)(it % chunks);
+    const long long cs = it / chunks;
+    const int slab_i = (int)(cs % n_slabs);
+    const int c = (int)(cs / n_slabs);
+    const int o0 = chain_start[c], o1 = chain_start[c + 1];
+    u32x4* pool = reinterpret_cast<u32x4*>(base + (size_t)slab_i * layer_bytes);
+    const int v0 = chunk * (kCopyThreads * kVecPerThread) + threadIdx.x;
+    u32x4 held[kVecPerThread];
+    u32x4 ra[kVecPerThread], rb[kVecPerThread];
+    auto load_src = [&](int o, u32x4 (&r)[kVecPerThread]) __attribute__((always_inline)) {
+      const int s = ops[2 * o];
+      if (s < 0) return;  // the write-back of a cycle comes from `held`
 #pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j) {
-      const int v = v0 + j * kCopyThreads;
-      if (v < block_vec) r[j] = __builtin_nontemporal_load(pool + (size_t)s * block_vec + v);
-    }
-  };
-  if (o0 < o1) load_src(o0, ra);
-  for (int o = o0; o < o1; ++o) {
-    const int s = ops[2 * o], d = ops[2 * o + 1];
-    if (o + 1 < o1) load_src(o + 1, rb);  // next source: never a block this move writes
-#pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j) {
-      const int v = v0 + j * kCopyThreads;
-      if (v < block_vec) {
-        const u32x4 x = s >= 0 ? ra[j] : held[j];
-        if (d >= 0)
-          __builtin_nontemporal_store(x, pool + (size_t)d * block_vec + v);
-        else
-          held[j] = x;
+      for (int j = 0; j < kVecPerThread; ++j) {
+        const int v = v0 + j * kCopyThreads;
+        if (v < block_vec) r[j] = __builtin_nontemporal_load(pool + (size_t)s * block_vec + v);
       }
-    }
+    };
+    if (o0 < o1) load_src(o0, ra);
+    for (int o = o0; o < o1; ++o) {
+      const int s = ops[2 * o], d = ops[2 * o + 1];
+      if (o + 1 < o1) load_src(o + 1, rb);  // next source: never a block this move writes
 #pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j) ra[j] = rb[j];
+      for (int j = 0; j < kVecPerThread; ++j) {
+        const int v = v0 + j * kCopyThreads;
+        if (v < block_vec) {
+          const u32x4 x = s >= 0 ? ra[j] : held[j];
+          if (d >= 0)
+            __builtin_nontemporal_store(x, pool + (size_t)d * block_vec + v);
+          else
+            held[j] = x;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kVecPerThread; ++j) ra[j] = rb[j];
+    }
   }
 }
 
@@ -255,10 +264,11 @@ hipError_t launch_compact(const pkv_pool* p, const int32_t* ops,
   if (n_chains <= 0) return hipSuccess;
   int block_vec = (int)(p->block_bytes / 16);
   int per_block = kCopyThreads * kVecPerThread;
-  dim3 grid((unsigned)n_chains, (unsigned)(2 * p->n_layers),
-            (unsigned)((block_vec + per_block - 1) / per_block));
+  const int chunks = (block_vec + per_block - 1) / per_block;
+  const long long items = (long long)n_chains * 2 * p->n_layers * chunks;
+  const unsigned grid = (unsigned)(items < kCompactGrid ? items : kCompactGrid);
   compact_kernel<<<grid, kCopyThreads, 0, stream>>>(
-      p->base, p->layer_bytes, block_vec, ops, chain_start);
+      p->base, p->layer_bytes, block_vec, ops, chain_start, n_chains, 2 * p->n_layers, chunks);
   return hipGetLastError();
 }
 
