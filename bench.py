@@ -66,6 +66,9 @@ def main() -> int:
                          "rotary embedding, which the decode kernel applies "
                          "(pkv_decode_attention_rope) and the chunk store applies to k and q "
                          "(pkv_append_rope)")
+    ap.add_argument("--serial", action="store_true",
+                    help="cfg2: time eager launches on one stream only (default: the step as "
+                         "a HIP graph with each layer's decode on a second stream)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="minimum layer passes of the CPU baseline sample (0 = skip it)")
@@ -653,36 +656,105 @@ def mix(args, dev) -> int:
         if rc:
             chk(rc, h)
 
-    def decode(l):
+    def decode(l, on=None):
+        st = on if on is not None else sp
         if rope is not None:
             rc = lib.pkv_decode_attention_rope(h, l, rope.handle, None, pagedkv.F32,
                                                qd[l].data_ptr(), outd[l].data_ptr(), odt,
                                                dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND,
-                                               H, sc, kd[l].data_ptr(), vd[l].data_ptr(), sp)
+                                               H, sc, kd[l].data_ptr(), vd[l].data_ptr(), st)
         else:
             rc = lib.pkv_decode_attention(h, l, qd[l].data_ptr(), outd[l].data_ptr(), odt,
                                           dtab.data_ptr(), mbps, dctx.data_ptr(), max_d, ND, H,
-                                          sc, kd[l].data_ptr(), vd[l].data_ptr(), sp)
+                                          sc, kd[l].data_ptr(), vd[l].data_ptr(), st)
         if rc:
             chk(rc, h)
 
-    def step():
+    # Per layer the prefill rows' and the decode rows' attention are
+    # independent (an engine forks them after the QKV projection and joins
+    # before the output projection): the decode runs on a second stream
+    # (default priority) between a fork and a join event of each layer.
+    dec_stream = torch.cuda.Stream(dev)
+    dsp = int(dec_stream.cuda_stream)
+    forks = [torch.cuda.Event() for _ in range(L)]
+    joins = [torch.cuda.Event() for _ in range(L)]
+
+    def step_serial():
         for l in range(L):
             append(l)
             prefill(l)
             decode(l)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    def step_overlap():
+        for l in range(L):
+            forks[l].record(stream)
+            dec_stream.wait_event(forks[l])
+            decode(l, dsp)
+            append(l)
+            prefill(l)
+            joins[l].record(dec_stream)
+            stream.wait_event(joins[l])
+
+    # the decode's split-context partials live in the pool workspace, which a
+    # split prefill would share: overlap only when the prefill does not split
+    overlap_ok = cache.prefill_workspace_bytes(NP, H, C, max_p) == 0
+
+    def time_steps(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / args.steps
+
+    def capture(fn):
+        # the library calls take the stream pointer `sp`: point it at the
+        # capture stream while fn is recorded
+        nonlocal stream, sp
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(stream)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        saved = (stream, sp)
+        with torch.cuda.graph(gr, stream=cap):
+            stream, sp = cap, int(cap.cuda_stream)
+            fn()
+        stream, sp = saved
+        torch.cuda.synchronize()
+        return gr
+
+    ms_serial = time_steps(step_serial)   # eager, one stream
+    ms_graph_serial = None
+    schedule = "eager launches, one stream"
+    ms_step = ms_serial
+    if not args.serial:
+        # the step as a HIP graph, each layer's decode forked onto a second
+        # stream when allowed; one replay must reproduce an eager step's
+        # outputs bit for bit (both kernels are deterministic and the step's
+        # appends rewrite the same rows)
+        step_serial()
+        torch.cuda.synchronize()
+        ref_p, ref_d = outp.clone(), outd.clone()
+        g_serial = capture(step_serial)
+        g_step = capture(step_overlap) if overlap_ok else g_serial
+        outp.zero_()
+        outd.zero_()
+        g_step.replay()
+        torch.cuda.synchronize()
+        if not (torch.equal(outp, ref_p) and torch.equal(outd, ref_d)):
+            print(json.dumps({"error": "graph replay differs from eager launches"}))
+            return 1
+        del ref_p, ref_d
+        ms_graph_serial = time_steps(g_serial.replay)
+        ms_step = time_steps(g_step.replay)
+        schedule = ("HIP graph; per layer the decode on a second stream, forked and joined "
+                    "around the prefill" if overlap_ok else "HIP graph, one stream")
     cache.check()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(args.steps):
-        step()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / args.steps
 
     n_kt = max(1, min(args.steps, 5))
 
@@ -718,7 +790,9 @@ def mix(args, dev) -> int:
     tflops = flops / (pre_ms / 1e3) / 1e12
     dec_gbps = dbytes / (dec_ms / 1e3) / 1e9
     tok_s = (T + ND) / (ms_step / 1e3)
-    log(f"[bench] {ms_step:.3f} ms/step, {tok_s:.0f} tok/s; per layer: prefill {pre_ms * 1e3:.1f} us "
+    log(f"[bench] {ms_step:.3f} ms/step ({schedule}; eager serial {ms_serial:.3f}, graph serial "
+        f"{ms_graph_serial if ms_graph_serial is None else round(ms_graph_serial, 3)}), "
+        f"{tok_s:.0f} tok/s; per layer: prefill {pre_ms * 1e3:.1f} us "
         f"({tflops:.1f} TFLOP/s), decode {dec_ms * 1e3:.1f} us ({dec_gbps:.0f} GB/s), "
         f"chunk append {app_ms * 1e3:.1f} us")
 
@@ -777,6 +851,9 @@ def mix(args, dev) -> int:
                             "algorithmic_bytes_per_launch": dbytes},
         "append": {"us": round(app_ms * 1e3, 2), "GBps": round(abytes / (app_ms / 1e3) / 1e9, 1),
                    "rope": rope is not None},
+        "schedule": schedule,
+        "ms_per_step_eager_serial": round(ms_serial, 4),
+        "ms_per_step_graph_serial": None if ms_graph_serial is None else round(ms_graph_serial, 4),
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
