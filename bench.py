@@ -15,6 +15,7 @@ decode math timed on this host on a bounded sample (see --cpu-layers).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -69,6 +70,9 @@ def main() -> int:
     ap.add_argument("--serial", action="store_true",
                     help="cfg2: time eager launches on one stream only (default: the step as "
                          "a HIP graph with each layer's decode on a second stream)")
+    ap.add_argument("--kv-dtype", choices=["f32", "f16", "bf16"], default=None,
+                    help="decode configs: pool dtype instead of the config's (f32 is the "
+                         "reference's KvPool dtype)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="minimum layer passes of the CPU baseline sample (0 = skip it)")
@@ -111,6 +115,11 @@ def main() -> int:
         return gather_bench(args, dev)
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
+    if args.kv_dtype:
+        # another pool dtype on the same shape (f32: the reference's own KvPool)
+        shape = dataclasses.replace(shape, dtype={"f32": wl.F32, "f16": wl.F16,
+                                                  "bf16": wl.BF16}[args.kv_dtype])
+        desc += f" [KV pool in {args.kv_dtype}]"
     L, H, KVH, hd, bs = shape.n_layers, shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
     tdt = pagedkv.torch_dtype(shape.dtype)
     num_blocks = 2048 if args.config == "cfg1" else None
@@ -245,8 +254,9 @@ def main() -> int:
     if os.path.exists(prof):
         with open(prof) as f:
             tr = json.load(f)
-        if tr.get("seed") == args.seed and tr.get("config") == args.config:
-            traffic = tr.get("bytes_per_launch")
+        if (tr.get("seed") == args.seed and tr.get("config") == args.config
+                and not args.kv_dtype and not args.rope):
+            traffic = tr.get("bytes_per_launch")  # measured for the config's own dtype
 
     cpu = None
     if args.cpu_layers > 0 and not args.rope:
