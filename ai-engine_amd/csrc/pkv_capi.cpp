@@ -414,6 +414,29 @@ int pkv_gather_seq(pkv_pool* p, int layer, const int32_t* block_table, int len,
   return PKV_OK;
 }
 
+int pkv_gather_varlen(pkv_pool* p, int layer, const int32_t* block_tables,
+                      int max_blocks_per_seq, const int32_t* cu_lens, int batch, int total_rows,
+                      void* out_k, void* out_v, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (batch < 0 || total_rows < 0)
+    return fail(p, PKV_ERR_INVALID, "batch %d, total_rows %d", batch, total_rows);
+  if (batch > 4096) return fail(p, PKV_ERR_UNSUPPORTED, "gather_varlen: batch %d > 4096", batch);
+  if (batch == 0 || total_rows == 0) return PKV_OK;
+  if (max_blocks_per_seq <= 0)
+    return fail(p, PKV_ERR_INVALID, "max_blocks_per_seq %d <= 0", max_blocks_per_seq);
+  if (!block_tables || !cu_lens || !out_k || !out_v)
+    return fail(p, PKV_ERR_INVALID, "block_tables, cu_lens, out_k and out_v must be non-NULL");
+  if (!aligned16(out_k) || !aligned16(out_v))
+    return fail(p, PKV_ERR_INVALID, "out_k and out_v must be 16-byte aligned");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_gather_varlen(p, layer, block_tables, max_blocks_per_seq, cu_lens,
+                                           batch, total_rows, out_k, out_v,
+                                           static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "gather_varlen launch");
+  return PKV_OK;
+}
+
 static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee);
 
 int pkv_copy_blocks(pkv_pool* p, const int32_t* src, const int32_t* dst, int n, void* stream) {

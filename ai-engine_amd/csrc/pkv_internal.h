@@ -87,6 +87,9 @@ hipError_t launch_append(const pkv_pool* p, int layer, const void* k,
 hipError_t launch_gather(const pkv_pool* p, int layer, const int32_t* table,
                          int len, void* out_k, void* out_v,
                          hipStream_t stream);
+hipError_t launch_gather_varlen(const pkv_pool* p, int layer, const int32_t* tables, int mbps,
+                                const int32_t* cu_lens, int batch, int total_rows, void* out_k,
+                                void* out_v, hipStream_t stream);
 hipError_t launch_copy_blocks(const pkv_pool* p, const int32_t* src,
                               const int32_t* dst, int n, hipStream_t stream);
 // Compaction: ops[] holds (src, dst) pairs executed in order within each

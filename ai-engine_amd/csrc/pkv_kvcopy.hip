@@ -65,6 +65,46 @@ __global__ void __launch_bounds__(kCopyThreads)
   ov[i] = b;
 }
 
+// Gather of several sequences: thread per 16-byte chunk of an output row;
+// the row's sequence is found by a binary search of cu_lens held in LDS
+// (batch <= kVarlenMaxBatch).  Sequence b's row r is its position r.
+constexpr int kVarlenMaxBatch = 4096;
+__global__ void __launch_bounds__(kCopyThreads)
+    gather_varlen_kernel(const u32x4* __restrict__ kp, const u32x4* __restrict__ vp,
+                         u32x4* __restrict__ ok, u32x4* __restrict__ ov,
+                         const int32_t* __restrict__ tables, int mbps,
+                         const int32_t* __restrict__ cu_lens, int batch, int total_rows,
+                         int row_vec, int bs_log2, int num_blocks, uint32_t* err) {
+  __shared__ int cu[kVarlenMaxBatch + 1];
+  for (int i = threadIdx.x; i <= batch; i += kCopyThreads) cu[i] = cu_lens[i];
+  __syncthreads();
+  const long long i = (long long)blockIdx.x * kCopyThreads + threadIdx.x;
+  if (i >= (long long)total_rows * row_vec) return;
+  const int row = (int)(i / row_vec);
+  const int c = (int)(i - (long long)row * row_vec);
+  // last b with cu[b] <= row
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= row) lo = mid;
+    else hi = mid - 1;
+  }
+  const int p = row - cu[lo];
+  const int tb = p >> bs_log2;
+  const int blk = tb < mbps && p >= 0 ? tables[(size_t)lo * mbps + tb] : -1;
+  if (blk < 0 || blk >= num_blocks) {
+    if (c == 0) atomicOr(err, PKV_EBIT_BLOCK);
+    ok[i] = u32x4{0, 0, 0, 0};
+    ov[i] = u32x4{0, 0, 0, 0};
+    return;
+  }
+  const size_t o = (((size_t)blk << bs_log2) + (p & ((1 << bs_log2) - 1))) * row_vec + c;
+  const u32x4 a = kp[o];
+  const u32x4 b = vp[o];
+  ok[i] = a;
+  ov[i] = b;
+}
+
 // Copy-on-write: items (pair, K/V slab of a layer, chunk of a block), chunk
 // fastest; each workgroup moves items blockIdx.x, + gridDim.x, ... and each
 // thread kVecPerThread 16-byte vectors of an item, all loads before the
@@ -241,6 +281,22 @@ hipError_t launch_gather(const pkv_pool* p, int layer, const int32_t* table,
       reinterpret_cast<const u32x4*>(p->layer_v(layer)),
       reinterpret_cast<u32x4*>(out_k), reinterpret_cast<u32x4*>(out_v), table,
       len, row_vec, ilog2(p->block_size), p->num_blocks, p->err);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_varlen(const pkv_pool* p, int layer, const int32_t* tables, int mbps,
+                                const int32_t* cu_lens, int batch, int total_rows, void* out_k,
+                                void* out_v, hipStream_t stream) {
+  if (total_rows <= 0 || batch <= 0) return hipSuccess;
+  if (batch > kVarlenMaxBatch) return hipErrorInvalidValue;
+  const int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
+  const long long total = (long long)total_rows * row_vec;
+  const unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
+  gather_varlen_kernel<<<grid, kCopyThreads, 0, stream>>>(
+      reinterpret_cast<const u32x4*>(p->layer_k(layer)),
+      reinterpret_cast<const u32x4*>(p->layer_v(layer)), reinterpret_cast<u32x4*>(out_k),
+      reinterpret_cast<u32x4*>(out_v), tables, mbps, cu_lens, batch, total_rows, row_vec,
+      ilog2(p->block_size), p->num_blocks, p->err);
   return hipGetLastError();
 }
 

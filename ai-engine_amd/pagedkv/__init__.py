@@ -423,6 +423,27 @@ class KvPool:
                                    _dev_ptr(ok), _dev_ptr(ov), _stream_ptr(stream)), self._h)
         return ok, ov
 
+    def gather_varlen(self, block_tables, lengths, stream=None):
+        """Several sequences' K/V in one launch: rows of sequence b at
+        cu[b] .. cu[b+1]-1 of the returned (total, n_kv, hd) K and V, where
+        cu = [0, cumsum(lengths)]; returns (k, v, cu) with cu on the device."""
+        import numpy as np
+        import torch
+        c = self.cache
+        lens = np.asarray(lengths, np.int64)
+        cu_np = np.zeros(lens.size + 1, np.int32)
+        cu_np[1:] = np.cumsum(lens)
+        total = int(cu_np[-1])
+        bt = _i32(block_tables, c.device)
+        cu = torch.from_numpy(cu_np).to(c.device)
+        ok = torch.empty((total, c.n_kv_head, c.head_dim), dtype=c.dtype, device=c.device)
+        ov = torch.empty_like(ok)
+        if total:
+            check(lib().pkv_gather_varlen(self._h, self.layer_index, _dev_ptr(bt), bt.shape[1],
+                                          _dev_ptr(cu), lens.size, total, _dev_ptr(ok),
+                                          _dev_ptr(ov), _stream_ptr(stream)), self._h)
+        return ok, ov, cu
+
     # -- decode attention ---------------------------------------------------
     def decode_attention(self, q, block_tables, context_lens, max_context_len: int | None = None,
                          k_new=None, v_new=None, scale: float | None = None, out_dtype=None,

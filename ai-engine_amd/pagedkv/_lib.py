@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_append": (_I, [_P, _I, _P, _P, _P, _I, _P]),
     "pkv_append_rope": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
     "pkv_gather_seq": (_I, [_P, _I, _P, _I, _P, _P, _P]),
+    "pkv_gather_varlen": (_I, [_P, _I, _P, _I, _P, _I, _I, _P, _P, _P]),
     "pkv_copy_blocks": (_I, [_P, _P, _P, _I, _P]),
     "pkv_compact": (_I, [_P, _I32P, _I32P, _I, _P]),
     "pkv_decode_attention": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I,

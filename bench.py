@@ -364,6 +364,41 @@ def gather_bench(args, dev) -> int:
     if not ok:
         print(json.dumps({"error": "gather differs from the oracle"}))
         return 1
+    # the same rows by one pkv_gather_varlen call (no reference counterpart),
+    # checked equal to the per-sequence outputs
+    mb = max(t.numel() for t in tables)
+    vt = torch.zeros((B, mb), dtype=torch.int32, device=dev)
+    for b in range(B):
+        vt[b, :tables[b].numel()] = tables[b]
+    total = int(lens.sum())
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(dev)
+    vk = torch.empty((total, KVH, hd), dtype=torch.bfloat16, device=dev)
+    vv = torch.empty_like(vk)
+    sp0 = int(torch.cuda.current_stream(dev).cuda_stream) or None
+
+    def varlen():
+        rc = lib.pkv_gather_varlen(h, 0, vt.data_ptr(), mb, cu.data_ptr(), B, total,
+                                   vk.data_ptr(), vv.data_ptr(), sp0)
+        if rc:
+            pagedkv._lib.check(rc, h)
+    for _ in range(max(1, args.warmup)):
+        varlen()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        varlen()
+    e1.record()
+    torch.cuda.synchronize()
+    cache.check()
+    ms_varlen = e0.elapsed_time(e1) / args.steps
+    same = all(torch.equal(vk[int(c0):int(c0) + int(n)], outs[b][0]) and
+               torch.equal(vv[int(c0):int(c0) + int(n)], outs[b][1])
+               for b, (c0, n) in enumerate(zip(np.concatenate([[0], np.cumsum(lens)])[:-1], lens)))
+    log(f"[bench] gather_varlen (one call): {ms_varlen * 1e3:.1f} us "
+        f"({gbytes / (ms_varlen / 1e3) / 1e9:.0f} GB/s), equal to the per-sequence calls: {same}")
+    if not same:
+        print(json.dumps({"error": "gather_varlen differs from gather_seq"}))
+        return 1
     cpu = None
     if args.cpu_layers > 0:
         tb = batch.tables.astype(np.uint32)
@@ -389,6 +424,9 @@ def gather_bench(args, dev) -> int:
                      "frac": round(gbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "pkv::gather_kernel", "kernel_avg_us": round(ms * 1e3 / B, 2),
                      "algorithmic_bytes_per_launch": gbytes // B},
+        "varlen_one_call": {"us": round(ms_varlen * 1e3, 2),
+                            "GBps": round(gbytes / (ms_varlen / 1e3) / 1e9, 1),
+                            "kernel": "pkv::gather_varlen_kernel"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

@@ -115,6 +115,21 @@ int pkv_append(pkv_pool* pool, int layer, const void* k, const void* v,
 int pkv_gather_seq(pkv_pool* pool, int layer, const int32_t* block_table,
                    int len, void* out_k, void* out_v, void* stream);
 
+/* ---- gather of several sequences in one launch (no reference counterpart:
+ * the batched form of gather_seq for callers that want the K/V of many
+ * sequences contiguous, e.g. a varlen attention kernel) ------------------
+ * Sequence b's positions 0 .. cu_lens[b+1]-cu_lens[b]-1 are copied, bit for
+ * bit as by pkv_gather_seq with block_tables[b], to rows cu_lens[b] ..
+ * cu_lens[b+1]-1 of out_k / out_v ([total_rows][n_kv_head][head_dim]).
+ * cu_lens: device int32 [batch+1], cu_lens[0] = 0, nondecreasing;
+ * total_rows = cu_lens[batch] (host value).  block_tables: device int32
+ * [batch][max_blocks_per_seq].  batch <= 4096.  A block id out of range, or
+ * a length beyond the table, zeroes those rows and is reported by
+ * pkv_pool_check(). */
+int pkv_gather_varlen(pkv_pool* pool, int layer, const int32_t* block_tables,
+                      int max_blocks_per_seq, const int32_t* cu_lens, int batch,
+                      int total_rows, void* out_k, void* out_v, void* stream);
+
 /* ---- block copy (copy-on-write after fork; no reference counterpart) ----
  * For every layer and both K and V: block dst[i] <- block src[i], i < n.
  * src, dst: device int32 [n].  dst ids must be distinct and no dst may be a

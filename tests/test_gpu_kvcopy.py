@@ -123,6 +123,58 @@ def test_gather_bit_exact(gpu, dt):
     cache.close()
 
 
+@pytest.mark.parametrize("dt,bs", [(wl.BF16, 16), (wl.F32, 32)])
+def test_gather_varlen_equals_per_sequence_gathers(gpu, dt, bs):
+    # several sequences in one launch: each sequence's rows equal its own
+    # gather_seq and the oracle's, bit for bit; empty sequences and a ragged
+    # last block included
+    kvh, hd, nb = 4, 128, 200
+    cache = pagedkv.PagedKvCache(2, nb, bs, kvh, hd, TD[dt])
+    _fill(cache, 8)
+    kp, vp = _host_pool(cache, 1)
+    lens = [0, 1, bs - 1, bs, bs + 1, 5 * bs + 3, 0, 17 * bs]
+    need = [-(-n // bs) for n in lens]
+    mbps = max(need)
+    perm = wl.permutation(4, nb)
+    tables = np.zeros((len(lens), mbps), np.int32)
+    o = 0
+    for b, k in enumerate(need):
+        tables[b, :k] = perm[o:o + k]
+        o += k
+    pool = cache.layer(1)
+    gk, gv, cu = pool.gather_varlen(torch.from_numpy(tables).to(gpu), lens)
+    torch.cuda.synchronize()
+    cache.check()
+    assert cu.cpu().tolist() == [0] + list(np.cumsum(lens))
+    view = (lambda t: t.cpu().numpy()) if dt == wl.F32 else (
+        lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16))
+    c = cu.cpu().numpy()
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        ok, ov = oracle.gather_seq(kp, vp, bs, tables[b].astype(np.uint32), n)
+        assert np.array_equal(view(gk[c[b]:c[b + 1]]), ok)
+        assert np.array_equal(view(gv[c[b]:c[b + 1]]), ov)
+        sk, sv = pool.gather_seq(tables[b, :need[b]].tolist(), n)
+        assert torch.equal(sk, gk[c[b]:c[b + 1]]) and torch.equal(sv, gv[c[b]:c[b + 1]])
+    cache.close()
+
+
+def test_gather_varlen_bad_block_reported(gpu):
+    cache = pagedkv.PagedKvCache(1, 8, 16, 2, 64, torch.float16)
+    _fill(cache, 3)
+    tables = torch.tensor([[0, 1], [2, 99]], dtype=torch.int32, device=gpu)
+    gk, gv, _ = cache.layer(0).gather_varlen(tables, [20, 20])
+    torch.cuda.synchronize()
+    with pytest.raises(pagedkv.PagedKvError):
+        cache.check()
+    assert torch.count_nonzero(gk[36:]) == 0        # rows 16..19 of sequence 1: block 99
+    assert torch.count_nonzero(gv[36:]) == 0
+    assert bool((gk[:36] != 0).any(dim=(1, 2)).all())   # every valid row holds data
+    cache.check()                                   # the error was cleared
+    cache.close()
+
+
 def _all_bytes(cache):
     return np.concatenate([np.concatenate([cache.read_bytes(l, pagedkv.K), cache.read_bytes(l, pagedkv.V)])
                            for l in range(cache.n_layers)])
