@@ -590,11 +590,12 @@ int pkv_decode_attention_rope(pkv_pool* p, int layer, const pkv_rope* rope,
   return decode_call(p, layer, a, stream);
 }
 
-int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
-                          const int32_t* cu_q_lens, const int32_t* context_lens,
-                          const int32_t* block_tables, int max_blocks_per_seq, int n_seqs,
-                          int max_q_len, int max_context_len, int n_head, float scale,
-                          void* stream) {
+namespace {
+int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
+                 const int32_t* cu_q_lens, const int32_t* context_lens,
+                 const int32_t* block_tables, int max_blocks_per_seq, int n_seqs, int max_q_len,
+                 int max_context_len, int n_head, float scale, const void* k_new,
+                 const void* v_new, void* stream) {
   CHECK_POOL(p);
   if (int rc = check_layer(p, layer)) return rc;
   if (n_seqs < 0) return fail(p, PKV_ERR_INVALID, "n_seqs %d < 0", n_seqs);
@@ -603,6 +604,9 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
     return fail(p, PKV_ERR_INVALID, "q, out, cu_q_lens, context_lens, block_tables must be non-NULL");
   if (!aligned16(q) || !aligned16(out))
     return fail(p, PKV_ERR_INVALID, "q and out must be 16-byte aligned");
+  if (!k_new != !v_new) return fail(p, PKV_ERR_INVALID, "k_new and v_new: both or neither");
+  if (k_new && (!aligned16(k_new) || !aligned16(v_new)))
+    return fail(p, PKV_ERR_INVALID, "k_new and v_new must be 16-byte aligned");
   if (max_q_len < 0 || max_blocks_per_seq <= 0 || max_context_len <= 0)
     return fail(p, PKV_ERR_INVALID, "max_q_len, max_blocks_per_seq, max_context_len must be > 0");
   if (n_head <= 0 || n_head % p->n_kv_head != 0)
@@ -622,12 +626,36 @@ int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int 
       if (int rc = ensure_workspace(p, p->ws_counter_bytes + need, p->ws_counter_bytes)) return rc;
   }
   pkv::PrefillArgs a{q, out, out_dtype, cu_q_lens, context_lens, block_tables,
-                     max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale};
+                     max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale,
+                     k_new, v_new};
   hipEvent_t eb = nullptr, ee = nullptr;
   if (int rc = profile_slot(p, &eb, &ee)) return rc;
   hipError_t e = pkv::launch_prefill(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "prefill launch");
   return PKV_OK;
+}
+}  // namespace
+
+int pkv_prefill_attention(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
+                          const int32_t* cu_q_lens, const int32_t* context_lens,
+                          const int32_t* block_tables, int max_blocks_per_seq, int n_seqs,
+                          int max_q_len, int max_context_len, int n_head, float scale,
+                          void* stream) {
+  return prefill_call(p, layer, q, out, out_dtype, cu_q_lens, context_lens, block_tables,
+                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale,
+                      nullptr, nullptr, stream);
+}
+
+int pkv_prefill_attention_append(pkv_pool* p, int layer, const void* q, void* out,
+                                 int out_dtype, const int32_t* cu_q_lens,
+                                 const int32_t* context_lens, const int32_t* block_tables,
+                                 int max_blocks_per_seq, int n_seqs, int max_q_len,
+                                 int max_context_len, int n_head, float scale, const void* k_new,
+                                 const void* v_new, void* stream) {
+  if (p && (!k_new || !v_new)) return fail(p, PKV_ERR_INVALID, "k_new and v_new must be non-NULL");
+  return prefill_call(p, layer, q, out, out_dtype, cu_q_lens, context_lens, block_tables,
+                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale,
+                      k_new, v_new, stream);
 }
 
 size_t pkv_prefill_workspace_bytes(const pkv_pool* p, int n_seqs, int n_head, int max_q_len,

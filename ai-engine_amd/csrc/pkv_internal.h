@@ -159,6 +159,9 @@ struct PrefillArgs {
   int max_context_len;
   int n_head;
   float scale;
+  // fused store of the prompt's K/V ([total_q][n_kv][hd], pool dtype), or null
+  const void* k_new = nullptr;
+  const void* v_new = nullptr;
 };
 bool prefill_supported(const pkv_pool* p, int n_head);
 // Split of long key ranges for launches with few row blocks: keys per part,

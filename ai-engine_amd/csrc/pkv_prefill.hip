@@ -126,6 +126,11 @@ struct PrefillKArgs {
   float* part_ml;  // split key ranges: (m, l) per (item, row)
   float* part_o;   //   and the unnormalised O row
   uint32_t* err;
+  // Fused store of the prompt's own K/V ([total_q][kvh][hd], pool dtype),
+  // or null: keys at or past a sequence's prior context are read from these
+  // rows, and each workgroup stores its own tokens' rows into the pool.
+  const char* k_new;
+  const char* v_new;
 };
 
 // Parts of a row block whose rows have prior context `prior`: every part but
@@ -166,7 +171,7 @@ __device__ __forceinline__ uint32_t cvt_pk16(float x0, float x1) {
   }
 }
 
-template <int DT, int HD, int R>
+template <int DT, int HD, int R, bool FUSED>
 __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   using C = PCfg<DT, HD, R>;
   __shared__ __attribute__((aligned(16))) char lds[2 * C::STAGE];
@@ -228,6 +233,40 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const int n_keys = prior + min(row0 + C::ROWS - 1, n_rows - 1) / R + 1;
   const int nparts = n_parts_of(prior, a.part_keys);
   if (part >= nparts) return;  // uniform over the workgroup
+
+  // Fused store of the K/V rows of the chunk's tokens at positions prior + i
+  // (row blocks partition the tokens; ROWS is a multiple of R).  The store's
+  // load round trip must not lengthen the heaviest row blocks (the last
+  // ones, which see the most keys): row block rb of the sequence's nrb
+  // stores its own tokens and those of its mirror nrb - 1 - rb when rb is
+  // the lighter of the two, nothing when it is the heavier; only the last
+  // part of a row block stores.  No workgroup of this launch reads these rows
+  // from the pool: keys >= prior come from k_new / v_new.
+  const char* kin = FUSED ? a.k_new + (size_t)g * C::RB : nullptr;
+  const char* vin = FUSED ? a.v_new + (size_t)g * C::RB : nullptr;
+  const int nrb = (n_rows + C::ROWS - 1) / C::ROWS;
+  const int mirror = nrb - 1 - rb;
+  if (FUSED && part == nparts - 1 && rb <= mirror) {
+    const int tpb = C::ROWS / R;  // tokens per row block
+    const int own = (min(row0 + C::ROWS, n_rows) - row0) / R;
+    const int mir = rb < mirror ? (min((mirror + 1) * C::ROWS, n_rows) - mirror * C::ROWS) / R : 0;
+    const int nch = (own + mir) * C::CH;
+    for (int idx = tid; idx < nch; idx += kPT) {
+      const int j = idx / C::CH, c16 = 16 * (idx % C::CH);
+      const int tok = j < own ? rb * tpb + j : mirror * tpb + (j - own);
+      const int pos = prior + tok;
+      const int blk = table[pos >> a.bs_log2];
+      if ((unsigned)blk >= (unsigned)a.num_blocks) {
+        atomicOr(a.err, PKV_EBIT_BLOCK);
+        continue;
+      }
+      const size_t off = (size_t)blk * blk_stride + (size_t)(pos & tmask) * slot_stride + c16;
+      const size_t src = (size_t)(q0 + tok) * a.kvh * C::RB + c16;
+      const u32x4 kx = ld16(kin + src), vx = ld16(vin + src);
+      st16(const_cast<char*>(kh) + off, kx);
+      st16(const_cast<char*>(vh) + off, vx);
+    }
+  }
   const int k_hi = part + 1 < nparts ? (part + 1) * a.part_keys : n_keys;
   const int t_lo = part * (a.part_keys / C::KT);
   const int n_tiles = (k_hi + C::KT - 1) / C::KT;  // tiles t_lo .. n_tiles - 1
@@ -280,29 +319,53 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
     }
   };
   u32x4 kreg[C::NSET][C::NKL], vreg[C::NSET][C::NVP][2];
-  auto loads = [&](int t, u32x4 (&kr)[C::NKL], u32x4 (&vr)[C::NVP][2],
-                   const int (&kbs)[C::NKL], const int (&vbs)[C::NVP]) __attribute__((always_inline)) {
+  // A tile's K/V rows: from the pool, or (fused store) from the prompt's
+  // rows for keys >= prior.  MODE 0: every key from the pool; 1: every key
+  // from the prompt (keys past n_keys are clamped to n_keys - 1 >= prior);
+  // 2: the one tile that straddles the prior, chosen per key.
+  auto loads_m = [&](int t, u32x4 (&kr)[C::NKL], u32x4 (&vr)[C::NVP][2],
+                     const int (&kbs)[C::NKL], const int (&vbs)[C::NVP], auto mode_c)
+                     __attribute__((always_inline)) {
+    constexpr int MODE = decltype(mode_c)::value;
+    auto src = [&](const char* pool_row_base, const char* in, int key) __attribute__((always_inline)) {
+      if constexpr (MODE == 1) return in + (size_t)(q0 + key - prior) * a.kvh * C::RB + lbyte;
+      const char* pr = pool_row_base + ((uint32_t)((key & tmask) * slot_stride) + lbyte);
+      if constexpr (MODE == 0) return pr;
+      return key < prior ? pr : in + (size_t)(q0 + key - prior) * a.kvh * C::RB + lbyte;
+    };
 #pragma unroll
     for (int i = 0; i < C::NKL; ++i) {
       const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
-      const char* base = kh + (size_t)checked(kbs[i]) * blk_stride;
-      kr[i] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
+      kr[i] = ld16(src(kh + (size_t)checked(kbs[i]) * blk_stride, kin, key));
     }
     if constexpr (DT == PKV_F32) {
 #pragma unroll
       for (int v = 0; v < C::NVP; ++v) {
         const int k0 = t * C::KT + 2 * (wkey + kPT * v / C::CH + lkey);
         const char* base = vh + (size_t)checked(vbs[v]) * blk_stride;
-        vr[v][0] = ld16(base + ((uint32_t)((min(k0, n_keys - 1) & tmask) * slot_stride) + lbyte));
-        vr[v][1] = ld16(base + ((uint32_t)((min(k0 + 1, n_keys - 1) & tmask) * slot_stride) + lbyte));
+        vr[v][0] = ld16(src(base, vin, min(k0, n_keys - 1)));
+        vr[v][1] = ld16(src(base, vin, min(k0 + 1, n_keys - 1)));
       }
     } else {  // V chunk 2 v + h: the same key and bytes as K chunk 2 v + h
 #pragma unroll
       for (int i = 0; i < C::NKL; ++i) {
         const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
-        const char* base = vh + (size_t)checked(kbs[i]) * blk_stride;
-        vr[i >> 1][i & 1] = ld16(base + ((uint32_t)((key & tmask) * slot_stride) + lbyte));
+        vr[i >> 1][i & 1] = ld16(src(vh + (size_t)checked(kbs[i]) * blk_stride, vin, key));
       }
+    }
+  };
+  auto loads = [&](int t, u32x4 (&kr)[C::NKL], u32x4 (&vr)[C::NVP][2],
+                   const int (&kbs)[C::NKL], const int (&vbs)[C::NVP]) __attribute__((always_inline)) {
+    if constexpr (!FUSED) {
+      loads_m(t, kr, vr, kbs, vbs, std::integral_constant<int, 0>{});
+    } else {
+      const int tk0 = t * C::KT;  // wave-uniform choice of path
+      if (tk0 + C::KT <= prior)
+        loads_m(t, kr, vr, kbs, vbs, std::integral_constant<int, 0>{});
+      else if (tk0 >= prior)
+        loads_m(t, kr, vr, kbs, vbs, std::integral_constant<int, 1>{});
+      else
+        loads_m(t, kr, vr, kbs, vbs, std::integral_constant<int, 2>{});
     }
   };
   auto store = [&](int stage, const u32x4 (&kr)[C::NKL], const u32x4 (&vr)[C::NVP][2]) __attribute__((always_inline)) {
@@ -689,7 +752,10 @@ hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
     k.per_xcd = (int)per;
     grid = per * kXcd;
   }
-  prefill_kernel<DT, HD, R><<<(unsigned)grid, kPT, 0, s>>>(k);
+  if (k.k_new)
+    prefill_kernel<DT, HD, R, true><<<(unsigned)grid, kPT, 0, s>>>(k);
+  else
+    prefill_kernel<DT, HD, R, false><<<(unsigned)grid, kPT, 0, s>>>(k);
   return hipGetLastError();
 }
 
@@ -802,6 +868,8 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
   k.max_context_len = a.max_context_len;
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.err = p->err;
+  k.k_new = reinterpret_cast<const char*>(a.k_new);
+  k.v_new = reinterpret_cast<const char*>(a.v_new);
   size_t ws = 0;
   prefill_plan(p, a.n_seqs, a.n_head, a.max_q_len, a.max_context_len, &k.part_keys,
                &k.max_parts, &ws);

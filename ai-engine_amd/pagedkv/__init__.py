@@ -521,7 +521,11 @@ class KvPool:
     # -- chunked prefill attention -------------------------------------------
     def prefill_attention(self, q, cu_q_lens, context_lens, block_tables, max_q_len: int,
                           max_context_len: int, scale: float | None = None, out_dtype=None,
-                          out=None, stream=None):
+                          out=None, stream=None, k_new=None, v_new=None):
+        """Causal attention of prompt chunks over prior context + chunk.  With
+        k_new / v_new (total_q, n_kv, hd), the chunk's K/V are stored in the
+        same launch (pkv_prefill_attention_append); without, they must
+        already be in the pool."""
         import torch
         c = self.cache
         T, H, hd = q.shape
@@ -534,11 +538,16 @@ class KvPool:
         bt = _i32(block_tables, c.device)
         if out is None:
             out = torch.empty((T, H * hd), dtype=out_dtype, device=c.device)
-        check(lib().pkv_prefill_attention(
-            self._h, self.layer_index, _dev_ptr(q.contiguous()), _dev_ptr(out),
-            pkv_dtype(out.dtype), _dev_ptr(cu), _dev_ptr(cl), _dev_ptr(bt), bt.shape[1],
-            cl.numel(), int(max_q_len), int(max_context_len), H, float(scale),
-            _stream_ptr(stream)), self._h)
+        args = [self._h, self.layer_index, _dev_ptr(q.contiguous()), _dev_ptr(out),
+                pkv_dtype(out.dtype), _dev_ptr(cu), _dev_ptr(cl), _dev_ptr(bt), bt.shape[1],
+                cl.numel(), int(max_q_len), int(max_context_len), H, float(scale)]
+        if k_new is not None or v_new is not None:
+            self._check_rows(k_new, "k_new")
+            self._check_rows(v_new, "v_new")
+            check(lib().pkv_prefill_attention_append(*args, _dev_ptr(k_new), _dev_ptr(v_new),
+                                                     _stream_ptr(stream)), self._h)
+        else:
+            check(lib().pkv_prefill_attention(*args, _stream_ptr(stream)), self._h)
         return out
 
     def _check_rows(self, t, name: str) -> None:

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_pool_reserve_decode": (_I, [_P, _I, _I, _I]),
     "pkv_prefill_attention": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                    ctypes.c_float, _P]),
+    "pkv_prefill_attention_append": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
+                                          ctypes.c_float, _P, _P, _P]),
     "pkv_pool_check": (_I, [_P]),
     "pkv_prefill_workspace_bytes": (_SZ, [_P, _I, _I, _I, _I]),
     "pkv_pool_reserve_prefill": (_I, [_P, _I, _I, _I, _I]),

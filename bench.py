@@ -70,6 +70,8 @@ def main() -> int:
     ap.add_argument("--serial", action="store_true",
                     help="cfg2: time eager launches on one stream only (default: the step as "
                          "a HIP graph with each layer's decode on a second stream)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="cfg2: store the chunk's K/V with a separate pkv_append launch")
     ap.add_argument("--kv-dtype", choices=["f32", "f16", "bf16"], default=None,
                     help="decode configs: pool dtype instead of the config's (f32 is the "
                          "reference's KvPool dtype)")
@@ -704,6 +706,24 @@ def mix(args, dev) -> int:
         if rc:
             chk(rc, h)
 
+    def prefill_store(l):
+        # the chunk's K/V stored by the prefill launch itself
+        rc = lib.pkv_prefill_attention_append(h, l, qp[l].data_ptr(), outp[l].data_ptr(), odt,
+                                              cu.data_ptr(), pctx.data_ptr(), ptab.data_ptr(),
+                                              mbps, NP, C, max_p, H, sc, kc[l].data_ptr(),
+                                              vc[l].data_ptr(), sp)
+        if rc:
+            chk(rc, h)
+
+    fused_store = rope is None and not args.unfused
+
+    def chunk(l):
+        if fused_store:
+            prefill_store(l)
+        else:
+            append(l)
+            prefill(l)
+
     def decode(l, on=None):
         st = on if on is not None else sp
         if rope is not None:
@@ -729,8 +749,7 @@ def mix(args, dev) -> int:
 
     def step_serial():
         for l in range(L):
-            append(l)
-            prefill(l)
+            chunk(l)
             decode(l)
 
     def step_overlap():
@@ -738,8 +757,7 @@ def mix(args, dev) -> int:
             forks[l].record(stream)
             dec_stream.wait_event(forks[l])
             decode(l, dsp)
-            append(l)
-            prefill(l)
+            chunk(l)
             joins[l].record(dec_stream)
             stream.wait_event(joins[l])
 
@@ -816,7 +834,7 @@ def mix(args, dev) -> int:
         cache.profile(False)
         return tot / max(1, n), n
 
-    pre_ms, pre_n = kernel_ms(prefill)
+    pre_ms, pre_n = kernel_ms(prefill_store if fused_store else prefill)
     dec_ms, dec_n = kernel_ms(decode)
     t0.record(stream)
     for _ in range(n_kt):
@@ -900,6 +918,8 @@ def mix(args, dev) -> int:
         "append": {"us": round(app_ms * 1e3, 2), "GBps": round(abytes / (app_ms / 1e3) / 1e9, 1),
                    "rope": rope is not None},
         "schedule": schedule,
+        "chunk_store": ("fused into the prefill launch (pkv_prefill_attention_append)"
+                        if fused_store else "separate launch (append us above)"),
         "ms_per_step_eager_serial": round(ms_serial, 4),
         "ms_per_step_graph_serial": None if ms_graph_serial is None else round(ms_graph_serial, 4),
         "cpu_baseline": cpu,

@@ -204,6 +204,25 @@ int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int n_seqs, int max_q_len, int max_context_len,
                           int n_head, float scale, void* stream);
 
+/* pkv_prefill_attention with the chunk's K/V stored in the same launch (the
+ * reference stores every prompt token with KvPool::write before attending,
+ * transformer.rs:173-177; pkv_append + pkv_prefill_attention in one call).
+ * k_new, v_new: [total_q][n_kv_head][head_dim] in the pool dtype, 16-byte
+ * aligned; token i of sequence s is stored at its position
+ * context_lens[s] - q_len_s + i (slot from block_tables) and attended from
+ * these rows, so the result and the pool afterwards equal pkv_append
+ * followed by pkv_prefill_attention.  A block id out of range is reported by
+ * pkv_pool_check(). */
+int pkv_prefill_attention_append(pkv_pool* pool, int layer, const void* q,
+                                 void* out, int out_dtype,
+                                 const int32_t* cu_q_lens,
+                                 const int32_t* context_lens,
+                                 const int32_t* block_tables,
+                                 int max_blocks_per_seq, int n_seqs,
+                                 int max_q_len, int max_context_len,
+                                 int n_head, float scale, const void* k_new,
+                                 const void* v_new, void* stream);
+
 /* Workspace of pkv_prefill_attention for the given launch shape: launches
  * with few row blocks (fewer than can fill the GPU) split long key ranges
  * into parts that are merged afterwards, with partial results in the pool's

@@ -211,3 +211,71 @@ def test_split_workspace_reserved_up_front(gpu):
     assert c.cache.prefill_workspace_bytes(512, 8, 2048, 8192) == 0
     assert need > 0
     c.close()
+
+
+# -- the chunk's K/V stored in the same launch (pkv_prefill_attention_append) --
+def _slots(case):
+    """Pool slots of every chunk token (positions prior + i), in token order."""
+    out = []
+    for s in range(len(case.chunks)):
+        for i in range(int(case.chunks[s])):
+            pos = int(case.priors[s]) + i
+            out.append(int(case.tables[s, pos // case.bs]) * case.bs + pos % case.bs)
+    return np.asarray(out, np.int32)
+
+
+@pytest.mark.parametrize("dt,hd,R,bs", [(wl.F16, 64, 8, 16), (wl.BF16, 128, 4, 16),
+                                        (wl.BF16, 64, 1, 32), (wl.F32, 128, 2, 16),
+                                        (wl.BF16, 256, 2, 64), (wl.F16, 128, 8, 128)])
+def test_fused_store_equals_append_then_prefill(gpu, dt, hd, R, bs):
+    # same attention output and same pool bytes, bit for bit, as pkv_append
+    # followed by pkv_prefill_attention; chunks that start and end mid-block,
+    # an empty prior, a one-token chunk and a prior long enough to split
+    KVH = 2
+    priors, chunks = [0, 37, 300, 1, 4100], [45, 130, 1, 64, 20]
+    a = PCase(gpu, dt, R * KVH, KVH, hd, bs, priors, chunks, seed=hd + R + bs)
+    b = PCase(gpu, dt, R * KVH, KVH, hd, bs, priors, chunks, seed=hd + R + bs)
+    T = int(a.cu[-1])
+    kn = wl.normal_storage(hd + 91, (T, KVH, hd), dt)
+    vn = wl.normal_storage(hd + 92, (T, KVH, hd), dt)
+    knd, vnd = _to_dev(kn, dt, gpu), _to_dev(vn, dt, gpu)
+    args = dict(max_q_len=int(max(chunks)), max_context_len=int(a.ctx.max()), scale=a.scale,
+                out_dtype=torch.float32)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+    qd = _to_dev(a.q, dt, gpu)
+    a.cache.layer(0).append(knd, vnd, _slots(a))
+    ref = a.cache.layer(0).prefill_attention(qd, dev(a.cu), dev(a.ctx), dev(a.tables), **args)
+    got = b.cache.layer(0).prefill_attention(qd, dev(b.cu), dev(b.ctx), dev(b.tables), **args,
+                                             k_new=knd, v_new=vnd)
+    torch.cuda.synchronize()
+    a.cache.check()
+    b.cache.check()
+    assert torch.equal(got, ref)
+    for which in (pagedkv.K, pagedkv.V):
+        assert np.array_equal(a.cache.read_bytes(0, which), b.cache.read_bytes(0, which))
+    a.close()
+    b.close()
+
+
+def test_fused_store_matches_oracle(gpu):
+    # the fused call against the fp64 closed form over the pool with the
+    # chunk stored by the oracle's KvPool::write restatement
+    dt, KVH, R, hd, bs = wl.F16, 4, 8, 64, 16
+    case = PCase(gpu, dt, R * KVH, KVH, hd, bs, [900, 29, 0], [256, 256, 100], seed=61)
+    T = int(case.cu[-1])
+    kn = wl.normal_storage(71, (T, KVH, hd), dt)
+    vn = wl.normal_storage(72, (T, KVH, hd), dt)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+    got = case.cache.layer(0).prefill_attention(
+        _to_dev(case.q, dt, gpu), dev(case.cu), dev(case.ctx), dev(case.tables),
+        max_q_len=256, max_context_len=int(case.ctx.max()), scale=case.scale,
+        out_dtype=torch.float32, k_new=_to_dev(kn, dt, gpu), v_new=_to_dev(vn, dt, gpu))
+    torch.cuda.synchronize()
+    case.cache.check()
+    for s in range(3):   # the oracle's write of each sequence's chunk
+        rows = slice(int(case.cu[s]), int(case.cu[s + 1]))
+        oracle.kv_write(case.kp, case.vp, bs, case.tables[s].astype(np.uint32),
+                        int(case.priors[s]), kn[rows], vn[rows])
+    _close(got.cpu().numpy(), case.reference(), "fused store vs oracle")
+    assert np.array_equal(case.cache.read_bytes(0, pagedkv.K), case.kp.view(np.uint8).reshape(-1))
+    case.close()
