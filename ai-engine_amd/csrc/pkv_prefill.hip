@@ -464,20 +464,35 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   // whether this lane's rows moved (alpha: their rescale factors).
   auto softmax = [&](STile& sacc, float (&alpha)[C::NR]) __attribute__((always_inline)) {
     bool moved = false;
+    // A row's max over the tile exceeds m + kTau iff one of its lane
+    // groups' partial maxima does (scale > 0, checked by the host, and
+    // rounding is monotone), so the cross-lane reduction runs only when some
+    // row of the wave can move -- after the first tiles, rarely.
+    float lmax[C::NR];
+    bool over = false;
 #pragma unroll
     for (int rn = 0; rn < C::NR; ++rn) {
-      float tmax = -INFINITY;
+      lmax[rn] = -INFINITY;
 #pragma unroll
       for (int km = 0; km < C::NKM; ++km)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sacc[km][rn][j]);
-      tmax = row_group_max(tmax) * a.scale_log2;  // scale > 0 (checked by the host)
+        for (int j = 0; j < 4; ++j) lmax[rn] = fmaxf(lmax[rn], sacc[km][rn][j]);
+      over |= lmax[rn] * a.scale_log2 > m[rn] + kTau;
       alpha[rn] = 1.0f;
-      if (tmax > m[rn] + kTau) {  // always in tile 0: m starts at -inf, key 0 is visible
-        alpha[rn] = fast_exp2(m[rn] - tmax);
-        m[rn] = tmax;
-        moved = true;
+    }
+    if (__builtin_amdgcn_ballot_w64(over)) {  // wave-uniform
+#pragma unroll
+      for (int rn = 0; rn < C::NR; ++rn) {
+        const float tmax = row_group_max(lmax[rn]) * a.scale_log2;
+        if (tmax > m[rn] + kTau) {  // always in tile 0: m starts at -inf, key 0 is visible
+          alpha[rn] = fast_exp2(m[rn] - tmax);
+          m[rn] = tmax;
+          moved = true;
+        }
       }
+    }
+#pragma unroll
+    for (int rn = 0; rn < C::NR; ++rn) {
       const float nm = -m[rn];
       float ssum = 0.0f;
 #pragma unroll

@@ -55,6 +55,25 @@ def timed_passes(fn, args):
     return (time.time() - t0) / n, n, res
 
 
+def timed_steps(step, n, stream):
+    """Times n calls of step(i) on `stream` with a HIP event at every step
+    boundary: returns (mean ms per step, {median, p10, p90} of the steps)."""
+    import numpy as np
+    import torch
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    marks[0].record(stream)
+    for i in range(n):
+        step(i)
+        marks[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([marks[i].elapsed_time(marks[i + 1]) for i in range(n)])
+    dist = {"median": round(float(np.median(per)), 4),
+            "p10": round(float(np.percentile(per, 10)), 4),
+            "p90": round(float(np.percentile(per, 90)), 4)}
+    return marks[0].elapsed_time(marks[n]) / n, dist
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,15 +241,7 @@ def main() -> int:
             print(json.dumps({"error": "graph replay differs from eager launches"}))
             return 1
 
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / args.steps
+    ms_step, step_dist = timed_steps(step, args.steps, stream)
 
     # Dominant-kernel duration: the library records HIP events on the launch
     # stream right before and after each call's main decode kernel (not the
@@ -274,6 +285,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "step_ms": step_dist,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -765,17 +777,13 @@ def mix(args, dev) -> int:
     # split prefill would share: overlap only when the prefill does not split
     overlap_ok = cache.prefill_workspace_bytes(NP, H, C, max_p) == 0
 
+    dists = {}
+
     def time_steps(fn):
         for _ in range(args.warmup):
             fn()
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        for _ in range(args.steps):
-            fn()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1) / args.steps
+        ms, dists[fn] = timed_steps(lambda i: fn(), args.steps, stream)
+        return ms
 
     def capture(fn):
         # the library calls take the stream pointer `sp`: point it at the
@@ -794,6 +802,7 @@ def mix(args, dev) -> int:
         return gr
 
     ms_serial = time_steps(step_serial)   # eager, one stream
+    step_fn = step_serial
     ms_graph_serial = None
     schedule = "eager launches, one stream"
     ms_step = ms_serial
@@ -816,7 +825,8 @@ def mix(args, dev) -> int:
             return 1
         del ref_p, ref_d
         ms_graph_serial = time_steps(g_serial.replay)
-        ms_step = time_steps(g_step.replay)
+        step_fn = g_step.replay
+        ms_step = time_steps(step_fn)
         schedule = ("HIP graph; per layer the decode on a second stream, forked and joined "
                     "around the prefill" if overlap_ok else "HIP graph, one stream")
     cache.check()
@@ -897,8 +907,8 @@ def mix(args, dev) -> int:
     res = {
         "metric": "continuous-batching mix tokens/s (chunked prefill + decode), TinyLlama-1.1B shape, 1 GPU",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "step_ms": dists[step_fn],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) K/V/Q, random block tables)",
         "config": {"workload": "cfg2: 22 layers, 32q/4kv heads, hd 64, bs 16, f16 KV; 8 chunked "
                                "prefills of 256 over prior U[0,1024] + 56 decodes, ctx U[256,2048]"
