@@ -397,7 +397,8 @@ __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long 
 // the thread holding the n-th match.
 template <bool FILTER, int DT, bool VEC>
 __device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
-                        unsigned long long n) {
+                        unsigned long long n, int lo = 0, int hi = -1) {
+  if (hi < 0) hi = rw.V;  // the walk covers [lo, hi); lo is a multiple of 8
   constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
   constexpr int kTE = 64 / E;               // elements per thread per step
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -405,10 +406,10 @@ __device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
   if (tid == 0) sm.found = rw.V - 1;
   __syncthreads();
   unsigned long long base = 0;
-  for (int c = 0; c < rw.V; c += kST * kTE) {
+  for (int c = lo; c < hi; c += kST * kTE) {
     const int i0 = c + tid * kTE;
     float xs[kTE];
-    if (VEC && i0 + kTE <= rw.V) {
+    if (VEC && i0 + kTE <= hi) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const u32x4 w = ld16(rw.x + (size_t)i0 * E + 16 * q);
@@ -424,7 +425,7 @@ __device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < kTE; ++e) xs[e] = i0 + e < rw.V ? logit<DT>(rw.x, i0 + e) : NAN;
+      for (int e = 0; e < kTE; ++e) xs[e] = i0 + e < hi ? logit<DT>(rw.x, i0 + e) : NAN;
     }
     uint32_t mask = 0u;
 #pragma unroll
@@ -617,15 +618,18 @@ struct SplitWs {  // per row
   unsigned long long h3[kB2];
   unsigned int cnt3[kB2];
   int min3[kB2];
+  unsigned int cntc[kMaxG][kB2];  // third digit: tokens per bucket in each chunk
 };
 
 // Workgroup blockIdx.x's chunk of a row: multiples of 8 elements (whole
 // 16-byte vectors for every dtype), the last one ending at V.
-__device__ __forceinline__ void split_chunk(int V, int& lo, int& hi) {
-  const int G = (int)gridDim.x;
+__device__ __forceinline__ void chunk_of(int V, int g, int G, int& lo, int& hi) {
   const int ce = (((V + G - 1) / G) + 7) / 8 * 8;
-  lo = min(V, (int)blockIdx.x * ce);
+  lo = min(V, g * ce);
   hi = min(V, lo + ce);
+}
+__device__ __forceinline__ void split_chunk(int V, int& lo, int& hi) {
+  chunk_of(V, (int)blockIdx.x, (int)gridDim.x, lo, hi);
 }
 
 template <int DT, bool VEC>
@@ -744,6 +748,8 @@ __global__ void __launch_bounds__(kST) split_digit_kernel(SampleArgs a, SplitWs*
   digit_pass<false>(sm, rw, lo, hi, prefix, LAST ? 0xfffffc00u : 0xfff00000u, LAST ? 0 : 10,
                     LAST);
   SplitWs& w = ws[row];
+  if (LAST)  // every bucket, zeros included: no clearing needed
+    for (int b = tid; b < kB2; b += kST) w.cntc[blockIdx.x][b] = sm.cnt[b];
   for (int b = tid; b < kB2; b += kST) {
     if (!sm.h[b]) continue;
     atomicAdd(LAST ? &w.h3[b] : &w.h2[b], sm.h[b]);
@@ -795,8 +801,34 @@ __global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs
   s.minidx = sm.minidx[b];
   __syncthreads();
   const unsigned long long n = ties_needed(s);
-  const int tok = n == 1ull ? (s.minidx == INT_MAX ? V - 1 : s.minidx)
-                            : nth_tied<true>(sm, rw, s.key, n);
+  int tok;
+  if (n == 1ull) {
+    tok = s.minidx == INT_MAX ? V - 1 : s.minidx;
+  } else {
+    // The chunks' counts of the selected key, in index order, locate the
+    // chunk holding the n-th tied token; only that chunk is walked.
+    if (tid < kWave) {
+      const unsigned long long c = tid < G ? (unsigned long long)w.cntc[tid][b] : 0ull;
+      unsigned long long incl = c;
+      for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned long long o = shfl_up_u64(incl, d);
+        if (tid >= d) incl += o;
+      }
+      const unsigned long long hit = __ballot(incl >= n);
+      if (tid == 0 && !hit) sm.red_i[0] = -1;  // counts inconsistent: walk the row
+      if (hit && tid == __ffsll((long long)hit) - 1) {
+        sm.red_i[0] = tid;
+        sm.red_u[0] = n - (incl - c);
+      }
+    }
+    __syncthreads();
+    const int gs = sm.red_i[0];
+    const unsigned long long nn = gs < 0 ? n : sm.red_u[0];
+    __syncthreads();  // nth_tied reuses sm.red_i
+    int lo = 0, hi = V;
+    if (gs >= 0) chunk_of(V, gs, G, lo, hi);
+    tok = nth_tied<true>(sm, rw, s.key, nn, lo, hi);
+  }
   if (tid == 0) a.tokens[row] = tok;
 }
 
