@@ -619,6 +619,8 @@ struct SplitWs {  // per row
   unsigned int cnt3[kB2];
   int min3[kB2];
   unsigned int cntc[kMaxG][kB2];  // third digit: tokens per bucket in each chunk
+  uint32_t pre1, pre2;            // first one / two digits of the selected key
+  unsigned long long rem1, rem2;  // what remains to select inside them
 };
 
 // Workgroup blockIdx.x's chunk of a row: multiples of 8 elements (whole
@@ -736,13 +738,35 @@ __global__ void __launch_bounds__(kST) split_digit_kernel(SampleArgs a, SplitWs*
   __shared__ SampleSmem sm;
   const int row = blockIdx.y, tid = threadIdx.x;
   const SplitLoad l = split_load(ws[row], gridDim.x, LAST ? 2 : 1);
+  const uint32_t pre1 = LAST ? ws[row].pre1 : 0u;  // issued with the histogram loads
+  const unsigned long long rem1 = LAST ? ws[row].rem1 : 0ull;
   const float T = a.temps ? a.temps[row] : 0.0f;
   if (T == 0.0f || a.vocab <= 1) return;
   const char* x = a.logits + (long long)row * a.stride_bytes;
   Row<DT, VEC> rw{x, a.vocab, T, ymax_of(block_max(sm, l.pmax), T), false, 0u, a.vocab};
   uint32_t prefix;
   unsigned long long rem;
-  split_prefix(sm, l, a.r, LAST ? 2 : 1, prefix, rem);
+  if constexpr (LAST) {
+    // the first digit was selected by the second digit pass (workgroup 0
+    // stored it): only the second digit's scan is left
+    sm.h[tid] = l.h2;
+    __syncthreads();
+    scan_buckets(sm, sm.h, kB2, rem1);
+    prefix = pre1 | (sm.sel_bucket << 10);
+    rem = sm.sel_rem;
+    __syncthreads();  // every thread has read sm.sel_*
+  } else {
+    split_prefix(sm, l, a.r, 1, prefix, rem);
+  }
+  if (blockIdx.x == 0 && tid == 0) {  // for the next launch
+    if (LAST) {
+      ws[row].pre2 = prefix;
+      ws[row].rem2 = rem;
+    } else {
+      ws[row].pre1 = prefix;
+      ws[row].rem1 = rem;
+    }
+  }
   int lo, hi;
   split_chunk(a.vocab, lo, hi);
   digit_pass<false>(sm, rw, lo, hi, prefix, LAST ? 0xfffffc00u : 0xfff00000u, LAST ? 0 : 10,
@@ -781,15 +805,15 @@ __global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs
     }
     return;
   }
-  const SplitLoad l = split_load(w, G, 3);
+  // The first two digits were selected by the third digit pass (the same
+  // scans in every one of its workgroups; workgroup 0 stored the result).
+  const uint32_t prefix = w.pre2;
+  const unsigned long long rem = w.rem2;
+  sm.h[tid] = w.h3[tid];
+  sm.cnt[tid] = w.cnt3[tid];
+  sm.minidx[tid] = w.min3[tid];
   const char* x = a.logits + (long long)row * a.stride_bytes;
-  Row<DT, VEC> rw{x, V, T, ymax_of(block_max(sm, l.pmax), T), false, 0u, V};
-  uint32_t prefix;
-  unsigned long long rem;
-  split_prefix(sm, l, a.r, 2, prefix, rem);
-  sm.h[tid] = l.h3;
-  sm.cnt[tid] = l.cnt3;
-  sm.minidx[tid] = l.min3;
+  Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};  // the tie walk reads no ymax
   __syncthreads();
   scan_buckets(sm, sm.h, kB2, rem);
   const uint32_t b = sm.sel_bucket;
