@@ -112,7 +112,8 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the paged-KV path has no "
-                                   "inter-GPU exchange here (see DESIGN.md, sharding); "
+                                   "inter-GPU exchange here (sequences or kv heads would "
+                                   "shard across GPUs with no exchange; not built); "
                                    "run with --gpus 1"}))
         return 2
 
