@@ -538,8 +538,8 @@ static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream)
     return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", a.n_head,
                 p->n_kv_head);
   if (!pkv::decode_supported(p, a.n_head))
-    return fail(p, PKV_ERR_UNSUPPORTED, "decode: n_head/n_kv_head = %d not in {1,2,4,8}",
-                a.n_head / p->n_kv_head);
+    return fail(p, PKV_ERR_UNSUPPORTED, "decode: head_dim %d with n_head %d / n_kv_head %d",
+                p->head_dim, a.n_head, p->n_kv_head);
   if (a.out_dtype != PKV_F32 && a.out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   if (!(a.scale == a.scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
@@ -612,7 +612,8 @@ int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype
   if (n_head <= 0 || n_head % p->n_kv_head != 0)
     return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
   if (!pkv::prefill_supported(p, n_head))
-    return fail(p, PKV_ERR_UNSUPPORTED, "prefill: shape not supported");
+    return fail(p, PKV_ERR_UNSUPPORTED, "prefill: head_dim %d with n_head %d / n_kv_head %d",
+                p->head_dim, n_head, p->n_kv_head);
   if (!(scale > 0.0f) || !std::isfinite(scale))
     return fail(p, PKV_ERR_INVALID, "prefill: scale must be positive and finite");
   if (out_dtype != PKV_F32 && out_dtype != p->dtype)

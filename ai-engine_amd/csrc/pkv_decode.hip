@@ -64,6 +64,9 @@ constexpr int kWavesPerBlock = 4;
 #define PKV_DECODE_MIN_ITEMS 2048
 #endif
 
+// R is the number of query heads a wave carries (1, 2, 4, 8 or 16): the
+// GQA ratio itself, or the next of these widths above it, the extra heads
+// being zero rows of the MFMA A operand whose results are never stored.
 template <int DT, int HD, int R>
 struct DCfg {
   static constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
@@ -75,17 +78,19 @@ struct DCfg {
   // more) and a 32-token tile otherwise.  The kernel is bound by the loads
   // in flight, so the larger tile is faster where it fits (-3 % on the
   // Llama-3-70B shape); narrower rows keep 32, where the shorter partitions
-  // of small batches would waste more of a 48-token tile.
+  // of small batches would waste more of a 48-token tile.  Sixteen heads
+  // hold four times the GQA-4 accumulators: 16-token tiles.
   static constexpr int NSTMAX =
-      (R >= 8 ? (DT == PKV_BF16 && HD == 128 ? 48 : 32) : PKV_DECODE_TILE) / 16;
+      (R >= 16 ? 16 : R >= 8 ? (DT == PKV_BF16 && HD == 128 ? 48 : 32) : PKV_DECODE_TILE) / 16;
   static constexpr int NST = NST0 < 1 ? 1 : (NST0 > NSTMAX ? NSTMAX : NST0);  // sub-tiles
   static constexpr int TILE = 16 * NST;            // tokens per tile
   static constexpr int CH = RB / 16;               // 16-byte chunks per row
   static constexpr int TPL = 64 / CH;              // tokens per V load
   static constexpr int NV = TILE / TPL;            // V loads per tile
   static constexpr int EPL = 16 / E;               // elements per chunk
-  static constexpr int RP = R <= 4 ? 4 : R;        // LDS pitch of a P row
+  static constexpr int PP = R <= 4 ? 4 : R;        // LDS pitch of a P row
   static constexpr int RG = (R + 3) / 4;           // MFMA row groups with heads
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "group width");
   static_assert(CH <= 64, "row wider than a wave of 16-byte chunks");
   static_assert(TILE % TPL == 0, "tile/V-load mismatch");
 };
@@ -117,6 +122,13 @@ struct DecodeKArgs {
   int rope_max;
   const int32_t* positions;  // null: position = context_len - 1
   int in_f32;                // q / k_new / v_new are f32 (else the pool dtype)
+  // GQA: kv head g serves query heads g * rtot .. g * rtot + rtot - 1; this
+  // launch computes heads h0 .. h0 + rq - 1 of every group (rq <= the
+  // kernel's width R; rtot > 16 takes several launches).
+  int rq;
+  int rtot;
+  int h0;
+  int store_new;  // 1: the launch stores k_new / v_new into the pool
 };
 
 // N elements of a row, from f32 or 16-bit storage, as floats.
@@ -313,8 +325,10 @@ template <int DT, int HD, int R, bool ROPE>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
   using C = DCfg<DT, HD, R>;
-  __shared__ float p_lds_all[kWavesPerBlock][C::TILE * C::RP];
+  __shared__ float p_lds_all[kWavesPerBlock][C::TILE * C::PP];
   __shared__ int ctx_lds[kCtxCache];
+  // The new token's K and V rows as stored (fused append), per wave.
+  __shared__ __attribute__((aligned(16))) char new_lds_all[kWavesPerBlock][2 * C::RB];
 
   // The wave index is uniform within a wave; readfirstlane tells the
   // compiler so, which keeps every per-wave quantity in SGPRs.
@@ -327,7 +341,8 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   __syncthreads();
   const CtxLens cl{a.context_lens, ctx_lds, ncache};
 
-  const int H = a.kvh * R;
+  const int H = a.kvh * a.rtot;
+  const int rq = a.rq;  // query heads of this launch per group (<= R)
   const int BS = 1 << a.bs_log2;
   const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
   const int g = (int)(item % a.kvh);
@@ -350,8 +365,9 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       for (int e = 0; e < C::EPL; ++e) z[e] = 0.0f;
 #pragma unroll
       for (int h = 0; h < R; ++h)
-        store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
-                          a.out_f32, DT, z);
+        if (h < rq)
+          store_out<C::EPL>(a.out, ((size_t)b * H + g * a.rtot + a.h0 + h) * HD + c * C::EPL,
+                            a.out_f32, DT, z);
     }
     return;
   }
@@ -383,7 +399,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       rpos = 0;
     }
     const size_t irb = a.in_f32 ? (size_t)HD * 4 : (size_t)C::RB;
-    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * irb;
+    const char* qrow = a.q + ((size_t)b * H + g * a.rtot + a.h0 + (col < rq ? col : 0)) * irb;
     const float* cr = a.rope_cos + (size_t)rpos * (HD / 2);
     const float* sr = a.rope_sin + (size_t)rpos * (HD / 2);
 #pragma unroll
@@ -395,14 +411,14 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       load_elems<PKV_F32, C::EPL>(reinterpret_cast<const char*>(cr), e0, true, cs);
       load_elems<PKV_F32, C::EPL>(reinterpret_cast<const char*>(sr), e0, true, sn);
       rope_rotate<C::EPL>(x1, x2, cs, sn);
-      qf[f] = col < R ? pack16<DT, C::EPL>(x1) : u32x4{0, 0, 0, 0};
-      qf[f + C::NF / 2] = col < R ? pack16<DT, C::EPL>(x2) : u32x4{0, 0, 0, 0};
+      qf[f] = col < rq ? pack16<DT, C::EPL>(x1) : u32x4{0, 0, 0, 0};
+      qf[f + C::NF / 2] = col < rq ? pack16<DT, C::EPL>(x2) : u32x4{0, 0, 0, 0};
     }
   } else {
-    const char* qrow = a.q + ((size_t)b * H + g * R + (col < R ? col : 0)) * C::RB;
+    const char* qrow = a.q + ((size_t)b * H + g * a.rtot + a.h0 + (col < rq ? col : 0)) * C::RB;
 #pragma unroll
     for (int f = 0; f < C::NF; ++f)
-      qf[f] = col < R ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
+      qf[f] = col < rq ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
   }
   if (lane < nblk && (tbl < 0 || tbl >= a.num_blocks)) {
     atomicOr(a.err, PKV_EBIT_BLOCK);
@@ -412,12 +428,18 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const size_t head_off = (size_t)g * C::RB;
   const size_t slot_stride = (size_t)a.kvh * C::RB;
 
-  // Fused append: store the new token's row (write before attend).
-  if (new_pos >= 0 && p == n_parts - 1) {
-    const char* knew_row = a.k_new + ((size_t)b * a.kvh + g) * C::RB;
-    const char* vnew_row = a.v_new + ((size_t)b * a.kvh + g) * C::RB;
+  // Fused append: the wave of the last partition stores the new token's row
+  // (write before attend) and keeps the stored bytes in its LDS slice; its
+  // last tile takes that token's K and V from there.  The attention thus
+  // never reads back the pool bytes this launch writes, so no ordering of a
+  // store before a load of the same address is assumed, on any memory type.
+  char* new_lds = new_lds_all[wave];
+  const bool has_new = new_pos >= 0 && p == n_parts - 1;
+  if (has_new) {
     int blk = readlane_i(tbl, (new_pos >> a.bs_log2) - blk_begin);
     size_t off = ((size_t)blk * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
+    char* kst = a.k_pool + off;
+    char* vst = a.v_pool + off;
     if constexpr (ROPE) {
       // k rotated like q (same position), v converted; chunk c < CH/2 and its
       // partner c + CH/2 are rotated together by lane c.
@@ -434,21 +456,31 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
         load_elems<PKV_F32, C::EPL>(
             reinterpret_cast<const char*>(a.rope_sin + (size_t)rpos * (HD / 2)), e0, true, sn);
         rope_rotate<C::EPL>(x1, x2, cs, sn);
-        st16(a.k_pool + off + lane * 16, pack16<DT, C::EPL>(x1));
-        st16(a.k_pool + off + (lane + C::CH / 2) * 16, pack16<DT, C::EPL>(x2));
+        const u32x4 k1 = pack16<DT, C::EPL>(x1), k2 = pack16<DT, C::EPL>(x2);
+        st16(new_lds + lane * 16, k1);
+        st16(new_lds + (lane + C::CH / 2) * 16, k2);
+        if (a.store_new) {
+          st16(kst + lane * 16, k1);
+          st16(kst + (lane + C::CH / 2) * 16, k2);
+        }
       }
       if (lane < C::CH) {
         float x[C::EPL];
         load_elems<DT, C::EPL>(vrow, lane * C::EPL, a.in_f32, x);
-        st16(a.v_pool + off + lane * 16, pack16<DT, C::EPL>(x));
+        const u32x4 v1 = pack16<DT, C::EPL>(x);
+        st16(new_lds + C::RB + lane * 16, v1);
+        if (a.store_new) st16(vst + lane * 16, v1);
       }
     } else if (lane < C::CH) {
-      st16(a.k_pool + off + lane * 16, ld16(knew_row + lane * 16));
-      st16(a.v_pool + off + lane * 16, ld16(vnew_row + lane * 16));
+      const u32x4 k1 = ld16(a.k_new + ((size_t)b * a.kvh + g) * C::RB + lane * 16);
+      const u32x4 v1 = ld16(a.v_new + ((size_t)b * a.kvh + g) * C::RB + lane * 16);
+      st16(new_lds + lane * 16, k1);
+      st16(new_lds + C::RB + lane * 16, v1);
+      if (a.store_new) {
+        st16(kst + lane * 16, k1);
+        st16(vst + lane * 16, v1);
+      }
     }
-    // Release/acquire at workgroup scope: the stores are complete and
-    // visible to this wave's loads of the same rows below.
-    __threadfence_block();
   }
 
   // A row is addressed as a wave-uniform base (pool + head + physical block)
@@ -512,6 +544,21 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   auto tile_body = [&](const int tile_base, auto prefetch) {
     constexpr bool PF = decltype(prefetch)::value;
     const int next = tile_base + C::TILE;
+    if constexpr (!PF) {
+      // The last tile holds the new token (position t_end - 1, where every
+      // clamped lane points too): its K and V come from the LDS copy.
+      if (has_new) {
+#pragma unroll
+        for (int st = 0; st < C::NST; ++st)
+          if (tile_base + 16 * st + col >= new_pos) {
+#pragma unroll
+            for (int f = 0; f < C::NF; ++f) kf[st][f] = ld16(new_lds + 64 * f + 16 * G);
+          }
+#pragma unroll
+        for (int i = 0; i < C::NV; ++i)
+          if (tile_base + i * C::TPL + tg >= new_pos) vf[i] = ld16(new_lds + C::RB + 16 * c);
+      }
+    }
     f32x4 acc[C::NST];
 #pragma unroll
     for (int st = 0; st < C::NST; ++st) {
@@ -554,7 +601,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     if (G < C::RG) {
 #pragma unroll
       for (int st = 0; st < C::NST; ++st)
-        *reinterpret_cast<f32x4*>(p_lds + (16 * st + col) * C::RP + 4 * G) =
+        *reinterpret_cast<f32x4*>(p_lds + (16 * st + col) * C::PP + 4 * G) =
             f32x4{sc[st][0], sc[st][1], sc[st][2], sc[st][3]};
     }
     __builtin_amdgcn_wave_barrier();
@@ -568,7 +615,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     }
 #pragma unroll
     for (int i = 0; i < C::NV; ++i) {
-      const float* pr = p_lds + (i * C::TPL + tg) * C::RP;
+      const float* pr = p_lds + (i * C::TPL + tg) * C::PP;
       float ph[R];
       if constexpr (R >= 4) {
 #pragma unroll
@@ -619,12 +666,12 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   if (n_parts == 1) {
 #pragma unroll
     for (int h = 0; h < R; ++h) {
-      if (h % NG != tg) continue;
+      if (h % NG != tg || h >= rq) continue;
       float inv = 1.0f / lh[h];
       float x[C::EPL];
 #pragma unroll
       for (int e = 0; e < C::EPL; ++e) x[e] = o[h][e] * inv;
-      store_out<C::EPL>(a.out, ((size_t)b * H + g * R + h) * HD + c * C::EPL,
+      store_out<C::EPL>(a.out, ((size_t)b * H + g * a.rtot + a.h0 + h) * HD + c * C::EPL,
                         a.out_f32, DT, x);
     }
     return;
@@ -638,7 +685,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   float* po = a.part_o + (pair * a.max_parts + p) * R * HD;
 #pragma unroll
   for (int h = 0; h < R; ++h) {
-    if (h % NG != tg) continue;
+    if (h % NG != tg || h >= rq) continue;
 #pragma unroll
     for (int e = 0; e < C::EPL; e += 4)
       __builtin_nontemporal_store(f32x4{o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]},
@@ -678,13 +725,15 @@ __device__ __forceinline__ float wave_sum_f(float x) {
 template <int HD>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_merge_kernel(DecodeKArgs a, int R, int dt) {
+  // R: the main kernel's group width (partials hold R heads per partition);
+  // heads h < a.rq of each group are merged.
   constexpr int LPR = HD / 4;      // lanes per partial row (16 B each)
   constexpr int PPI = kWave / LPR; // partial rows per load instruction
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const long long qh = (long long)blockIdx.x * kWavesPerBlock + wave;  // (b, g, h)
-  const long long pair = qh / R;
-  const int h = (int)(qh - pair * R);
+  const long long pair = qh / a.rq;
+  const int h = (int)(qh - pair * a.rq);
   if (pair >= (long long)a.batch * a.kvh) return;
   const int b = (int)(pair / a.kvh);
   const int g = (int)(pair % a.kvh);
@@ -758,7 +807,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   if (lane >= LPR) return;
 
   const float inv = 1.0f / L;
-  const size_t eo = ((size_t)b * a.kvh * R + g * R + h) * HD + 4 * c;
+  const size_t eo = ((size_t)b * a.kvh * a.rtot + g * a.rtot + a.h0 + h) * HD + 4 * c;
   if (a.out_f32) {
     *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) =
         f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
@@ -783,6 +832,14 @@ hipError_t launch_t(const DecodeKArgs& k, long long items, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Group width of the kernel instantiated for a GQA ratio (a slice of at
+// most 16 heads of it): the ratio itself or the next of 1, 2, 4, 8, 16.
+int group_width(int r) {
+  int w = 1;
+  while (w < r && w < 16) w <<= 1;
+  return w;
+}
+
 template <int DT, int HD>
 hipError_t launch_r(int R, const DecodeKArgs& k, long long items, hipStream_t s) {
   switch (R) {
@@ -790,6 +847,7 @@ hipError_t launch_r(int R, const DecodeKArgs& k, long long items, hipStream_t s)
     case 2: return launch_t<DT, HD, 2>(k, items, s);
     case 4: return launch_t<DT, HD, 4>(k, items, s);
     case 8: return launch_t<DT, HD, 8>(k, items, s);
+    case 16: return launch_t<DT, HD, 16>(k, items, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -814,8 +872,6 @@ int ilog2i(int x) {
 
 bool decode_supported(const pkv_pool* p, int n_head) {
   if (n_head <= 0 || n_head % p->n_kv_head != 0) return false;
-  int R = n_head / p->n_kv_head;
-  if (R != 1 && R != 2 && R != 4 && R != 8) return false;
   return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
 }
 
@@ -847,7 +903,7 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
   int pt = 0, mp = 0;
   decode_plan(p, batch, n_head, max_context_len, &pt, &mp);
   size_t pairs = (size_t)batch * p->n_kv_head;
-  size_t R = (size_t)(n_head / p->n_kv_head);
+  size_t R = (size_t)group_width(n_head / p->n_kv_head);  // partial heads per partition
   size_t cb = 0;  // no counters: the merge is a separate kernel
   if (counter_bytes) *counter_bytes = cb;
   if (mp <= 1) return 256;
@@ -861,7 +917,8 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   int pt = 0, mp = 0;
   decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
   size_t pairs = (size_t)a.batch * p->n_kv_head;
-  int R = a.n_head / p->n_kv_head;
+  const int rtot = a.n_head / p->n_kv_head;
+  const int R = group_width(rtot);  // kernel width; ratios above 16 run in slices of 16
   DecodeKArgs k{};
   k.k_pool = p->layer_k(layer);
   k.v_pool = p->layer_v(layer);
@@ -886,29 +943,40 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   k.rope_max = a.rope_max;
   k.positions = a.positions;
   k.in_f32 = a.in_f32;
+  k.rtot = rtot;
   size_t cb = p->ws_counter_bytes;
   size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   k.part_ml = reinterpret_cast<float*>(p->ws + cb);
   k.part_o = reinterpret_cast<float*>(p->ws + cb + ml_bytes);
   k.err = p->err;
   long long items = (long long)pairs * mp;
-  hipError_t e;
-  if (ev_begin && (e = hipEventRecord(ev_begin, stream)) != hipSuccess) return e;
-  switch (p->dtype) {
-    case PKV_F32: e = launch_hd<PKV_F32>(p->head_dim, R, k, items, stream); break;
-    case PKV_F16: e = launch_hd<PKV_F16>(p->head_dim, R, k, items, stream); break;
-    default: e = launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream); break;
+  hipError_t e = hipSuccess;
+  // Slices of at most 16 query heads per group, each a main launch and its
+  // merge (stream-ordered, so the slices share the workspace); the first
+  // slice stores the new token, every slice attends to it.
+  for (int h0 = 0; h0 < rtot; h0 += 16) {
+    k.h0 = h0;
+    k.rq = rtot - h0 < R ? rtot - h0 : R;
+    k.store_new = h0 == 0;
+    const bool timed = h0 == 0;  // the profile events bracket the first slice
+    if (timed && ev_begin && (e = hipEventRecord(ev_begin, stream)) != hipSuccess) return e;
+    switch (p->dtype) {
+      case PKV_F32: e = launch_hd<PKV_F32>(p->head_dim, R, k, items, stream); break;
+      case PKV_F16: e = launch_hd<PKV_F16>(p->head_dim, R, k, items, stream); break;
+      default: e = launch_hd<PKV_BF16>(p->head_dim, R, k, items, stream); break;
+    }
+    if (e != hipSuccess) return e;
+    if (timed && ev_end && (e = hipEventRecord(ev_end, stream)) != hipSuccess) return e;
+    if (mp <= 1) continue;
+    unsigned grid = (unsigned)((pairs * k.rq + kWavesPerBlock - 1) / kWavesPerBlock);
+    switch (p->head_dim) {
+      case 64: decode_merge_kernel<64><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+      case 128: decode_merge_kernel<128><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+      default: decode_merge_kernel<256><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (e != hipSuccess) return e;
-  if (ev_end && (e = hipEventRecord(ev_end, stream)) != hipSuccess) return e;
-  if (mp <= 1) return e;
-  unsigned grid = (unsigned)((pairs * R + kWavesPerBlock - 1) / kWavesPerBlock);
-  switch (p->head_dim) {
-    case 64: decode_merge_kernel<64><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
-    case 128: decode_merge_kernel<128><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
-    default: decode_merge_kernel<256><<<grid, kWavesPerBlock * kWave, 0, stream>>>(k, R, p->dtype); break;
-  }
-  return hipGetLastError();
+  return e;
 }
 
 }  // namespace pkv

@@ -122,6 +122,7 @@ struct PrefillKArgs {
   int part_keys;   // keys per part: a multiple of two tiles
   int max_parts;   // parts per row block at most (1 + (max_context_len - 1) / part_keys)
   int per_xcd;     // workgroup slots per XCD (affinity mapping), 0 = plain order
+  int rq;          // GQA ratio n_head / n_kv_head (kernels built for a fixed ratio ignore it)
   float scale_log2;
   float* part_ml;  // split key ranges: (m, l) per (item, row)
   float* part_o;   //   and the unnormalised O row
@@ -171,10 +172,13 @@ __device__ __forceinline__ uint32_t cvt_pk16(float x0, float x1) {
   }
 }
 
-template <int DT, int HD, int R, bool FUSED>
+// RT: the GQA ratio the kernel is built for, or 0 for any ratio (a.rq); the
+// ratio only enters the row <-> (token, head) index arithmetic.
+template <int DT, int HD, int RT, bool FUSED>
 __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
-  using C = PCfg<DT, HD, R>;
+  using C = PCfg<DT, HD, RT>;
   __shared__ __attribute__((aligned(16))) char lds[2 * C::STAGE];
+  const int R = RT > 0 ? RT : a.rq;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -234,26 +238,28 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const int nparts = n_parts_of(prior, a.part_keys);
   if (part >= nparts) return;  // uniform over the workgroup
 
-  // Fused store of the K/V rows of the chunk's tokens at positions prior + i
-  // (row blocks partition the tokens; ROWS is a multiple of R).  The store's
-  // load round trip must not lengthen the heaviest row blocks (the last
-  // ones, which see the most keys): row block rb of the sequence's nrb
-  // stores its own tokens and those of its mirror nrb - 1 - rb when rb is
-  // the lighter of the two, nothing when it is the heavier; only the last
-  // part of a row block stores.  No workgroup of this launch reads these rows
-  // from the pool: keys >= prior come from k_new / v_new.
+  // Fused store of the K/V rows of the chunk's tokens at positions prior + i.
+  // Row blocks partition the tokens: token j belongs to the row block of its
+  // first row, j R / ROWS, so row block r owns tokens tok_lo(r) ..
+  // tok_lo(r + 1) - 1 with tok_lo(r) = ceil(r ROWS / R).  The store's load
+  // round trip must not lengthen the heaviest row blocks (the last ones,
+  // which see the most keys): row block rb of the sequence's nrb stores its
+  // own tokens and those of its mirror nrb - 1 - rb when rb is the lighter of
+  // the two, nothing when it is the heavier; only the last part of a row
+  // block stores.  No workgroup of this launch reads these rows from the
+  // pool: keys >= prior come from k_new / v_new.
   const char* kin = FUSED ? a.k_new + (size_t)g * C::RB : nullptr;
   const char* vin = FUSED ? a.v_new + (size_t)g * C::RB : nullptr;
   const int nrb = (n_rows + C::ROWS - 1) / C::ROWS;
   const int mirror = nrb - 1 - rb;
   if (FUSED && part == nparts - 1 && rb <= mirror) {
-    const int tpb = C::ROWS / R;  // tokens per row block
-    const int own = (min(row0 + C::ROWS, n_rows) - row0) / R;
-    const int mir = rb < mirror ? (min((mirror + 1) * C::ROWS, n_rows) - mirror * C::ROWS) / R : 0;
+    auto tok_lo = [&](int r) { return min((r * C::ROWS + R - 1) / R, q_len); };
+    const int own0 = tok_lo(rb), own = tok_lo(rb + 1) - own0;
+    const int mir0 = tok_lo(mirror), mir = rb < mirror ? tok_lo(mirror + 1) - mir0 : 0;
     const int nch = (own + mir) * C::CH;
     for (int idx = tid; idx < nch; idx += kPT) {
       const int j = idx / C::CH, c16 = 16 * (idx % C::CH);
-      const int tok = j < own ? rb * tpb + j : mirror * tpb + (j - own);
+      const int tok = j < own ? own0 + j : mir0 + (j - own);
       const int pos = prior + tok;
       const int blk = table[pos >> a.bs_log2];
       if ((unsigned)blk >= (unsigned)a.num_blocks) {
@@ -752,10 +758,10 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <int DT, int HD, int R>
+template <int DT, int HD, int RT>
 hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
-  using C = PCfg<DT, HD, R>;
-  k.row_blocks = (k.max_q_len * R + C::ROWS - 1) / C::ROWS;
+  using C = PCfg<DT, HD, RT>;
+  k.row_blocks = (int)(((long long)k.max_q_len * k.rq + C::ROWS - 1) / C::ROWS);
   const long long n_sg = (long long)k.n_seqs * k.kvh;
   const long long items = n_sg * k.row_blocks * k.max_parts;
   if (items <= 0) return hipSuccess;
@@ -768,9 +774,9 @@ hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
     grid = per * kXcd;
   }
   if (k.k_new)
-    prefill_kernel<DT, HD, R, true><<<(unsigned)grid, kPT, 0, s>>>(k);
+    prefill_kernel<DT, HD, RT, true><<<(unsigned)grid, kPT, 0, s>>>(k);
   else
-    prefill_kernel<DT, HD, R, false><<<(unsigned)grid, kPT, 0, s>>>(k);
+    prefill_kernel<DT, HD, RT, false><<<(unsigned)grid, kPT, 0, s>>>(k);
   return hipGetLastError();
 }
 
@@ -781,7 +787,7 @@ hipError_t plaunch_r(int R, const PrefillKArgs& k, hipStream_t s) {
     case 2: return plaunch<DT, HD, 2>(k, s);
     case 4: return plaunch<DT, HD, 4>(k, s);
     case 8: return plaunch<DT, HD, 8>(k, s);
-    default: return hipErrorInvalidValue;
+    default: return plaunch<DT, HD, 0>(k, s);  // any other ratio, at run time
   }
 }
 
@@ -790,9 +796,7 @@ hipError_t plaunch_hd(int HD, int R, const PrefillKArgs& k, hipStream_t s) {
   switch (HD) {
     case 64: return plaunch_r<DT, 64>(R, k, s);
     case 128: return plaunch_r<DT, 128>(R, k, s);
-    case 256:
-      if constexpr (DT != PKV_F32) return plaunch_r<DT, 256>(R, k, s);
-      return hipErrorInvalidValue;
+    case 256: return plaunch_r<DT, 256>(R, k, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -857,9 +861,6 @@ void prefill_plan(const pkv_pool* p, int n_seqs, int n_head, int max_q_len, int 
 
 bool prefill_supported(const pkv_pool* p, int n_head) {
   if (n_head <= 0 || n_head % p->n_kv_head != 0) return false;
-  int R = n_head / p->n_kv_head;
-  if (R != 1 && R != 2 && R != 4 && R != 8) return false;
-  if (p->dtype == PKV_F32 && p->head_dim > 128) return false;  // register budget
   return p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256;
 }
 
@@ -885,6 +886,7 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
   k.err = p->err;
   k.k_new = reinterpret_cast<const char*>(a.k_new);
   k.v_new = reinterpret_cast<const char*>(a.v_new);
+  k.rq = a.n_head / p->n_kv_head;
   size_t ws = 0;
   prefill_plan(p, a.n_seqs, a.n_head, a.max_q_len, a.max_context_len, &k.part_keys,
                &k.max_parts, &ws);

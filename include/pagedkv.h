@@ -73,8 +73,18 @@ const char* pkv_last_error(const pkv_pool* pool);
  * stands for the reference's Vec<KvPool> (engine.rs:70-72): layer l of the
  * handle is the reference's kv[l].  Block ids are shared by all layers.
  * dtype: PKV_F32 (the reference's own dtype), PKV_F16 or PKV_BF16.
- * head_dim must be 64, 128 or 256; block_size a power of two in [16, 256]
- * (the reference's default is 16, app.rs:701). */
+ * Shape limits (PKV_ERR_UNSUPPORTED otherwise), narrower than the
+ * reference's KvPool::new, which takes any sizes:
+ *  - head_dim 64, 128 or 256.  The reference reads it from GGUF
+ *    (`attention.key_length`, else embedding_length / head_count,
+ *    arch.rs:77-83); every llama / qwen2 / qwen3 model of the supported
+ *    architectures (arch.rs:27-36) has 64 or 128.
+ *  - block_size a power of two in [16, 256].  The reference takes any
+ *    usize (block_table.rs:17-30); its engine default and the block size of
+ *    its tests is 16 (app.rs:701, tests/paged_parity.rs:33).
+ * n_kv_head is any positive count; the GQA ratio n_head / n_kv_head of the
+ * attention calls is any positive integer (repeat_kv, attention.rs:113,
+ * 128-136).  The pool is plain device memory from hipMalloc. */
 int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
                     int block_size, int n_kv_head, int head_dim, int dtype,
                     int device);
@@ -165,9 +175,19 @@ int pkv_compact(pkv_pool* pool, const int32_t* src_host,
  *                stores them at token position context_lens[b]-1 of sequence
  *                b (KvPool::write at seq_lens[b], transformer.rs:276) and the
  *                attention sees them -- append and attention in one launch.
- * GQA: query head h reads kv head h / (n_head / n_kv_head) (attention.rs:128-136).
+ * GQA: query head h reads kv head h / (n_head / n_kv_head) (attention.rs:128-136),
+ * for any integer ratio; ratios above 16 run as one launch (and merge) per
+ * slice of 16 query heads, each reading the group's K/V.
  * fp32 accumulation; softmax in fp32 with an exp2 formulation.
- * context_lens[b] == 0 yields a zero output row. */
+ * context_lens[b] == 0 yields a zero output row.
+ * Mask: key k of row b is attended iff k < context_lens[b] -- the
+ * reference's build_mask(seq_lens + 1, positions, kv_len) as the decode step
+ * calls it, where positions == seq_lens (transformer.rs:289-290,
+ * engine.rs:130-133), so its second bound k <= positions[b]
+ * (attention.rs:22) coincides with the first.  A caller whose positions
+ * differ from seq_lens gets that mask by passing context_lens[b] =
+ * min(seq_lens[b] + 1, positions[b] + 1) without k_new / v_new (which are
+ * stored at context_lens[b] - 1), after storing the row with pkv_append. */
 int pkv_decode_attention(pkv_pool* pool, int layer, const void* q, void* out,
                          int out_dtype, const int32_t* block_tables,
                          int max_blocks_per_seq, const int32_t* context_lens,
@@ -196,7 +216,7 @@ int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,
  *  block_tables: [n_seqs][max_blocks_per_seq] int32.
  *  max_q_len, max_context_len: host upper bounds.  scale > 0 and finite
  *  (the reference's 1/sqrt(head_dim)); otherwise PKV_ERR_INVALID.
- *  Supported: n_head/n_kv_head in {1,2,4,8}; f32 pools up to head_dim 128. */
+ *  Any GQA ratio n_head / n_kv_head; every pool dtype and head_dim. */
 int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,
                           int out_dtype, const int32_t* cu_q_lens,
                           const int32_t* context_lens,

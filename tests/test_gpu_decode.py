@@ -131,8 +131,11 @@ def test_golden_fixtures(gpu):
 
 @pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
 @pytest.mark.parametrize("hd", [64, 128, 256])
-@pytest.mark.parametrize("R", [1, 2, 4, 8])
+@pytest.mark.parametrize("R", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_decode_matches_oracle(gpu, dt, hd, R):
+    # any GQA ratio n_head / n_kv_head (repeat_kv, attention.rs:113,128-136):
+    # ratios other than 1, 2, 4, 8, 16 run on the next wider kernel with the
+    # extra query rows zero and unstored
     KVH = 2
     ctx = [0, 1, 14, 15, 16, 63, 64, 200, 257, 700]
     c = Case(gpu, dt, R * KVH, KVH, hd, 16, ctx, seed=hd * 10 + R + dt)
@@ -143,7 +146,9 @@ def test_decode_matches_oracle(gpu, dt, hd, R):
 
 
 @pytest.mark.parametrize("dt,hd,R", [(wl.BF16, 64, 4), (wl.F16, 64, 8), (wl.BF16, 128, 4),
-                                     (wl.BF16, 128, 8), (wl.F16, 256, 2), (wl.F32, 128, 4)])
+                                     (wl.BF16, 128, 8), (wl.F16, 256, 2), (wl.F32, 128, 4),
+                                     (wl.BF16, 128, 7), (wl.F16, 64, 6), (wl.F32, 64, 5),
+                                     (wl.BF16, 128, 3), (wl.BF16, 64, 16), (wl.F32, 256, 12)])
 def test_many_partitions_merge(gpu, dt, hd, R):
     # a small batch with long contexts: 64-token partitions, up to ~150 per
     # sequence, so the merge covers several (m, l) lane groups and unrolled
@@ -251,7 +256,7 @@ def test_batched_equals_solo(gpu):
                                     torch.from_numpy(c.context_lens[b:b + 1]).to(gpu),
                                     max_context_len=int(c.context_lens.max()), scale=c.scale,
                                     out_dtype=torch.float32)
-        np.testing.assert_allclose(out.cpu().numpy()[0], full[b], rtol=1e-5, atol=1e-6)
+        assert np.array_equal(out.cpu().numpy()[0], full[b])  # identical, as the reference demands
     c.close()
 
 
@@ -265,4 +270,70 @@ def test_profile_hook_times_main_kernel(gpu):
     c.cache.profile(False)
     c.run()
     assert c.cache.profile_read() == (0.0, 0)
+    c.close()
+
+
+@pytest.mark.parametrize("dt,hd,R", [(wl.BF16, 128, 20), (wl.F32, 64, 33), (wl.F16, 64, 17),
+                                     (wl.BF16, 256, 32)])
+def test_ratio_above_sixteen_in_head_slices(gpu, dt, hd, R):
+    # ratios above 16 run as launches over slices of at most 16 query heads of
+    # every group (each reads the group's K/V); the first slice stores the new
+    # token and every slice attends to it
+    KVH = 2
+    c = Case(gpu, dt, R * KVH, KVH, hd, 16, [0, 3, 700, 2100, 64], seed=hd + R, fused=True)
+    got = c.run()
+    ref, kp, vp = c.reference()
+    _close(got, ref, f"R={R} dt={dt} hd={hd}")
+    k1, v1 = _host_pool(c.cache, 0)
+    assert np.array_equal(k1.view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(v1.view(np.uint8), vp.view(np.uint8))
+    c.close()
+
+
+@pytest.mark.parametrize("R", [3, 6, 7, 12])
+def test_fused_equals_separate_append_any_ratio(gpu, R):
+    # the fused new token (taken from the launch's own copy of the stored
+    # row) gives the same bits as KvPool::write followed by attention
+    dt, KVH, hd = wl.BF16, 2, 128
+    ctx = list(wl.randint(50 + R, 9, 0, 2500))
+    c = Case(gpu, dt, R * KVH, KVH, hd, 16, ctx, seed=50 + R, fused=True)
+    fused = c.run()
+    d = Case(gpu, dt, R * KVH, KVH, hd, 16, ctx, seed=50 + R, fused=False)
+    slots = d.tables[np.arange(len(ctx)), d.ctx // 16].astype(np.int64) * 16 + d.ctx % 16
+    d.cache.layer(0).append(_to_dev(d.kn, dt, gpu), _to_dev(d.vn, dt, gpu), slots.astype(np.int32))
+    assert np.array_equal(fused, d.run())
+    k1, _ = _host_pool(c.cache, 0)
+    k2, _ = _host_pool(d.cache, 0)
+    assert np.array_equal(k1, k2)
+    c.close()
+    d.close()
+
+
+def test_positions_bound_of_build_mask(gpu):
+    # build_mask's second bound k <= positions[b] (attention.rs:22) with
+    # positions different from seq_lens: the reference's decode-step order
+    # (write at seq_lens, gather seq_lens + 1, mask with both bounds, sdpa)
+    # equals pkv_append at seq_lens plus attention over
+    # min(seq_lens + 1, positions + 1) keys
+    B, H, KVH, hd, bs = 5, 14, 2, 64, 16
+    ctx = [3, 40, 17, 100, 64]
+    pos = [1, 40, 5, 99, 0]   # <= seq_lens
+    c = Case(gpu, wl.F32, H, KVH, hd, bs, ctx, seed=19)
+    kp, vp = c.kp.copy(), c.vp.copy()
+    ref = oracle.decode_step_f32(kp, vp, bs, c.tables.astype(np.uint32), c.ctx, pos, c.q, c.kn,
+                                 c.vn, c.scale)
+    slots = c.tables[np.arange(B), c.ctx // bs].astype(np.int64) * bs + c.ctx % bs
+    pool = c.cache.layer(0)
+    pool.append(_to_dev(c.kn, wl.F32, gpu), _to_dev(c.vn, wl.F32, gpu), slots.astype(np.int32))
+    cl = np.minimum(c.ctx + 1, np.asarray(pos) + 1).astype(np.int32)
+    got = pool.decode_attention(_to_dev(c.q, wl.F32, gpu), torch.from_numpy(c.tables).to(gpu),
+                                torch.from_numpy(cl).to(gpu), max_context_len=int(c.ctx.max()) + 1,
+                                scale=c.scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    c.cache.check()
+    _close(got.cpu().numpy(), ref.astype(np.float64), "positions bound")
+    # and the bound matters: attention over seq_lens + 1 keys differs
+    full = oracle.paged_attention_f64(kp, vp, wl.F32, bs, c.tables.astype(np.uint32),
+                                      (c.ctx + 1).astype(np.int32), c.q, c.scale)
+    assert np.abs(full - ref).max() > 1e-2
     c.close()

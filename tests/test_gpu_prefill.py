@@ -85,10 +85,10 @@ class PCase:
 
 @pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
 @pytest.mark.parametrize("hd", [64, 128, 256])
-@pytest.mark.parametrize("R", [1, 2, 4, 8])
+@pytest.mark.parametrize("R", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_prefill_matches_oracle(gpu, dt, hd, R):
-    if dt == wl.F32 and hd == 256:
-        pytest.skip("f32 prefill supports head_dim <= 128 (documented)")
+    # any GQA ratio: rows are (token, head) pairs, so with R not dividing a
+    # row block's 128 (64) rows a token's heads straddle two row blocks
     KVH = 2
     priors = [0, 0, 37, 300, 5]
     chunks = [1, 45, 16, 70, 33]
@@ -182,7 +182,8 @@ def test_tinyllama_chunked_prefill_shape(gpu):
 
 
 @pytest.mark.parametrize("dt,hd,R", [(wl.F16, 64, 8), (wl.BF16, 128, 4), (wl.BF16, 256, 2),
-                                     (wl.F32, 64, 4), (wl.F32, 128, 1), (wl.BF16, 64, 2)])
+                                     (wl.F32, 64, 4), (wl.F32, 128, 1), (wl.BF16, 64, 2),
+                                     (wl.BF16, 128, 7), (wl.F32, 256, 3), (wl.F16, 64, 12)])
 def test_long_prior_split_into_parts(gpu, dt, hd, R):
     # Priors beyond the part length split a row block's keys into parts run
     # by separate workgroups and merged afterwards (launches with few row
@@ -226,7 +227,9 @@ def _slots(case):
 
 @pytest.mark.parametrize("dt,hd,R,bs", [(wl.F16, 64, 8, 16), (wl.BF16, 128, 4, 16),
                                         (wl.BF16, 64, 1, 32), (wl.F32, 128, 2, 16),
-                                        (wl.BF16, 256, 2, 64), (wl.F16, 128, 8, 128)])
+                                        (wl.BF16, 256, 2, 64), (wl.F16, 128, 8, 128),
+                                        (wl.BF16, 64, 7, 16), (wl.F16, 128, 3, 32),
+                                        (wl.F32, 256, 6, 16), (wl.BF16, 128, 20, 16)])
 def test_fused_store_equals_append_then_prefill(gpu, dt, hd, R, bs):
     # same attention output and same pool bytes, bit for bit, as pkv_append
     # followed by pkv_prefill_attention; chunks that start and end mid-block,

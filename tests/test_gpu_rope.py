@@ -122,7 +122,9 @@ class RopeCase:
 
 @pytest.mark.parametrize("dt,in_dt,hd,R", [(wl.BF16, wl.F32, 128, 4), (wl.BF16, wl.BF16, 128, 4),
                                            (wl.F16, wl.F32, 64, 8), (wl.F32, wl.F32, 128, 2),
-                                           (wl.BF16, wl.F32, 256, 2), (wl.F16, wl.F16, 64, 4)])
+                                           (wl.BF16, wl.F32, 256, 2), (wl.F16, wl.F16, 64, 4),
+                                           (wl.BF16, wl.F32, 128, 7), (wl.F32, wl.F32, 64, 7),
+                                           (wl.BF16, wl.F32, 128, 5), (wl.BF16, wl.F32, 64, 20)])
 def test_decode_attention_rope_matches_oracle(gpu, dt, in_dt, hd, R):
     KVH = 2
     ctx = [0, 1, 15, 16, 300, 1100, 2500]
@@ -211,7 +213,9 @@ def _slot_case(seed, n, nb, bs):
                                                (wl.F16, wl.F32, 64, 4, 8),
                                                (wl.F16, wl.F16, 64, 2, 1),
                                                (wl.F32, wl.F32, 256, 2, 2),
-                                               (wl.BF16, wl.F32, 256, 1, 8)])
+                                               (wl.BF16, wl.F32, 256, 1, 8),
+                                               (wl.F32, wl.F32, 64, 2, 7),
+                                               (wl.BF16, wl.F32, 64, 2, 7)])
 def test_append_rope_bit_exact(gpu, dt, in_dt, hd, KVH, R):
     n, nb, bs, H, max_seq = 203, 40, 16, KVH * R, 3000
     seed = hd + KVH + R + 3 * dt + in_dt

@@ -155,7 +155,9 @@ def _torch_sdpa64(q, k, v, mask, n_head, n_kv, scale, gqa="consecutive"):
 
 
 @pytest.mark.parametrize("B,H,KVH,Lq,kv,hd", [(2, 4, 2, 1, 37, 16), (1, 8, 1, 3, 20, 8),
-                                                (3, 4, 4, 1, 5, 32), (2, 8, 2, 2, 64, 64)])
+                                                (3, 4, 4, 1, 5, 32), (2, 8, 2, 2, 64, 64),
+                                                (2, 14, 2, 1, 40, 16), (1, 9, 3, 2, 21, 8),
+                                                (2, 12, 2, 1, 33, 16), (1, 20, 1, 1, 17, 8)])
 def test_sdpa_f32_matches_torch_float64(B, H, KVH, Lq, kv, hd):
     rng = np.random.default_rng(B * 100 + kv)
     q = rng.standard_normal((B, H, Lq, hd)).astype(np.float32)
@@ -223,7 +225,8 @@ def _random_paged(seed, B, KVH, hd, bs, ctx_hi, dtype=wl.F32):
     return ctx, tables, kp, vp
 
 
-@pytest.mark.parametrize("B,H,KVH,hd,bs", [(3, 8, 2, 16, 16), (4, 4, 4, 8, 16), (2, 8, 1, 32, 32)])
+@pytest.mark.parametrize("B,H,KVH,hd,bs", [(3, 8, 2, 16, 16), (4, 4, 4, 8, 16), (2, 8, 1, 32, 32),
+                                           (3, 14, 2, 16, 16), (2, 15, 5, 8, 16)])
 def test_decode_step_f32_matches_closed_form(B, H, KVH, hd, bs):
     ctx, tables, kp, vp = _random_paged(11 + B, B, KVH, hd, bs, 70)
     rng = np.random.default_rng(3)
@@ -258,8 +261,9 @@ def test_decode_step_faithful_equals_in_place():
     assert np.array_equal(kp, k2) and np.array_equal(vp, v2)
 
 
-def test_paged_attention_f64_matches_torch_on_gathered():
-    B, H, KVH, hd, bs = 3, 8, 2, 16, 16
+@pytest.mark.parametrize("H,KVH", [(8, 2), (14, 2), (6, 2), (21, 3)])
+def test_paged_attention_f64_matches_torch_on_gathered(H, KVH):
+    B, hd, bs = 3, 16, 16
     ctx, tables, kp, vp = _random_paged(5, B, KVH, hd, bs, 50, wl.BF16)
     q = wl.widen(wl.normal_storage(9, (B, H, hd), wl.BF16), wl.BF16)
     got = oracle.paged_attention_f64(kp, vp, wl.BF16, bs, tables, ctx + 1, q, 0.25)
@@ -300,9 +304,10 @@ def _prefill_setup(seed, P, C, H, KVH, hd, bs):
     return tb, kp, vp, q
 
 
-def test_prefill_reduces_to_reference_prefill_seq():
+@pytest.mark.parametrize("H,KVH", [(4, 2), (14, 2), (9, 3)])
+def test_prefill_reduces_to_reference_prefill_seq(H, KVH):
     # prior context 0: the reference's one-shot causal prefill attention
-    H, KVH, hd, bs, N = 4, 2, 16, 16, 37
+    hd, bs, N = 16, 16, 37
     tb, kp, vp, q = _prefill_setup(31, 0, N, H, KVH, hd, bs)
     got = oracle.prefill_attention_f64(kp, vp, wl.F32, bs, tb[None], [0, N], [N], q,
                                        1 / math.sqrt(hd))
@@ -329,18 +334,20 @@ def test_prefill_chunking_invariance_and_decode_reduction():
     np.testing.assert_allclose(dec, full[n - 1:n], rtol=1e-12, atol=1e-14)
 
 
-def test_prefill_brute_force_tiny():
-    H, KVH, hd, bs = 2, 1, 4, 16
+@pytest.mark.parametrize("H,KVH", [(2, 1), (6, 2), (7, 1)])
+def test_prefill_brute_force_tiny(H, KVH):
+    hd, bs = 4, 16
     P, C = 3, 2
     tb, kp, vp, q = _prefill_setup(51, P, C, H, KVH, hd, bs)
     got = oracle.prefill_attention_f64(kp, vp, wl.F32, bs, tb[None], [0, C], [P + C], q[P:], 0.5)
     kf, vf = oracle.gather_seq(kp, vp, bs, tb, P + C)
     for i in range(C):
         for h in range(H):
-            s = [0.5 * float(np.dot(q[P + i, h].astype(np.float64), kf[j, 0])) for j in range(P + i + 1)]
+            g = h // (H // KVH)   # query head h reads kv head h / (H / KVH)
+            s = [0.5 * float(np.dot(q[P + i, h].astype(np.float64), kf[j, g])) for j in range(P + i + 1)]
             w = np.exp(np.array(s) - max(s))
             w /= w.sum()
-            o = (w[:, None] * vf[: P + i + 1, 0].astype(np.float64)).sum(0)
+            o = (w[:, None] * vf[: P + i + 1, g].astype(np.float64)).sum(0)
             np.testing.assert_allclose(got[i, h * hd:(h + 1) * hd], o, rtol=1e-12, atol=1e-14)
 
 
