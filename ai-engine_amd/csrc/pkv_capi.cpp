@@ -268,6 +268,17 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   }
   p->plan = static_cast<char*>(dplan);
   p->plan_host = static_cast<char*>(hplan);
+  // This device's copy of the static scratch of pkv_decode_attention_noalloc
+  // (looked up once per device, with the device current).
+  e = pkv::noalloc_scratch(device, &p->scratch);
+  if (e != hipSuccess) {
+    (void)hipFree(dplan);
+    (void)hipHostFree(hplan);
+    (void)hipFree(base);
+    (void)hipFree(err);
+    delete p;
+    return fail(nullptr, PKV_ERR_HIP, "scratch symbol lookup: %s", hipGetErrorString(e));
+  }
   *out = p;
   return PKV_OK;
 }
@@ -519,8 +530,11 @@ static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
   return PKV_OK;
 }
 
-// Shared validation and launch of pkv_decode_attention(_rope).
-static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream) {
+// Shared validation and launch of pkv_decode_attention(_rope, _noalloc).
+// noalloc: the partials go to the static scratch array, and nothing is
+// allocated (no workspace growth, no profile events).
+static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
+                       bool noalloc = false) {
   if (int rc = check_layer(p, layer)) return rc;
   if (a.batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", a.batch);
   if (a.batch == 0) return PKV_OK;
@@ -546,10 +560,22 @@ static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream)
   DeviceGuard dg(p->device);
   size_t cb = 0;
   size_t need = pkv::decode_workspace_bytes(p, a.batch, a.n_head, a.max_context_len, &cb);
+  if (noalloc) {
+    if (need > pkv::noalloc_scratch_bytes())
+      return fail(p, PKV_ERR_UNSUPPORTED,
+                  "decode_noalloc: the partials need %zu bytes, the static scratch holds %zu "
+                  "(batch %d, n_head %d, max_context_len %d)",
+                  need, pkv::noalloc_scratch_bytes(), a.batch, a.n_head, a.max_context_len);
+    if (!p->scratch) return fail(p, PKV_ERR_HIP, "decode_noalloc: no scratch address");
+    hipError_t e = pkv::launch_decode(p, layer, a, p->scratch, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(p, e, "decode_noalloc launch");
+    return PKV_OK;
+  }
   if (int rc = ensure_workspace(p, need, cb)) return rc;
   hipEvent_t eb = nullptr, ee = nullptr;
   if (int rc = profile_slot(p, &eb, &ee)) return rc;
-  hipError_t e = pkv::launch_decode(p, layer, a, static_cast<hipStream_t>(stream), eb, ee);
+  hipError_t e = pkv::launch_decode(p, layer, a, p->ws + p->ws_counter_bytes,
+                                    static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "decode launch");
   return PKV_OK;
 }
@@ -563,6 +589,17 @@ int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int o
   pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
                     max_context_len, batch, n_head, scale, k_new, v_new};
   return decode_call(p, layer, a, stream);
+}
+
+int pkv_decode_attention_noalloc(pkv_pool* p, int layer, const void* q, void* out,
+                                 int out_dtype, const int32_t* block_tables,
+                                 int max_blocks_per_seq, const int32_t* context_lens,
+                                 int max_context_len, int batch, int n_head, float scale,
+                                 const void* k_new, const void* v_new, void* stream) {
+  CHECK_POOL(p);
+  pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
+                    max_context_len, batch, n_head, scale, k_new, v_new};
+  return decode_call(p, layer, a, stream, true);
 }
 
 int pkv_decode_attention_rope(pkv_pool* p, int layer, const pkv_rope* rope,

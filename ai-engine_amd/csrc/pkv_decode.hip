@@ -38,6 +38,7 @@
 // visible to itself with a workgroup-scope fence, and then reads it back
 // like every other row -- write-then-attend exactly as transformer.rs:276-277,
 // with no data-dependent loads in the main loop.
+#include <mutex>
 #include <type_traits>
 
 #include "pkv_device.h"
@@ -912,7 +913,7 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
   return cb + ml + po;
 }
 
-hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
+hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a, char* partials,
                          hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   int pt = 0, mp = 0;
   decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
@@ -944,10 +945,9 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
   k.positions = a.positions;
   k.in_f32 = a.in_f32;
   k.rtot = rtot;
-  size_t cb = p->ws_counter_bytes;
   size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
-  k.part_ml = reinterpret_cast<float*>(p->ws + cb);
-  k.part_o = reinterpret_cast<float*>(p->ws + cb + ml_bytes);
+  k.part_ml = reinterpret_cast<float*>(partials);
+  k.part_o = reinterpret_cast<float*>(partials + ml_bytes);
   k.err = p->err;
   long long items = (long long)pairs * mp;
   hipError_t e = hipSuccess;
@@ -977,6 +977,37 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return e;
+}
+
+// ---- scratch of the allocation-free entry point -------------------------
+// The split-context partials of pkv_decode_attention_noalloc live in this
+// file-scope device array: every GPU the library runs on holds its own copy
+// for the life of the process.  Host code never uses the array's name as an
+// address (on the host it is only a stand-in for the symbol): the address of
+// each device's copy comes from hipGetSymbolAddress, looked up once per
+// device with that device current, and is what the kernels receive.
+// Nothing in it needs clearing between calls: every partial a merge reads
+// was written by the same call's main kernel.
+constexpr size_t kNoallocScratch = PKV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kNoallocScratch];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static char* g_scratch_ptr[kMaxDevices] = {};
+
+size_t noalloc_scratch_bytes() { return kNoallocScratch; }
+
+hipError_t noalloc_scratch(int device, char** ptr) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = static_cast<char*>(addr);
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
 }
 
 }  // namespace pkv

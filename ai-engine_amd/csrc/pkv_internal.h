@@ -33,6 +33,9 @@ struct pkv_pool {
   char* ws = nullptr;
   size_t ws_bytes = 0;
   size_t ws_counter_bytes = 0;
+  // this device's copy of the static scratch array of
+  // pkv_decode_attention_noalloc (looked up at pool creation)
+  char* scratch = nullptr;
   // compaction plan (chains of block moves), kept between calls: device
   // buffer and its pinned host staging copy
   char* plan = nullptr;
@@ -140,11 +143,16 @@ void decode_plan(const pkv_pool* p, int batch, int n_head,
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
                               int max_context_len, size_t* counter_bytes);
 bool decode_supported(const pkv_pool* p, int n_head);
-// ev_begin / ev_end (may be null) are recorded on `stream` right before and
-// right after the main partition kernel.
+// The split-context partials go to `partials` (decode_workspace_bytes of the
+// launch).  ev_begin / ev_end (may be null) are recorded on `stream` right
+// before and right after the main partition kernel.
 hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a,
-                         hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                         char* partials, hipStream_t stream, hipEvent_t ev_begin = nullptr,
                          hipEvent_t ev_end = nullptr);
+// Bytes of the static scratch array of pkv_decode_attention_noalloc, and the
+// address of the current device's copy (looked up once per device).
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch(int device, char** ptr);
 
 struct PrefillArgs {
   const void* q;

@@ -204,6 +204,28 @@ size_t pkv_decode_workspace_bytes(const pkv_pool* pool, int batch, int n_head,
 int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,
                             int max_context_len);
 
+/* pkv_decode_attention without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory during a call
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as pkv_decode_attention
+ * (bit for bit), but the split-context partials go to a static device array
+ * of PKV_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds for
+ * the life of the process, not to the pool's workspace; the call makes no
+ * hipMalloc, hipFree or other allocating call and records no profile
+ * events.  A launch whose partials need more than the array
+ * (pkv_decode_workspace_bytes > PKV_NOALLOC_SCRATCH_BYTES, e.g. batch 256
+ * with contexts up to 32k on 8 kv heads of 128) returns PKV_ERR_UNSUPPORTED
+ * before anything is enqueued.  All calls on one GPU share its array, so
+ * calls that overlap on one GPU (different streams, threads or pools)
+ * race: the caller orders them, e.g. on one stream. */
+#define PKV_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int pkv_decode_attention_noalloc(pkv_pool* pool, int layer, const void* q, void* out,
+                                 int out_dtype, const int32_t* block_tables,
+                                 int max_blocks_per_seq, const int32_t* context_lens,
+                                 int max_context_len, int batch, int n_head,
+                                 float scale, const void* k_new, const void* v_new,
+                                 void* stream);
+
 /* ---- chunked prefill attention (prefill_seq attention,
  * transformer.rs:139-196, generalised to a prior context) -----------------
  * Sequence s has q_len_s = cu_q_lens[s+1]-cu_q_lens[s] query tokens whose K/V
