@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -258,8 +259,12 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   void* hplan = nullptr;
   e = hipMalloc(&dplan, p->plan_bytes);
   if (e == hipSuccess) e = hipHostMalloc(&hplan, p->plan_bytes, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->plan_uploaded, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->plan_consumed, hipEventDisableTiming);
   if (e != hipSuccess) {
+    if (p->plan_uploaded) (void)hipEventDestroy(p->plan_uploaded);
     if (dplan) (void)hipFree(dplan);
+    if (hplan) (void)hipHostFree(hplan);
     (void)hipFree(base);
     (void)hipFree(err);
     delete p;
@@ -272,6 +277,8 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   // (looked up once per device, with the device current).
   e = pkv::noalloc_scratch(device, &p->scratch);
   if (e != hipSuccess) {
+    (void)hipEventDestroy(p->plan_uploaded);
+    (void)hipEventDestroy(p->plan_consumed);
     (void)hipFree(dplan);
     (void)hipHostFree(hplan);
     (void)hipFree(base);
@@ -292,6 +299,8 @@ int pkv_pool_destroy(pkv_pool* p) {
   if (p->ws) (void)hipFree(p->ws);
   if (p->plan) (void)hipFree(p->plan);
   if (p->plan_host) (void)hipHostFree(p->plan_host);
+  if (p->plan_uploaded) (void)hipEventDestroy(p->plan_uploaded);
+  if (p->plan_consumed) (void)hipEventDestroy(p->plan_consumed);
   for (auto& ev : p->prof_events) {
     (void)hipEventDestroy(ev.first);
     (void)hipEventDestroy(ev.second);
@@ -356,6 +365,28 @@ int pkv_pool_fill_normal(pkv_pool* p, uint64_t seed, void* stream) {
   DeviceGuard dg(p->device);
   hipError_t e = pkv::launch_fill_normal(p, seed, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(p, e, "fill_normal launch");
+  return PKV_OK;
+}
+
+int pkv_pool_verify_normal(pkv_pool* p, uint64_t seed, const int32_t* blocks,
+                           const int32_t* origin, int n, uint64_t* mismatches, void* stream) {
+  CHECK_POOL(p);
+  if (!mismatches) return fail(p, PKV_ERR_INVALID, "mismatches is NULL");
+  *mismatches = 0;
+  if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
+  if (n == 0) return PKV_OK;
+  if (!blocks || !origin) return fail(p, PKV_ERR_INVALID, "blocks and origin must be non-NULL");
+  DeviceGuard dg(p->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // the count lives in the pool's device error buffer, after the error word
+  unsigned long long* count = reinterpret_cast<unsigned long long*>(p->err + 2);
+  unsigned long long host = 0;
+  hipError_t e = hipMemsetAsync(count, 0, sizeof host, s);
+  if (e == hipSuccess) e = pkv::launch_verify_normal(p, seed, blocks, origin, n, count, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(&host, count, sizeof host, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(p, e, "verify_normal");
+  *mismatches = host;
   return PKV_OK;
 }
 
@@ -450,6 +481,40 @@ int pkv_gather_varlen(pkv_pool* p, int layer, const int32_t* block_tables,
 
 static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee);
 
+// PKV_DEBUG set (and not "0") in the environment turns on host checks of
+// device id arrays that the fast path leaves to the caller's contract.
+static bool debug_checks() {
+  const char* v = std::getenv("PKV_DEBUG");
+  return v && *v && std::strcmp(v, "0") != 0;
+}
+
+// The copy-on-write contract of pkv_copy_blocks, checked on host copies of
+// the id arrays: ids in range, destinations distinct, no destination also a
+// source of the call.
+static int check_cow_contract(pkv_pool* p, const int32_t* src, const int32_t* dst, int n,
+                              hipStream_t s) {
+  std::vector<int32_t> hs(n), hd(n);
+  hipError_t e = hipStreamSynchronize(s);
+  if (e == hipSuccess) e = hipMemcpy(hs.data(), src, n * sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(hd.data(), dst, n * sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(p, e, "copy_blocks debug check");
+  std::vector<char> role(p->num_blocks, 0);  // 1 = source, 2 = destination
+  for (int i = 0; i < n; ++i) {
+    if (hs[i] < 0 || hs[i] >= p->num_blocks || hd[i] < 0 || hd[i] >= p->num_blocks)
+      return fail(p, PKV_ERR_INVALID, "copy_blocks: pair %d (%d -> %d) out of range [0, %d)", i,
+                  hs[i], hd[i], p->num_blocks);
+    role[hs[i]] |= 1;
+  }
+  for (int i = 0; i < n; ++i) {
+    if (role[hd[i]] & 2)
+      return fail(p, PKV_ERR_INVALID, "copy_blocks: destination block %d appears twice", hd[i]);
+    if (role[hd[i]] & 1)
+      return fail(p, PKV_ERR_INVALID, "copy_blocks: destination block %d is also a source", hd[i]);
+    role[hd[i]] |= 2;
+  }
+  return PKV_OK;
+}
+
 int pkv_copy_blocks(pkv_pool* p, const int32_t* src, const int32_t* dst, int n, void* stream) {
   CHECK_POOL(p);
   if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
@@ -457,6 +522,8 @@ int pkv_copy_blocks(pkv_pool* p, const int32_t* src, const int32_t* dst, int n, 
   if (!src || !dst) return fail(p, PKV_ERR_INVALID, "src and dst must be non-NULL");
   DeviceGuard dg(p->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (debug_checks())
+    if (int rc = check_cow_contract(p, src, dst, n, s)) return rc;
   hipEvent_t eb = nullptr, ee = nullptr;
   if (int rc = profile_slot(p, &eb, &ee)) return rc;
   hipError_t e = eb ? hipEventRecord(eb, s) : hipSuccess;
@@ -479,22 +546,34 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   size_t ob = ops.size() * sizeof(int32_t), sb = starts.size() * sizeof(int32_t);
   // The plan buffers were sized at pool creation for the largest plan (see
-  // plan_capacity_bytes); the call ends with a stream sync, so they are free.
+  // plan_capacity_bytes) and are reused by every call: the host staging copy
+  // once the previous call's upload has completed (normally long before),
+  // the device copy once the previous call's kernel has, which the upload
+  // waits for on the device -- the host does not wait for the moves.
   if (ob + sb > p->plan_bytes)
     return fail(p, PKV_ERR_INVALID, "compact: plan of %zu bytes exceeds its buffer", ob + sb);
+  hipError_t e = hipSuccess;
+  if (p->plan_pending && (e = hipEventSynchronize(p->plan_uploaded)) != hipSuccess)
+    return hip_fail(p, e, "compact: previous plan upload");
   std::memcpy(p->plan_host, ops.data(), ob);
   std::memcpy(p->plan_host + ob, starts.data(), sb);
   int32_t* d_ops = reinterpret_cast<int32_t*>(p->plan);
   int32_t* d_starts = d_ops + ops.size();
   hipEvent_t eb = nullptr, ee = nullptr;
   if (int rc = profile_slot(p, &eb, &ee)) return rc;
-  hipError_t e = hipMemcpyAsync(p->plan, p->plan_host, ob + sb, hipMemcpyHostToDevice, s);
+  if (p->plan_pending) e = hipStreamWaitEvent(s, p->plan_consumed, 0);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->plan, p->plan_host, ob + sb, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipEventRecord(p->plan_uploaded, s);
   if (e == hipSuccess && eb) e = hipEventRecord(eb, s);
   if (e == hipSuccess) e = pkv::launch_compact(p, d_ops, d_starts, n_chains, s);
   if (e == hipSuccess && ee) e = hipEventRecord(ee, s);
-  hipError_t e2 = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_fail(p, e, "compact");
-  if (e2 != hipSuccess) return hip_fail(p, e2, "compact sync");
+  if (e == hipSuccess) e = hipEventRecord(p->plan_consumed, s);
+  if (e != hipSuccess) {
+    (void)hipStreamSynchronize(s);  // leave the buffers free for the next call
+    p->plan_pending = false;
+    return hip_fail(p, e, "compact");
+  }
+  p->plan_pending = true;
   return PKV_OK;
 }
 
@@ -844,8 +923,11 @@ float pkv_sample_draw(uint64_t seed) { return pkv::sample_draw(seed); }
 int pkv_sample(const void* logits, int dtype, long long row_stride, int batch, int vocab,
                const float* temperatures, int top_k, float top_p, uint64_t seed,
                int32_t* tokens, void* stream) {
-  if (batch < 0 || vocab < 0 || vocab > (1 << 24))
-    return fail(nullptr, PKV_ERR_INVALID, "sample: batch %d, vocab %d (0 .. 2^24)", batch, vocab);
+  // Token masses are 2^-40 fixed point (at most 2^40 each) summed in 64-bit
+  // integers, so a row of 2^24 tokens could reach 2^64: vocab < 2^24.
+  if (batch < 0 || vocab < 0 || vocab >= (1 << 24))
+    return fail(nullptr, PKV_ERR_INVALID, "sample: batch %d, vocab %d (0 .. 2^24 - 1)", batch,
+                vocab);
   if (batch == 0) return PKV_OK;
   if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)
     return fail(nullptr, PKV_ERR_INVALID, "sample: dtype %d", dtype);

@@ -41,6 +41,12 @@ struct pkv_pool {
   char* plan = nullptr;
   char* plan_host = nullptr;
   size_t plan_bytes = 0;
+  // recorded by each compaction after its plan upload (the staging copy may
+  // be rewritten once it has completed) and after its kernel (the device
+  // plan may be rewritten once it has completed)
+  hipEvent_t plan_uploaded = nullptr;
+  hipEvent_t plan_consumed = nullptr;
+  bool plan_pending = false;
   // main-kernel timing events (pkv_pool_profile)
   bool prof_on = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
@@ -103,6 +109,11 @@ hipError_t launch_compact(const pkv_pool* p, const int32_t* ops,
                           hipStream_t stream);
 hipError_t launch_fill_normal(const pkv_pool* p, uint64_t seed,
                               hipStream_t stream);
+// Adds to *count the 16-byte chunks of blocks[i] (every layer, K and V) that
+// differ from what launch_fill_normal(seed) wrote into block origin[i].
+hipError_t launch_verify_normal(const pkv_pool* p, uint64_t seed, const int32_t* blocks,
+                                const int32_t* origin, int n, unsigned long long* count,
+                                hipStream_t stream);
 
 // Host computation of the RoPE tables (Rope::new, rope.rs:14-23).
 void rope_tables_host(int rope_dim, float freq_base, int max_seq, float* cos_t,

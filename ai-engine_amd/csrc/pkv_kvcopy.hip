@@ -9,6 +9,8 @@
 // thread issues all of its loads before its stores so that several requests
 // are in flight per lane.  Rows are head_dim * elem_bytes >= 128 bytes, so a
 // token row is always a whole number of 16-byte chunks.
+#include <algorithm>
+
 #include "pkv_device.h"
 #include "pkv_internal.h"
 
@@ -211,12 +213,36 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   return z ^ (z >> 31);
 }
 
-// N(0,1) by Box-Muller from two 32-bit uniforms of one hash.
+// N(0,1) by Box-Muller from two 32-bit uniforms of one hash.  No fused
+// multiply-adds, so the value does not depend on the code around a call.
 __device__ __forceinline__ float normal_at(uint64_t seed, uint64_t idx) {
+#pragma clang fp contract(off)
   uint64_t h = mix64(seed + 0x9e3779b97f4a7c15ull * (idx + 1));
   float u1 = ((uint32_t)(h >> 40) + 1) * (1.0f / 16777217.0f);  // (0,1]
   float u2 = (uint32_t)(h & 0xffffffu) * (1.0f / 16777216.0f);
   return sqrtf(-2.0f * __logf(u1)) * __cosf(6.28318530718f * u2);
+}
+
+// The 16-byte chunk `chunk` of a slab filled with seed (4 or 8 elements of
+// normal_at, rounded to DT).  One out-of-line body serves the fill and its
+// verification, so both produce the same bits.
+template <int DT>
+__device__ __noinline__ u32x4 normal_chunk(uint64_t seed, size_t chunk) {
+  u32x4 w;
+  if constexpr (DT == PKV_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(normal_at(seed, chunk * 4 + i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = normal_at(seed, chunk * 8 + 2 * i);
+      float b = normal_at(seed, chunk * 8 + 2 * i + 1);
+      uint32_t lo = DT == PKV_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);
+      uint32_t hi = DT == PKV_BF16 ? f32_to_bf16_bits(b) : f32_to_f16_bits(b);
+      w[i] = lo | (hi << 16);
+    }
+  }
+  return w;
 }
 
 template <int DT>
@@ -226,24 +252,51 @@ __global__ void __launch_bounds__(kCopyThreads)
   constexpr int EPL = DT == PKV_F32 ? 4 : 8;
   size_t chunk = (size_t)blockIdx.x * kCopyThreads + threadIdx.x;
   size_t stride = (size_t)gridDim.x * kCopyThreads;
-  for (; chunk * EPL < n_elems; chunk += stride) {
-    u32x4 w;
-    if constexpr (DT == PKV_F32) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = __float_as_uint(normal_at(seed, chunk * 4 + i));
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float a = normal_at(seed, chunk * 8 + 2 * i);
-        float b = normal_at(seed, chunk * 8 + 2 * i + 1);
-        uint32_t lo = DT == PKV_BF16 ? f32_to_bf16_bits(a) : f32_to_f16_bits(a);
-        uint32_t hi = DT == PKV_BF16 ? f32_to_bf16_bits(b) : f32_to_f16_bits(b);
-        w[i] = lo | (hi << 16);
+  for (; chunk * EPL < n_elems; chunk += stride)
+    reinterpret_cast<u32x4*>(base)[chunk] = normal_chunk<DT>(seed, chunk);
+}
+
+// Verification of a filled pool after blocks moved: entry i says that block
+// blocks[i] should hold, in every layer's K and V, the bytes the fill wrote
+// into block origin[i].  Items (entry, K/V slab of a layer) are spread over
+// a grid of long-lived workgroups; each counts the 16-byte chunks that
+// differ and adds its count to *count once.  An id out of range sets the
+// block error bit and counts the item's chunks as mismatches.
+template <int DT>
+__global__ void __launch_bounds__(kCopyThreads)
+    verify_normal_kernel(const char* __restrict__ base, size_t layer_bytes, int block_vec,
+                         int num_blocks, const int32_t* __restrict__ blocks,
+                         const int32_t* __restrict__ origin, int n, int n_slabs, uint64_t seed,
+                         unsigned long long* count, uint32_t* err) {
+  __shared__ unsigned long long wg_count;
+  if (threadIdx.x == 0) wg_count = 0;
+  __syncthreads();
+  unsigned long long bad = 0;
+  const long long items = (long long)n * n_slabs;
+  for (long long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int i = (int)(it / n_slabs);
+    const int slab = (int)(it % n_slabs);
+    const int b = blocks[i], o = origin[i];
+    if (b < 0 || o < 0 || b >= num_blocks || o >= num_blocks) {
+      if (threadIdx.x == 0) {
+        atomicOr(err, PKV_EBIT_BLOCK);
+        bad += block_vec;
       }
+      continue;
     }
-    reinterpret_cast<u32x4*>(base)[chunk] = w;
+    const u32x4* got =
+        reinterpret_cast<const u32x4*>(base + (size_t)slab * layer_bytes) + (size_t)b * block_vec;
+    // chunk index of the origin block's bytes in the whole slab
+    const size_t c0 = ((size_t)slab * num_blocks + o) * block_vec;
+    for (int v = threadIdx.x; v < block_vec; v += kCopyThreads) {
+      const u32x4 x = __builtin_nontemporal_load(got + v);
+      const u32x4 w = normal_chunk<DT>(seed, c0 + v);
+      bad += (x[0] != w[0]) | (x[1] != w[1]) | (x[2] != w[2]) | (x[3] != w[3]);
+    }
   }
+  if (bad) atomicAdd(&wg_count, bad);
+  __syncthreads();
+  if (threadIdx.x == 0 && wg_count) atomicAdd(count, wg_count);
 }
 
 int ilog2(int x) {
@@ -342,6 +395,34 @@ hipError_t launch_fill_normal(const pkv_pool* p, uint64_t seed,
       break;
     default:
       fill_normal_kernel<PKV_BF16><<<grid, kCopyThreads, 0, stream>>>(p->base, n_elems, seed);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_verify_normal(const pkv_pool* p, uint64_t seed, const int32_t* blocks,
+                                const int32_t* origin, int n, unsigned long long* count,
+                                hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int block_vec = (int)(p->block_bytes / 16);
+  const int n_slabs = 2 * p->n_layers;
+  const long long items = (long long)n * n_slabs;
+  const unsigned grid = (unsigned)std::min<long long>(items, kCompactGrid);
+  switch (p->dtype) {
+    case PKV_F32:
+      verify_normal_kernel<PKV_F32><<<grid, kCopyThreads, 0, stream>>>(
+          p->base, p->layer_bytes, block_vec, p->num_blocks, blocks, origin, n, n_slabs, seed,
+          count, p->err);
+      break;
+    case PKV_F16:
+      verify_normal_kernel<PKV_F16><<<grid, kCopyThreads, 0, stream>>>(
+          p->base, p->layer_bytes, block_vec, p->num_blocks, blocks, origin, n, n_slabs, seed,
+          count, p->err);
+      break;
+    default:
+      verify_normal_kernel<PKV_BF16><<<grid, kCopyThreads, 0, stream>>>(
+          p->base, p->layer_bytes, block_vec, p->num_blocks, blocks, origin, n, n_slabs, seed,
+          count, p->err);
       break;
   }
   return hipGetLastError();

@@ -610,6 +610,7 @@ __global__ void __launch_bounds__(kST) sample_kernel(SampleArgs a) {
 // workgroup per row: the last scan, a tie walk when needed, the token).
 constexpr int kMaxG = 32;
 static_assert(kB1 % kST == 0 && kB2 == kST && kMaxG <= kST, "split-path loads");
+static_assert(sizeof(unsigned long long) % alignof(unsigned int) == 0, "");
 struct SplitWs {  // per row
   float pmax[kMaxG];  // per workgroup: max x / -x (sampled), max x (greedy)
   int pidx[kMaxG];    // greedy: index of that max (INT_MAX: none)
@@ -618,10 +619,15 @@ struct SplitWs {  // per row
   unsigned long long h3[kB2];
   unsigned int cnt3[kB2];
   int min3[kB2];
-  unsigned int cntc[kMaxG][kB2];  // third digit: tokens per bucket in each chunk
   uint32_t pre1, pre2;            // first one / two digits of the selected key
   unsigned long long rem1, rem2;  // what remains to select inside them
 };
+// Behind the batch's SplitWs rows: the third digit's tokens per bucket in
+// each chunk, [batch][G][kB2] unsigned ints, sized by the call's G.
+__device__ __forceinline__ unsigned int* chunk_counts(SplitWs* ws, int batch, int row, int G,
+                                                      int g) {
+  return reinterpret_cast<unsigned int*>(ws + batch) + ((size_t)row * G + g) * kB2;
+}
 
 // Workgroup blockIdx.x's chunk of a row: multiples of 8 elements (whole
 // 16-byte vectors for every dtype), the last one ending at V.
@@ -772,8 +778,10 @@ __global__ void __launch_bounds__(kST) split_digit_kernel(SampleArgs a, SplitWs*
   digit_pass<false>(sm, rw, lo, hi, prefix, LAST ? 0xfffffc00u : 0xfff00000u, LAST ? 0 : 10,
                     LAST);
   SplitWs& w = ws[row];
-  if (LAST)  // every bucket, zeros included: no clearing needed
-    for (int b = tid; b < kB2; b += kST) w.cntc[blockIdx.x][b] = sm.cnt[b];
+  if (LAST) {  // every bucket, zeros included: no clearing needed
+    unsigned int* cc = chunk_counts(ws, (int)gridDim.y, row, (int)gridDim.x, (int)blockIdx.x);
+    for (int b = tid; b < kB2; b += kST) cc[b] = sm.cnt[b];
+  }
   for (int b = tid; b < kB2; b += kST) {
     if (!sm.h[b]) continue;
     atomicAdd(LAST ? &w.h3[b] : &w.h2[b], sm.h[b]);
@@ -832,7 +840,8 @@ __global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs
     // The chunks' counts of the selected key, in index order, locate the
     // chunk holding the n-th tied token; only that chunk is walked.
     if (tid < kWave) {
-      const unsigned long long c = tid < G ? (unsigned long long)w.cntc[tid][b] : 0ull;
+      const unsigned long long c =
+          tid < G ? (unsigned long long)chunk_counts(ws, (int)gridDim.x, row, G, tid)[b] : 0ull;
       unsigned long long incl = c;
       for (int d = 1; d < kWave; d <<= 1) {
         const unsigned long long o = shfl_up_u64(incl, d);
@@ -871,7 +880,8 @@ hipError_t launch_dt(const SampleArgs& a, int batch, hipStream_t stream) {
   const int G = split_groups(batch, a.vocab, a.temps, a.top_k, a.top_p);
   if (G > 1) {
     void* p = nullptr;
-    if (hipMallocAsync(&p, (size_t)batch * sizeof(SplitWs), stream) == hipSuccess) {
+    const size_t bytes = (size_t)batch * (sizeof(SplitWs) + (size_t)G * kB2 * sizeof(unsigned));
+    if (hipMallocAsync(&p, bytes, stream) == hipSuccess) {
       SplitWs* ws = static_cast<SplitWs*>(p);
       const dim3 grid(G, batch);
       split_max_kernel<DT, VEC><<<grid, kST, 0, stream>>>(a, ws);

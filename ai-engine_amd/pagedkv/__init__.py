@@ -165,18 +165,27 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
         raise ValueError("logits must be (batch, vocab) with unit stride along vocab")
     B, V = logits.shape
     dev = logits.device
-    if out is None:
-        out = torch.empty(B, dtype=torch.int32, device=dev)
-    t = None
-    if temperatures is not None:
-        t = torch.as_tensor(temperatures, dtype=torch.float32).to(dev).contiguous()
-        if t.numel() != B:
-            raise ValueError("temperatures must have one value per row")
-    check(lib().pkv_sample(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
-                           logits.stride(0) if B > 1 else V, B, V,
-                           _dev_ptr(t) if t is not None else None, top_k or 0,
-                           1.0 if top_p is None else float(top_p), seed, _dev_ptr(out),
-                           _stream_ptr(stream)), None)
+    # The kernels run on `stream`: it first waits for the work queued so far
+    # on the current stream (which produced the logits), and the temporaries
+    # made here are allocated on it, so they are neither read early nor
+    # reused before the launch has run.
+    cur = torch.cuda.current_stream(dev)
+    s = cur if stream is None else stream
+    if s != cur:
+        s.wait_stream(cur)
+    with torch.cuda.stream(s):
+        if out is None:
+            out = torch.empty(B, dtype=torch.int32, device=dev)
+        t = None
+        if temperatures is not None:
+            t = torch.as_tensor(temperatures, dtype=torch.float32).to(dev).contiguous()
+            if t.numel() != B:
+                raise ValueError("temperatures must have one value per row")
+        check(lib().pkv_sample(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
+                               logits.stride(0) if B > 1 else V, B, V,
+                               _dev_ptr(t) if t is not None else None, top_k or 0,
+                               1.0 if top_p is None else float(top_p), seed, _dev_ptr(out),
+                               _stream_ptr(s)), None)
     return out
 
 
@@ -278,6 +287,18 @@ class PagedKvCache:
 
     def fill_normal(self, seed: int, stream=None) -> None:
         check(lib().pkv_pool_fill_normal(self._h, seed, _stream_ptr(stream)), self._h)
+
+    def verify_normal(self, seed: int, blocks, origin, stream=None) -> int:
+        """16-byte chunks of blocks[i] (all layers, K and V) that differ from
+        what fill_normal(seed) wrote into block origin[i] (synchronous)."""
+        b = _i32(blocks, self.device)
+        o = _i32(origin, self.device)
+        if b.numel() != o.numel():
+            raise ValueError("blocks and origin must have the same length")
+        n = ctypes.c_uint64()
+        check(lib().pkv_pool_verify_normal(self._h, seed, _dev_ptr(b), _dev_ptr(o), b.numel(),
+                                           ctypes.byref(n), _stream_ptr(stream)), self._h)
+        return int(n.value)
 
     def copy_blocks(self, src, dst, stream=None) -> None:
         """Copy-on-write: block dst[i] <- src[i] in every layer, K and V."""

@@ -971,11 +971,13 @@ def churn(args, dev) -> int:
         seqs.append(t)
         live += nb
         i += 1
-    # fork events: a random block of a random sequence is copied to a fresh block
+    # fork events: a random block of a random (pre-fork) sequence is copied to
+    # a fresh block; no destination is also a source (the CoW contract)
     r = wl.splitmix64(args.seed ^ 0xF04C, 2 * 512)
     src, dst = [], []
+    n_parents = len(seqs)
     for k in range(512):
-        t = seqs[int(r[2 * k] % np.uint64(len(seqs)))]
+        t = seqs[int(r[2 * k] % np.uint64(n_parents))]
         blocks = t.blocks
         src.append(blocks[int(r[2 * k + 1] % np.uint64(len(blocks)))])
         child = pagedkv.BlockTable()
@@ -1001,6 +1003,14 @@ def churn(args, dev) -> int:
     cow_kms /= max(1, cow_n)
     cow_bytes = 2 * 512 * cache.block_bytes * 2 * L
     cache.check()
+    # validation (untimed): every live block, copies included, holds the
+    # bytes the fill wrote into its original block
+    origin = np.arange(N, dtype=np.int32)
+    origin[np.asarray(dst)] = origin[np.asarray(src)]
+    live_ids = np.concatenate([np.array(t.blocks, np.int32) for t in seqs if len(t)])
+    t0 = time.time()
+    bad_cow = cache.verify_normal(args.seed, live_ids, origin[live_ids])
+    verify_s = time.time() - t0
     # eviction of a random 25% of sequences
     order = wl.permutation(args.seed ^ 0xE51C, len(seqs))
     n_evict = len(seqs) // 4
@@ -1035,11 +1045,24 @@ def churn(args, dev) -> int:
     comp_kms, comp_n = cache.profile_read()
     comp_kms /= max(1, comp_n)
     cache.profile(False)
-    if comp_reps % 2:
-        cache.compact(remap, surv)  # leave the survivors where the tables say
+    if comp_reps % 2 == 0:
+        cache.compact(surv, remap)  # untimed: end on a forward compaction
     moved = int((surv != remap).sum())
     comp_bytes = 2 * moved * cache.block_bytes * 2 * L
     cache.check()
+    # validation (untimed): block remap[i] holds what survivor surv[i] held
+    t0 = time.time()
+    bad_comp = cache.verify_normal(args.seed, remap, origin[surv])
+    verify_s += time.time() - t0
+    validation = {"validated": bad_cow == 0 and bad_comp == 0,
+                  "mismatches": int(bad_cow + bad_comp),
+                  "blocks_checked": int(live_ids.size + remap.size),
+                  "method": "device recomputation of every live block's fill bytes "
+                            "(counter hash of seed, layer, K/V, original block, element) "
+                            "after the CoW copies and after compaction",
+                  "seconds": round(verify_s, 2)}
+    log(f"[bench] cfg5 validation: {validation['mismatches']} mismatching 16-byte chunks in "
+        f"{validation['blocks_checked']} blocks x {2 * L} slabs ({verify_s:.1f} s)")
     step_ms = cow_ms + comp_ms
     log(f"[bench] cfg5: CoW {cow_ms:.3f} ms ({cow_bytes / (cow_ms / 1e3) / 1e9:.0f} GB/s), "
         f"compaction {comp_ms:.2f} ms incl. host plan + upload, kernel {comp_kms:.2f} ms "
@@ -1073,6 +1096,7 @@ def churn(args, dev) -> int:
                      "traffic": traffic, "kernel": "pkv::compact_kernel",
                      "kernel_avg_us": round(comp_kms * 1e3, 1),
                      "algorithmic_bytes_per_launch": comp_bytes},
+        "validation": validation,
         "cow": {"copies": 512, "ms": round(cow_ms, 4), "kernel_ms": round(cow_kms, 4),
                 "GBps": round(cow_bytes / (cow_ms / 1e3) / 1e9, 1)},
         "compaction": {"moved_blocks": moved, "calls": comp_reps,

@@ -107,6 +107,16 @@ int pkv_pool_write(pkv_pool* pool, int layer, int which, size_t byte_offset,
  * A workload generator for benchmarks; no reference counterpart. */
 int pkv_pool_fill_normal(pkv_pool* pool, uint64_t seed, void* stream);
 
+/* The check of pkv_pool_fill_normal after blocks have moved (copy-on-write,
+ * compaction; no reference counterpart): counts, into *mismatches, the
+ * 16-byte chunks of block blocks[i], over every layer's K and V, that differ
+ * from what pkv_pool_fill_normal(seed) wrote into block origin[i].
+ * blocks, origin: device int32 [n]; an id out of range counts the item as
+ * mismatching and is reported by pkv_pool_check().  Synchronous. */
+int pkv_pool_verify_normal(pkv_pool* pool, uint64_t seed, const int32_t* blocks,
+                           const int32_t* origin, int n, uint64_t* mismatches,
+                           void* stream);
+
 /* ---- KV append / scatter (KvPool::write, attention.rs:57-83) -----------
  * k, v: [n_tokens][n_kv_head][head_dim] in the pool dtype.
  * slot_mapping: [n_tokens] int32, slot = block * block_size + offset
@@ -143,7 +153,12 @@ int pkv_gather_varlen(pkv_pool* pool, int layer, const int32_t* block_tables,
 /* ---- block copy (copy-on-write after fork; no reference counterpart) ----
  * For every layer and both K and V: block dst[i] <- block src[i], i < n.
  * src, dst: device int32 [n].  dst ids must be distinct and no dst may be a
- * src of the same call (the CoW contract: dst blocks are fresh). */
+ * src of the same call (the CoW contract: dst blocks are fresh); otherwise
+ * the copies race.  An id out of range is skipped and reported by
+ * pkv_pool_check().  With PKV_DEBUG set in the environment (to anything but
+ * "0") the call first checks the contract on host copies of src and dst
+ * (synchronising the stream) and returns PKV_ERR_INVALID, copying nothing,
+ * if it is broken. */
 int pkv_copy_blocks(pkv_pool* pool, const int32_t* src, const int32_t* dst,
                     int n, void* stream);
 
@@ -152,9 +167,11 @@ int pkv_copy_blocks(pkv_pool* pool, const int32_t* src, const int32_t* dst,
  * the dst set may overlap the src set (e.g. survivors gathered into a
  * contiguous prefix).  src ids distinct, dst ids distinct.  The plan (chains
  * and cycles of the move graph) is built on the host, so ids are host arrays;
- * it is uploaded to a device buffer the pool keeps (grown on demand) and the
- * call returns when the moves are done.  Each byte is read once and written
- * once; no scratch pool is allocated. */
+ * it is uploaded to a device buffer the pool allocates once, at creation,
+ * for the largest plan.  Stream-ordered: the call returns once the moves are
+ * enqueued (it waits only, if at all, for the previous call's plan upload
+ * before reusing the pinned staging copy).  Each byte is read once and
+ * written once; no scratch pool is allocated. */
 int pkv_compact(pkv_pool* pool, const int32_t* src_host,
                 const int32_t* dst_host, int n, void* stream);
 
@@ -363,12 +380,14 @@ int pkv_append_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
  * in the reference.  The token equals the reference's except where its f32
  * running sums fall within their rounding of r or top_p.  Temperatures must
  * be finite and logits of sampled rows free of NaN (the reference's sort is
- * unspecified there).  Runs on the calling thread's current device.  Batches
- * of at most 128 rows with temperatures and no top_k / top_p split each row
- * over several workgroups, with ~56 KB per row of partial histograms in a
- * stream-ordered allocation on `stream` (hipMallocAsync / hipFreeAsync,
- * capturable in a HIP graph); if that allocation fails, one workgroup per
- * row.  Both give the same tokens. */
+ * unspecified there).  vocab < 2^24 (probability masses are 2^-40 fixed
+ * point summed in 64 bits).  Runs on the calling thread's current device.
+ * Batches of at most 128 rows with temperatures and no top_k / top_p split
+ * each row over G = min(32, 256 / batch, ceil(vocab / 4096)) workgroups,
+ * with 57,624 + 4,096 G bytes per row of partial histograms (at most 184 KiB
+ * per row; 1.5 MB for 8 rows, 8.4 MB for 128) in a stream-ordered allocation
+ * on `stream` (hipMallocAsync / hipFreeAsync, capturable in a HIP graph); if
+ * that allocation fails, one workgroup per row.  Both give the same tokens. */
 int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
                int vocab, const float* temperatures, int top_k, float top_p,
                uint64_t seed, int32_t* tokens, void* stream);

@@ -270,3 +270,101 @@ def test_fill_normal_deterministic_and_standard(gpu):
     x = wl.widen(a, wl.BF16)
     assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1) < 0.01
     cache.close()
+
+
+def test_cfg5_geometry_churn_against_oracle(gpu):
+    # BASELINE configs[4]'s block geometry (8 kv heads, head_dim 128, bf16,
+    # block_size 16: 32 KiB per block and slab) on a 2-layer pool of 6,144
+    # blocks (768 MiB): 60 % occupancy, copy-on-write of 300 blocks into
+    # fresh ones, eviction, then the survivors gathered into a prefix under a
+    # random remap (long chains and cycles, in place).  Every byte of the pool
+    # equals the oracle's closed form after each step; the device
+    # recomputation of the fill (pkv_pool_verify_normal) agrees with it.
+    N, L, seed = 6144, 2, 505
+    cache = pagedkv.PagedKvCache(L, N, 16, 8, 128, torch.bfloat16)
+    cache.fill_normal(seed)
+    pool = _all_bytes(cache)
+    rng = np.random.default_rng(5)
+    perm = rng.permutation(N).astype(np.int32)
+    live = perm[: int(0.6 * N)]
+    free = perm[int(0.6 * N):]
+    src = rng.choice(live, size=300, replace=False).astype(np.int32)
+    dst = free[:300].copy()
+    cache.copy_blocks(src, dst)
+    cache.check()
+    oracle.copy_blocks(pool, L, cache.block_bytes, src, dst)
+    assert np.array_equal(_all_bytes(cache), pool)
+    origin = np.arange(N, dtype=np.int32)
+    origin[dst] = origin[src]
+    held = np.concatenate([live, dst])
+    assert cache.verify_normal(seed, held, origin[held]) == 0
+    # evict a quarter, gather the rest into [0, n) under a random remap
+    surv = rng.permutation(held)[: int(0.75 * held.size)].astype(np.int32)
+    remap = rng.permutation(surv.size).astype(np.int32)
+    cache.compact(surv, remap)
+    cache.check()
+    oracle.compact(pool, L, cache.block_bytes, surv, remap)
+    assert np.array_equal(_all_bytes(cache), pool)
+    assert cache.verify_normal(seed, remap, origin[surv]) == 0
+    cache.close()
+
+
+def test_verify_normal_counts_planted_differences(gpu):
+    # the check is not vacuous: a changed byte, a wrong origin and a wrong
+    # seed are all counted, chunk by chunk
+    cache = pagedkv.PagedKvCache(3, 40, 16, 8, 128, torch.bfloat16)
+    cache.fill_normal(77)
+    ids = np.arange(40, dtype=np.int32)
+    assert cache.verify_normal(77, ids, ids) == 0
+    slabs, block_chunks = 2 * 3, cache.block_bytes // 16
+    assert cache.verify_normal(78, ids[:5], ids[:5]) == 5 * slabs * block_chunks
+    assert cache.verify_normal(77, ids[:3], ids[1:4]) == 3 * slabs * block_chunks
+    off = 7 * cache.block_bytes + 100           # layer 1's V, block 7: flip one byte
+    byte = cache.read_bytes(1, pagedkv.V, off, 1)
+    cache.write_bytes(1, pagedkv.V, byte ^ np.uint8(0xFF), offset=off)
+    assert cache.verify_normal(77, ids, ids) == 1
+    cache.close()
+
+
+def test_copy_blocks_contract_checked_in_debug_mode(gpu, monkeypatch):
+    # PKV_DEBUG: a destination that is also a source, a repeated destination
+    # or an id out of range is refused before anything is copied
+    cache = pagedkv.PagedKvCache(1, 16, 16, 2, 64, torch.float16)
+    _fill(cache, 3)
+    before = _all_bytes(cache)
+    monkeypatch.setenv("PKV_DEBUG", "1")
+    for src, dst, what in (([1, 2], [3, 1], b"also a source"), ([1, 2], [5, 5], b"twice"),
+                           ([1, 2], [5, 16], b"out of range")):
+        with pytest.raises(pagedkv.PagedKvError, match=what.decode()):
+            cache.copy_blocks(src, dst)
+    assert np.array_equal(_all_bytes(cache), before)
+    cache.copy_blocks([1, 2], [5, 6])   # a valid call still copies
+    exp = before.copy()
+    oracle.copy_blocks(exp, 1, cache.block_bytes, [1, 2], [5, 6])
+    assert np.array_equal(_all_bytes(cache), exp)
+    cache.close()
+
+
+def test_compactions_back_to_back_on_two_streams(gpu):
+    # pkv_compact returns once the moves are enqueued; a second call on
+    # another stream reuses the plan buffers only after the first call's
+    # kernel (a device-side wait), so both plans apply in order
+    N = 1024
+    cache = pagedkv.PagedKvCache(2, N, 16, 4, 128, torch.bfloat16)
+    _fill(cache, 8)
+    exp = _all_bytes(cache)
+    rng = np.random.default_rng(9)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    plans = []
+    for k in range(4):
+        src = rng.choice(N, size=600, replace=False).astype(np.int32)
+        dst = rng.permutation(src).astype(np.int32)   # cycles only
+        plans.append((src, dst))
+    for k, (src, dst) in enumerate(plans):
+        cache.compact(src, dst, stream=s1 if k % 2 == 0 else s2)
+    torch.cuda.synchronize()
+    cache.check()
+    for src, dst in plans:
+        oracle.compact(exp, 2, cache.block_bytes, src, dst)
+    assert np.array_equal(_all_bytes(cache), exp)
+    cache.close()

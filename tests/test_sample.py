@@ -147,3 +147,15 @@ def test_f32_rounding_is_the_only_difference_from_exact_arithmetic():
             disagree += 1
             assert m64 < 1e-4, (t, V, a, b, m64)
     assert disagree < 40
+
+
+def test_vocab_of_two_to_the_24_is_refused():
+    # masses are 2^-40 fixed point summed in 64 bits: a flat row of 2^24
+    # tokens would total 2^64 and wrap, so the call refuses it before any
+    # device work (2^24 - 1 passes validation)
+    import pagedkv
+    from pagedkv import _lib
+    L = pagedkv.lib()
+    rc = L.pkv_sample(None, pagedkv.F32, 1 << 24, 1, 1 << 24, None, 0, 1.0, 42, None, None)
+    assert rc == _lib.PKV_ERR_INVALID
+    assert b"2^24" in L.pkv_last_error(None)
