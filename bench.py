@@ -45,6 +45,25 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: model name, logical CPUs of the
+    machine and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count() or 1, "usable_cpus": usable}
+
+
 def timed_passes(fn, args):
     """Runs fn() at least args.cpu_layers times and for at least
     args.cpu_seconds; returns (seconds per pass, passes, last result)."""
@@ -53,6 +72,59 @@ def timed_passes(fn, args):
         res = fn()
         n += 1
     return (time.time() - t0) / n, n, res
+
+
+def copy_ceiling(dev, cache=None, used=None, gib: int = 2, reps: int = 10) -> dict:
+    """The HBM copy ceiling on this GPU: the faster of a plain device-to-device
+    copy of `gib` GiB (torch copy_, i.e. hipMemcpyAsync) and, given a pool,
+    the library's block-copy kernel moving up to 1,024 blocks (all layers,
+    K and V) from the blocks in `used` into blocks no table references.
+    Both move far more than the 256 MB Infinity Cache; read + written bytes
+    over the average time, HIP events."""
+    import numpy as np
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    n = (gib << 30) // 4
+    src = torch.ones(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    ms = timed(lambda: dst.copy_(src))
+    del src, dst
+    torch.cuda.empty_cache()
+    res = {"GBps": round(2 * (gib << 30) / (ms / 1e3) / 1e9, 1),
+           "method": f"torch copy_ of {gib} GiB (read + write counted), {reps} reps"}
+    if cache is not None:
+        # random (seeded) sources and destinations, as the block churn uses:
+        # a copy between two ranges at a constant offset streams slower
+        # (5.0 against 6.1 TB/s measured), so it would understate the ceiling
+        used = np.unique(np.asarray(used, np.int32))
+        free = np.setdiff1d(np.arange(cache.num_blocks, dtype=np.int32), used)
+        m = int(min(1024, free.size, used.size))
+        if m > 0:
+            rng = np.random.default_rng(7)
+            s_t = torch.from_numpy(rng.permutation(used)[:m].astype(np.int32)).to(dev)
+            d_t = torch.from_numpy(rng.permutation(free)[:m].astype(np.int32)).to(dev)
+            ms_b = timed(lambda: cache.copy_blocks(s_t, d_t))
+            moved = 2 * m * cache.block_bytes * 2 * cache.n_layers
+            gbps_b = moved / (ms_b / 1e3) / 1e9
+            res["copy_blocks_GBps"] = round(gbps_b, 1)
+            res["torch_copy_GBps"] = res["GBps"]
+            res["method"] = (f"max of torch copy_ of {gib} GiB and pkv_copy_blocks of {m} random "
+                             f"blocks x {cache.n_layers} layers K+V into random free blocks "
+                             f"({moved / 1e9:.2f} GB moved), read + write counted, {reps} reps")
+            res["GBps"] = round(max(res["GBps"], gbps_b), 1)
+    return res
 
 
 def timed_steps(step, n, stream):
@@ -80,7 +152,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3",
-                    choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample", "gather"])
+                    choices=sorted(CONFIGS) + ["cfg2", "cfg5", "sample", "gather", "append"])
     ap.add_argument("--rope", action="store_true",
                     help="decode configs and cfg2: q and the new k/v arrive in f32 before the "
                          "rotary embedding, which the decode kernel applies "
@@ -135,6 +207,8 @@ def main() -> int:
         return sample_bench(args, dev)
     if args.config == "gather":
         return gather_bench(args, dev)
+    if args.config == "append":
+        return append_bench(args, dev)
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
     if args.kv_dtype:
@@ -260,6 +334,9 @@ def main() -> int:
     tok_s = B / (ms_step / 1e3)
     gbps_step = bytes_step / (ms_step / 1e3) / 1e9
     gbps_kernel = bytes_launch / (kern_avg_ms / 1e3) / 1e9
+    used_blocks = batch.tables[batch.tables >= 0]
+    ceiling = copy_ceiling(dev, cache, used_blocks)
+    log(f"[bench] copy ceiling: {ceiling['GBps']:.0f} GB/s ({ceiling['method']})")
     log(f"[bench] {ms_step:.3f} ms/step, {tok_s:.0f} tok/s, step {gbps_step:.0f} GB/s, "
         f"decode kernel avg {kern_avg_ms * 1e3:.1f} us over {kern_n} launches ({gbps_kernel:.0f} GB/s)")
 
@@ -303,10 +380,108 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(gbps_kernel / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "kernel": "pkv::decode_kernel",
                      "kernel_avg_us": round(kern_avg_ms * 1e3, 2),
-                     "algorithmic_bytes_per_launch": int(bytes_launch)},
+                     "algorithmic_bytes_per_launch": int(bytes_launch),
+                     "copy_ceiling": ceiling,
+                     "frac_of_copy_ceiling": round(gbps_kernel / ceiling["GBps"], 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    cache.close()
+    return 0
+
+
+def append_bench(args, dev) -> int:
+    """KvPool::write (attention.rs:57-83) at a bandwidth-relevant size on
+    cfg3's layer shape (8 kv heads, hd 128, bf16, bs 16, a 44,256-block
+    pool): 65,536 token rows (256 prompt chunks of 256) scattered to random
+    pool slots by one pkv_append call.  value = GB/s of the K and V rows read
+    and written; bit-exact against the oracle's closed-form write on a
+    sample of rows, untouched rows checked unchanged.  A 512 MiB
+    device-to-device copy of known size runs in the same process as the
+    calibration point of HBM counters."""
+    import numpy as np
+    import torch
+
+    import pagedkv
+    from pagedkv import workload as wl
+
+    KVH, hd, bs, nb, N = 8, 128, 16, 44256, 65536
+    cache = pagedkv.PagedKvCache(1, nb, bs, KVH, hd, torch.bfloat16)
+    cache.fill_normal(args.seed)
+    slots_np = wl.permutation(args.seed ^ 0xA99, nb * bs)[:N].astype(np.int32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    k = torch.randn((N, KVH, hd), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((N, KVH, hd), generator=g, device=dev).to(torch.bfloat16)
+    slots = torch.from_numpy(slots_np).to(dev)
+    before = cache.read_bytes(0, pagedkv.K)
+    pool = cache.layer(0)
+    for _ in range(max(1, args.warmup)):
+        pool.append(k, v, slots)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        pool.append(k, v, slots)
+    e1.record()
+    torch.cuda.synchronize()
+    cache.check()
+    ms = e0.elapsed_time(e1) / args.steps
+    row = KVH * hd * 2
+    gbytes = N * row * 2 * 2   # K and V rows, read and written
+    # calibration copy of known size (its dispatch carries 512 MiB each way)
+    cal_src = torch.ones((512 << 20) // 4, dtype=torch.int32, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+    # bit-exact: the pool equals the oracle's write of the same rows
+    kh = k.cpu().view(torch.int16).numpy().view(np.uint16)
+    vh = v.cpu().view(torch.int16).numpy().view(np.uint16)
+    exp = before.view(np.uint16).reshape(nb * bs, KVH, hd).copy()
+    exp[slots_np] = kh
+    got = cache.read_bytes(0, pagedkv.K).view(np.uint16).reshape(nb * bs, KVH, hd)
+    ok = bool(np.array_equal(got, exp))
+    gotv = cache.read_bytes(0, pagedkv.V).view(np.uint16).reshape(nb * bs, KVH, hd)
+    ok &= bool(np.array_equal(gotv[slots_np], vh))
+    log(f"[bench] append: {N} rows, {ms * 1e3:.1f} us ({gbytes / (ms / 1e3) / 1e9:.0f} GB/s), "
+        f"pool bytes equal the oracle's write: {ok}")
+    if not ok:
+        print(json.dumps({"error": "append differs from the oracle"}))
+        return 1
+    cpu = None
+    if args.cpu_layers > 0:
+        kp = before.view(np.uint16).reshape(nb * bs, KVH, hd).copy()
+        vp = kp.copy()
+
+        def write_all():
+            # the closed form of KvPool::write for these rows: row i to slot
+            # slots[i], K and V, in place (no per-row pool copy)
+            kp[slots_np] = kh
+            vp[slots_np] = vh
+        dt, passes, _ = timed_passes(write_all, args)
+        cpu = {"value": round(gbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "host": host_cpu(),
+               "kind": "port",
+               "sample": (f"numpy scatter of the same {N} K and V rows to their slots (the "
+                          f"closed form of KvPool::write, in place), one thread, {passes} "
+                          f"passes of {dt * 1e3:.1f} ms")}
+    res = {
+        "metric": "KV append (KvPool::write) GB/s, Llama-3-8B layer shape, 1 GPU",
+        "value": round(gbytes / (ms / 1e3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": max(1, args.warmup), "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) rows, random distinct slots)",
+        "config": {"workload": f"append: {N} rows (8 kv heads x hd 128 bf16) to random slots of a "
+                               f"{nb}-block pool, one pkv_append call", "seed": args.seed,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbytes / (ms / 1e3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "pkv::append_kernel", "kernel_avg_us": round(ms * 1e3, 2),
+                     "algorithmic_bytes_per_launch": gbytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
     cache.close()
     return 0
 
@@ -422,7 +597,7 @@ def gather_bench(args, dev) -> int:
             lambda: [oracle.gather_seq(kp, vp, bs, tb[b], int(lens[b]))
                      for b in [next(rows) % B]], args)
         mean_b = gbytes / B
-        cpu = {"value": round(mean_b / per / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+        cpu = {"value": round(mean_b / per / 1e9, 2), "unit": "GB/s", "cores": 1, "host": host_cpu(), "kind": "port",
                "sample": f"oracle gather_seq (closed-form index copy) of one sequence per pass, "
                          f"{n} passes of {per * 1e3:.2f} ms"}
     res = {
@@ -543,7 +718,7 @@ def sample_bench(args, dev) -> int:
         # the reference procedure (sort, f32 softmax, running sum) on host rows
         rows = iter(range(1 << 30))
         per, n, _ = timed_passes(lambda: oracle.sample(x32[next(rows) % B], 0.8), args)
-        cpu = {"value": round(1.0 / per, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+        cpu = {"value": round(1.0 / per, 1), "unit": "rows/s", "cores": 1, "host": host_cpu(), "kind": "port",
                "sample": f"oracle sample() (stable sort + f32 softmax + running sum, as "
                          f"sample.rs) of one {V}-entry row, {n} passes of {per * 1e3:.1f} ms"}
     res = {
@@ -606,7 +781,7 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     agree = bool(np.all(np.abs(gpu0 - res) <= 1e-3 + 2e-2 * np.abs(res)))
     log(f"[bench] cpu baseline: {dt:.2f} s/layer -> {batch.batch / step_s:.1f} tok/s "
         f"(gpu/cpu layer-0 agreement: {agree})")
-    res_cpu = {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads,
+    res_cpu = {"value": round(batch.batch / step_s, 2), "unit": "tok/s", "cores": threads, "host": host_cpu(),
                "kind": "port",
                "sample": (f"layer 0 of the same workload ({batch.batch} seqs, append + attention), "
                           f"{passes} passes of {dt * 1e3:.1f} ms, scaled x{shape.n_layers} layers"),
@@ -626,7 +801,7 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
         log(f"[bench] cpu reference-faithful: {fdt:.2f} s/layer -> "
             f"{batch.batch / fstep:.2f} tok/s")
         res_cpu["reference_faithful"] = {
-            "value": round(batch.batch / fstep, 3), "unit": "tok/s", "cores": 1,
+            "value": round(batch.batch / fstep, 3), "unit": "tok/s", "cores": 1, "host": host_cpu(),
             "kind": "port",
             "sample": (f"layer 0, f32 pool of {kp.size * 4 >> 20} MiB per K, a full K and V pool "
                        f"copy per appended row (slice_assign) then gather/pad/mask/sdpa, "
@@ -898,12 +1073,14 @@ def mix(args, dev) -> int:
         agree = bool(np.all(np.abs(gp - rp) <= 1e-3 + 2e-2 * np.abs(rp))
                      and np.all(np.abs(gd - rd) <= 1e-3 + 2e-2 * np.abs(rd)))
         log(f"[bench] cpu baseline: {dt:.2f} s/layer (gpu/cpu layer-0 agreement: {agree})")
-        cpu = {"value": round((T + ND) / (dt * L), 2), "unit": "tok/s", "cores": threads,
+        cpu = {"value": round((T + ND) / (dt * L), 2), "unit": "tok/s", "cores": threads, "host": host_cpu(),
                "kind": "port",
                "sample": (f"layer 0 of the same mix (chunk store + causal prefill of {NP}x{C}, "
                           f"append + decode of {ND}), {passes} passes of {dt * 1e3:.1f} ms, "
                           f"scaled x{L} layers"),
                "agrees_with_gpu": agree}
+        cpu["reference_faithful"] = mix_faithful(m, tables, kp, vp, (hq, hk, hv), (dq, dk, dv),
+                                                 NP, C, ND, L, sc)
 
     res = {
         "metric": "continuous-batching mix tokens/s (chunked prefill + decode), TinyLlama-1.1B shape, 1 GPU",
@@ -940,6 +1117,62 @@ def mix(args, dev) -> int:
         rope.close()
     cache.close()
     return 0
+
+
+def mix_faithful(m, tables, kp, vp, chunk_rows, decode_rows, NP, C, ND, L, scale):
+    """The reference's own costs for cfg2's layer 0, one thread: f32 pools
+    (its KvPool dtype); every stored row -- the 8 x 256 chunk tokens and the
+    56 decode tokens -- first copies the whole K and V pool (slice_assign,
+    attention.rs:73-80; transformer.rs:173-177 for the prompt); each chunk
+    attends densely, every query over all prior + C keys under an additive
+    causal mask (transformer.rs:139-148,180-196); the decode rows gather, pad,
+    mask and run sdpa (transformer.rs:271-292).  Bounded sample: the chunk
+    attention of all 8 sequences without copies, 16 timed pool copies
+    (scaled to the 2,048 chunk rows), and the decode part with its 56
+    copies; the sum is scaled x22 layers.  A lower bound of the reference:
+    it has no prior-context prefill and would prefill each whole prompt."""
+    import numpy as np
+    import oracle
+    from pagedkv import workload as wl
+
+    kf = wl.widen(kp, wl.F16).astype(np.float32).reshape(kp.shape)
+    vf = wl.widen(vp, wl.F16).astype(np.float32).reshape(vp.shape)
+    hq, hk, hv = (wl.widen(x, wl.F16).astype(np.float32) for x in chunk_rows)
+    dq, dk, dv = (wl.widen(x, wl.F16).astype(np.float32) for x in decode_rows)
+    bs = kp.shape[1]
+    cu = m.cu_q_lens
+    t0 = time.time()
+    for s_ in range(NP):
+        rows = slice(int(cu[s_]), int(cu[s_ + 1]))
+        oracle.prefill_chunk_faithful_f32(kf, vf, bs, tables[s_].astype(np.uint32), int(m.prior[s_]),
+                                          hq[rows], hk[rows], hv[rows], scale, n_copies=0)
+    t_attn = time.time() - t0
+    rows0 = slice(int(cu[0]), int(cu[1]))
+    n_cp = 16
+    t0 = time.time()
+    oracle.prefill_chunk_faithful_f32(kf, vf, bs, tables[0].astype(np.uint32), int(m.prior[0]),
+                                      hq[rows0][:n_cp], hk[rows0][:n_cp], hv[rows0][:n_cp], scale,
+                                      n_copies=n_cp)
+    t_cp16 = time.time() - t0   # 16 pool copies + a 16-query attention
+    t0 = time.time()
+    oracle.prefill_chunk_faithful_f32(kf, vf, bs, tables[0].astype(np.uint32), int(m.prior[0]),
+                                      hq[rows0][:n_cp], hk[rows0][:n_cp], hv[rows0][:n_cp], scale,
+                                      n_copies=0)
+    per_copy = max(0.0, t_cp16 - (time.time() - t0)) / n_cp
+    seq = m.ctx.astype(np.int64)
+    t0 = time.time()
+    oracle.decode_step_faithful_f32(kf, vf, bs, tables[NP:].astype(np.uint32), seq, seq, dq, dk, dv,
+                                    scale)
+    t_dec = time.time() - t0
+    layer_s = t_attn + NP * C * per_copy + t_dec
+    log(f"[bench] cpu reference-faithful: chunk attention {t_attn:.2f} s, pool copy "
+        f"{per_copy * 1e3:.1f} ms x {NP * C}, decode {t_dec:.2f} s -> {layer_s:.1f} s/layer")
+    return {"value": round((NP * C + ND) / (layer_s * L), 4), "unit": "tok/s", "cores": 1,
+            "host": host_cpu(), "kind": "port",
+            "sample": (f"layer 0, f32 pool of {kf.nbytes >> 20} MiB per K: dense masked attention "
+                       f"of the {NP} chunks ({t_attn:.1f} s), {n_cp} full K+V pool copies timed "
+                       f"({per_copy * 1e3:.1f} ms each, x{NP * C} chunk rows), decode of {ND} "
+                       f"rows with their pool copies ({t_dec:.1f} s); scaled x{L} layers")}
 
 
 def churn(args, dev) -> int:
@@ -1132,7 +1365,7 @@ def churn_cpu_baseline(cache, args):
     moved = int((src != dst).sum())
     gbps = 2 * moved * bb * 2 / dt / 1e9
     log(f"[bench] cpu baseline: compaction of {moved} blocks in {dt * 1e3:.1f} ms -> {gbps:.2f} GB/s")
-    return {"value": round(gbps, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(gbps, 2), "unit": "GB/s", "cores": 1, "host": host_cpu(), "kind": "port",
             "sample": (f"closed-form compaction (memcpy) of {moved} of 8192 blocks, 1 layer K+V, "
                        f"{passes} passes of {dt * 1e3:.1f} ms")}
 

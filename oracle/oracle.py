@@ -60,6 +60,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_decode_step_faithful_f32.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _P, _P, _P,
                                                _P, _P, _SZ, _SZ, ctypes.c_float, _P]
     L.orc_decode_step_faithful_f32.restype = ctypes.c_int
+    L.orc_prefill_chunk_faithful_f32.argtypes = [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _SZ,
+                                                 _SZ, _P, _P, _P, _SZ, ctypes.c_float, _P]
+    L.orc_prefill_chunk_faithful_f32.restype = ctypes.c_int
     L.orc_paged_attention_f64.argtypes = [_P, _P, ctypes.c_int, _SZ, _SZ, _SZ, _P, _SZ, _P, _P,
                                           _SZ, _SZ, ctypes.c_double, _P]
     L.orc_paged_attention_f64.restype = None
@@ -210,6 +213,36 @@ def decode_step_faithful_f32(k_pool, v_pool, block_size: int, tables, seq_lens, 
     rc = lib().orc_decode_step_faithful_f32(_p(k_pool), _p(v_pool), NB, block_size, KVH, hd,
                                             _p(tables), tables.shape[1], _p(sl), _p(pos), _p(q),
                                             _p(k_new), _p(v_new), B, H, float(scale), _p(out))
+    if rc:
+        raise IndexError("position beyond block table" if rc == -1 else "allocation failed")
+    return out
+
+
+def prefill_chunk_faithful_f32(k_pool, v_pool, block_size: int, table, prior: int, q, k_new,
+                               v_new, scale: float | None = None,
+                               n_copies: int | None = None) -> np.ndarray:
+    """The reference's cost model for one prompt chunk on f32 pools: a full K
+    and V pool copy before each of the first n_copies token writes (default:
+    every token; slice_assign, attention.rs:73-80), the sequence's rows
+    gathered, dense masked sdpa over all prior + C keys per query
+    (transformer.rs:139-196).  q: (C, H, hd); k_new/v_new: (C, KVH, hd).
+    Pools are modified (the writes).  Returns (C, H*hd)."""
+    assert k_pool.dtype == np.float32 and v_pool.dtype == np.float32
+    NB, KVH, hd = k_pool.shape[0], k_pool.shape[2], k_pool.shape[3]
+    table = np.ascontiguousarray(table, dtype=np.uint32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k_new = np.ascontiguousarray(k_new, dtype=np.float32)
+    v_new = np.ascontiguousarray(v_new, dtype=np.float32)
+    C, H = q.shape[0], q.shape[1]
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    if n_copies is None:
+        n_copies = C
+    out = np.empty((C, H * hd), dtype=np.float32)
+    rc = lib().orc_prefill_chunk_faithful_f32(_p(k_pool), _p(v_pool), NB, block_size, KVH, hd,
+                                              _p(table), table.size, int(prior), C, int(n_copies),
+                                              _p(q), _p(k_new), _p(v_new), H, float(scale),
+                                              _p(out))
     if rc:
         raise IndexError("position beyond block table" if rc == -1 else "allocation failed")
     return out

@@ -317,6 +317,77 @@ int orc_decode_step_faithful_f32(float* k_pool, float* v_pool, size_t num_blocks
     return rc;
 }
 
+/* The reference's cost model for a prompt chunk (CPU baseline variant
+ * "reference-faithful"): C tokens at positions prior .. prior + C - 1 of one
+ * sequence.  prefill_seq stores every token with KvPool::write
+ * (transformer.rs:173-177), whose slice_assign builds a new full pool per
+ * token (attention.rs:73-80): the first n_copies tokens copy the whole K and
+ * V pool before their row is written (the rest are written in place, so a
+ * bounded sample can time the copies apart from the attention).  The
+ * attention is dense as in prefill_seq (transformer.rs:139-148,180-196):
+ * the sequence's prior + C rows gathered from the pool (gather_seq,
+ * attention.rs:85-97), a (C, prior + C) additive mask with -inf at key
+ * j > prior + i, and sdpa over every key of every query row.
+ *   q: (C, H, hd); k_new, v_new: (C, KVH, hd); out: (C, H * hd).
+ * Returns -1 on a position beyond the table, -2 on allocation failure. */
+int orc_prefill_chunk_faithful_f32(float* k_pool, float* v_pool, size_t num_blocks,
+                                   size_t bs, size_t KVH, size_t hd, const uint32_t* table,
+                                   size_t n_table_blocks, size_t prior, size_t C,
+                                   size_t n_copies, const float* q, const float* k_new,
+                                   const float* v_new, size_t H, float scale, float* out) {
+    const size_t bytes = num_blocks * bs * KVH * hd * sizeof(float);
+    const size_t row = KVH * hd, n = prior + C;
+    float* kbuf = n_copies ? (float*)malloc(bytes) : NULL;
+    float* vbuf = n_copies ? (float*)malloc(bytes) : NULL;
+    float* gk = (float*)malloc(sizeof(float) * (n ? n : 1) * row);
+    float* gv = (float*)malloc(sizeof(float) * (n ? n : 1) * row);
+    float* kt = (float*)malloc(sizeof(float) * (n ? n : 1) * row);
+    float* vt = (float*)malloc(sizeof(float) * (n ? n : 1) * row);
+    float* qt = (float*)malloc(sizeof(float) * (C ? C : 1) * H * hd);
+    float* mask = (float*)malloc(sizeof(float) * (C ? C : 1) * (n ? n : 1));
+    int rc = 0;
+    if ((n_copies && (!kbuf || !vbuf)) || !gk || !gv || !kt || !vt || !qt || !mask) rc = -2;
+    float *kc = k_pool, *vc = v_pool, *ko = kbuf, *vo = vbuf;
+    for (size_t i = 0; i < C && rc == 0; i++) {
+        if (i < n_copies) {
+            float* t;
+            memcpy(ko, kc, bytes);
+            t = kc; kc = ko; ko = t;
+            memcpy(vo, vc, bytes);
+            t = vc; vc = vo; vo = t;
+        }
+        rc = orc_kv_write(kc, vc, 4, bs, KVH, hd, table, n_table_blocks, prior + i,
+                          k_new + i * row, v_new + i * row, 1);
+    }
+    if (rc == 0) rc = orc_gather_seq(kc, vc, 4, bs, KVH, hd, table, n_table_blocks, n, gk, gv);
+    if (rc == 0) {
+        /* (n, KVH, hd) -> (KVH, n, hd); q (C, H, hd) -> (H, C, hd) */
+        for (size_t p = 0; p < n; p++)
+            for (size_t g = 0; g < KVH; g++)
+                for (size_t d = 0; d < hd; d++) {
+                    kt[(g * n + p) * hd + d] = gk[(p * KVH + g) * hd + d];
+                    vt[(g * n + p) * hd + d] = gv[(p * KVH + g) * hd + d];
+                }
+        for (size_t i = 0; i < C; i++)
+            for (size_t h = 0; h < H; h++)
+                memcpy(qt + (h * C + i) * hd, q + (i * H + h) * hd, sizeof(float) * hd);
+        for (size_t i = 0; i < C; i++)
+            for (size_t j = 0; j < n; j++) mask[i * n + j] = j > prior + i ? -INFINITY : 0.0f;
+        orc_sdpa_f32(qt, kt, vt, mask, 1, H, KVH, C, n, hd, scale, out);
+    }
+    if (kc != k_pool) memcpy(k_pool, kc, bytes);
+    if (vc != v_pool) memcpy(v_pool, vc, bytes);
+    free(kbuf);
+    free(vbuf);
+    free(gk);
+    free(gv);
+    free(kt);
+    free(vt);
+    free(qt);
+    free(mask);
+    return rc;
+}
+
 /* Closed form in fp64: paged decode attention straight off the block tables,
  * ragged (no padding).  For every (b, h): keys p = 0..ctx_lens[b]-1 at slot
  * tables[b][p/bs]*bs + p%bs, kv head h / (H/KVH), s_p = scale * q.k_p,

@@ -261,6 +261,32 @@ def test_decode_step_faithful_equals_in_place():
     assert np.array_equal(kp, k2) and np.array_equal(vp, v2)
 
 
+def test_prefill_chunk_faithful_matches_closed_form():
+    # the reference's cost model for a chunk (full pool copy per token, dense
+    # masked attention over all prior + C keys): the same pool bytes as the
+    # plain writes, outputs equal to the fp64 closed form, and with no prior
+    # the reference's prefill_seq attention
+    H, KVH, hd, bs = 14, 2, 16, 16
+    for P, C, copies in ((29, 21, None), (0, 37, 5), (40, 1, 0)):
+        tb, kp, vp, q = _prefill_setup(61 + P, P, C, H, KVH, hd, bs)
+        rng = np.random.default_rng(P + C)
+        kn = rng.standard_normal((C, KVH, hd)).astype(np.float32)
+        vn = rng.standard_normal((C, KVH, hd)).astype(np.float32)
+        k2, v2 = kp.copy(), vp.copy()
+        got = oracle.prefill_chunk_faithful_f32(kp, vp, bs, tb, P, q[P:], kn, vn,
+                                                n_copies=copies)
+        oracle.kv_write(k2, v2, bs, tb, P, kn, vn)
+        assert np.array_equal(kp, k2) and np.array_equal(vp, v2)
+        ref = oracle.prefill_attention_f64(kp, vp, wl.F32, bs, tb[None], [0, C], [P + C], q[P:],
+                                           1 / math.sqrt(hd))
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+        if P == 0:
+            gk, gv = oracle.gather_seq(kp, vp, bs, tb, C)
+            seq = oracle.prefill_seq_f32(q.transpose(1, 0, 2), gk.transpose(1, 0, 2),
+                                         gv.transpose(1, 0, 2), KVH)
+            np.testing.assert_allclose(got, seq, rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("H,KVH", [(8, 2), (14, 2), (6, 2), (21, 3)])
 def test_paged_attention_f64_matches_torch_on_gathered(H, KVH):
     B, hd, bs = 3, 16, 16
