@@ -130,6 +130,9 @@ struct DecodeKArgs {
   int rtot;
   int h0;
   int store_new;  // 1: the launch stores k_new / v_new into the pool
+  // 1: wave item -> (sequence, partition) by arithmetic, every sequence
+  // given max_parts slots (small launches); 0: the longest-first work list.
+  int direct;
 };
 
 // N elements of a row, from f32 or 16-bit storage, as floats.
@@ -337,24 +340,54 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int lane = threadIdx.x & 63;
   float* p_lds = p_lds_all[wave];
 
-  const int ncache = min(a.batch, kCtxCache);
-  for (int i = threadIdx.x; i < ncache; i += kWavesPerBlock * kWave) ctx_lds[i] = a.context_lens[i];
-  __syncthreads();
-  const CtxLens cl{a.context_lens, ctx_lds, ncache};
-
   const int H = a.kvh * a.rtot;
   const int rq = a.rq;  // query heads of this launch per group (<= R)
   const int BS = 1 << a.bs_log2;
+  const int PT = a.part_tokens;
   const long long item = (long long)blockIdx.x * kWavesPerBlock + wave;
   const int g = (int)(item % a.kvh);
   int b = 0, p = 0;
-  if (!locate_pair(a, cl, item / a.kvh, lane, BS, b, p)) return;
+  CtxLens cl{a.context_lens, ctx_lds, 0};
+  if (a.direct) {  // launch-uniform
+    // Small launches: (b, p) straight from the item, so the wave issues its
+    // context length, table slice and Q loads at once (no staging round
+    // trip); slots past a sequence's partitions exit below.
+    const long long rest = item / a.kvh;
+    b = (int)(rest / a.max_parts);
+    p = (int)(rest - (long long)b * a.max_parts);
+    if (b >= a.batch) return;
+  } else {
+    cl.n = min(a.batch, kCtxCache);
+    for (int i = threadIdx.x; i < cl.n; i += kWavesPerBlock * kWave) ctx_lds[i] = a.context_lens[i];
+    __syncthreads();
+    if (!locate_pair(a, cl, item / a.kvh, lane, BS, b, p)) return;
+  }
+
+  const int G = lane >> 4;
+  const int col = lane & 15;
+  const int t_begin = p * PT;
+  const int blk_begin = t_begin >> a.bs_log2;
+  // Loads that do not depend on the context length go out first: the block
+  // ids a full partition spans (partitions are block-aligned and span at
+  // most 64 blocks, decode_plan; lane i holds entry blk_begin + i, ids past
+  // the sequence's blocks are never used) and, without RoPE, the Q group as
+  // the MFMA A operand (row = head lane % 16, k-slice lane / 16).
+  const int span = PT >> a.bs_log2 > 1 ? PT >> a.bs_log2 : 1;
+  int tbl = 0;
+  if (lane < span && blk_begin + lane < a.mbps)
+    tbl = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
+  u32x4 qf[C::NF];
+  if constexpr (!ROPE) {
+    const char* qrow = a.q + ((size_t)b * H + g * a.rtot + a.h0 + (col < rq ? col : 0)) * C::RB;
+#pragma unroll
+    for (int f = 0; f < C::NF; ++f)
+      qf[f] = col < rq ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
+  }
 
   const int ctx_raw = cl[b];
   const int ctx = clamp_ctx(a, ctx_raw, BS);
   const bool clamped = ctx != ctx_raw;
-  if (clamped && lane == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
-  const int PT = a.part_tokens;
+  if (clamped && lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
   const int n_parts = (ctx + PT - 1) / PT;
   const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
   const int tg = lane / C::CH;  // token group of a V load
@@ -374,21 +407,10 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   }
   if (p >= n_parts) return;
 
-  const int t_begin = p * PT;
   const int t_end = min(ctx, t_begin + PT);
-  const int blk_begin = t_begin >> a.bs_log2;
-  const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= 64 (plan)
+  const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= span
   const int new_pos = (a.k_new != nullptr && !clamped) ? ctx - 1 : -1;
 
-  const int G = lane >> 4;
-  const int col = lane & 15;
-
-  // Prologue loads are issued together: the block-table slice of this
-  // partition (lane i holds entry blk_begin + i) and the Q group as the MFMA
-  // A operand (row = head lane % 16, k-slice lane / 16).
-  int tbl = 0;
-  if (lane < nblk) tbl = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
-  u32x4 qf[C::NF];
   int rpos = 0;  // RoPE position of this sequence's new token
   if constexpr (ROPE) {
     // Rotate Q in the kernel (transformer.rs:252-269).  Fragment f of a lane
@@ -415,11 +437,6 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       qf[f] = col < rq ? pack16<DT, C::EPL>(x1) : u32x4{0, 0, 0, 0};
       qf[f + C::NF / 2] = col < rq ? pack16<DT, C::EPL>(x2) : u32x4{0, 0, 0, 0};
     }
-  } else {
-    const char* qrow = a.q + ((size_t)b * H + g * a.rtot + a.h0 + (col < rq ? col : 0)) * C::RB;
-#pragma unroll
-    for (int f = 0; f < C::NF; ++f)
-      qf[f] = col < rq ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
   }
   if (lane < nblk && (tbl < 0 || tbl >= a.num_blocks)) {
     atomicOr(a.err, PKV_EBIT_BLOCK);
@@ -704,13 +721,19 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 // Merge of the partitions of (b, g) for sequences with more than one
 // partition: M = max_p m_p, L = sum_p l_p 2^(m_p - M),
 // O = sum_p O_p 2^(m_p - M) / L (all in the exp2 domain of the main kernel).
-// One wave per query head (b, g, h).  The partitions are read in parallel:
-// (m, l) with one partition per lane, the partial rows O_p as 16-byte chunks
-// with HD / 4 lanes per row and 64 / (HD / 4) rows per load instruction,
-// kMergeUnroll instructions in flight per lane; the row groups are summed
-// with lane shuffles at the end.  Context clamping is identical to the main
-// kernel.
-constexpr int kMergeUnroll = 4;
+// One wave per query head (b, g, h).  The first loads go out together,
+// before the context length that says how many partitions there are has
+// arrived: the (m, l) pairs of partitions 0..63 (one per lane) and the first
+// PPI * MU partial rows O_p (16-byte chunks, HD / 4 lanes per row,
+// 64 / (HD / 4) rows per load instruction), all within the launch's
+// max_parts slots of the pair; entries of partitions the sequence does not
+// have are masked out once the length is known.  Longer sequences load the
+// rest in further rounds.  The row groups are summed with lane shuffles at
+// the end.  Context clamping is identical to the main kernel.
+// Row loads in flight per lane: 8 for rows of 64 (32 partitions per round,
+// which covers the small launches of short rows), else 4 (8 or 16 rows).
+template <int HD>
+constexpr int merge_unroll() { return HD == 64 ? 8 : 4; }
 
 __device__ __forceinline__ float wave_max_f(float x) {
 #pragma unroll
@@ -730,6 +753,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   // heads h < a.rq of each group are merged.
   constexpr int LPR = HD / 4;      // lanes per partial row (16 B each)
   constexpr int PPI = kWave / LPR; // partial rows per load instruction
+  constexpr int kMergeUnroll = merge_unroll<HD>();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const long long qh = (long long)blockIdx.x * kWavesPerBlock + wave;  // (b, g, h)
@@ -739,35 +763,51 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int b = (int)(pair / a.kvh);
   const int g = (int)(pair % a.kvh);
   const int BS = 1 << a.bs_log2;
-  const int ctx = clamp_ctx(a, a.context_lens[b], BS);
-  const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
-  if (n_parts <= 1) return;
   const size_t pstride_ml = (size_t)R * 2;   // floats between partitions
   const size_t pstride_o = (size_t)R * HD;
   const float* mlb = a.part_ml + (size_t)pair * a.max_parts * pstride_ml + 2 * h;
   const int q = lane / LPR;  // row group
   const int c = lane % LPR;  // 16-byte chunk of the row
   const float* pob = a.part_o + ((size_t)pair * a.max_parts * R + h) * HD + 4 * c;
+  const int mp = a.max_parts;
 
-  // The first PPI * kMergeUnroll partial rows are loaded together with the
-  // (m, l) pairs, before the reductions that weight them: one memory round
-  // trip for the partition counts of small launches instead of two.
+  const int ctx_raw = a.context_lens[b];
+  float m0 = -INFINITY, l0 = 0.0f;  // partition `lane`
+  if (lane < mp) {
+    m0 = mlb[(size_t)lane * pstride_ml];
+    l0 = mlb[(size_t)lane * pstride_ml + 1];
+  }
   f32x4 ov0[kMergeUnroll];
   float mv0[kMergeUnroll];
 #pragma unroll
   for (int u = 0; u < kMergeUnroll; ++u) {
     const int pp = u * PPI + q;
-    const bool ok = pp < n_parts;
+    const bool ok = pp < mp;
     ov0[u] = ok ? *reinterpret_cast<const f32x4*>(pob + (size_t)pp * pstride_o)
                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     mv0[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
   }
-  float M = -INFINITY;
-  for (int p0 = 0; p0 < n_parts; p0 += kWave)
+  const int ctx = clamp_ctx(a, ctx_raw, BS);
+  const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  if (n_parts <= 1) return;
+  // entries of partitions past n_parts hold whatever the slots held: select,
+  // never multiply, them away
+  if (lane >= n_parts) {
+    m0 = -INFINITY;
+    l0 = 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kMergeUnroll; ++u)
+    if (u * PPI + q >= n_parts) {
+      ov0[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      mv0[u] = -INFINITY;
+    }
+  float M = m0;
+  for (int p0 = kWave; p0 < n_parts; p0 += kWave)
     if (p0 + lane < n_parts) M = fmaxf(M, mlb[(size_t)(p0 + lane) * pstride_ml]);
   M = wave_max_f(M);
-  float L = 0.0f;
-  for (int p0 = 0; p0 < n_parts; p0 += kWave) {
+  float L = lane < n_parts ? fast_exp2(m0 - M) * l0 : 0.0f;
+  for (int p0 = kWave; p0 < n_parts; p0 += kWave) {
     const int pp = p0 + lane;
     if (pp < n_parts) {
       const float* e = mlb + (size_t)pp * pstride_ml;
@@ -863,6 +903,12 @@ hipError_t launch_hd(int HD, int R, const DecodeKArgs& k, long long items, hipSt
   }
 }
 
+// Launches of at most this many (sequence, kv head, partition) slots map
+// waves to items directly instead of through the longest-first work list:
+// they fit on the GPU at once, so dispatch order buys nothing, and the
+// direct mapping saves the context-length staging round trip.
+constexpr long long kDirectMaxItems = 2048;
+
 int ilog2i(int x) {
   int r = 0;
   while ((1 << r) < x) ++r;
@@ -945,6 +991,8 @@ hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a, char
   k.positions = a.positions;
   k.in_f32 = a.in_f32;
   k.rtot = rtot;
+  // small launches (every wave resident at once): direct wave mapping
+  k.direct = (long long)pairs * mp <= kDirectMaxItems;
   size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   k.part_ml = reinterpret_cast<float*>(partials);
   k.part_o = reinterpret_cast<float*>(partials + ml_bytes);
