@@ -84,7 +84,12 @@ const char* pkv_last_error(const pkv_pool* pool);
  *    its tests is 16 (app.rs:701, tests/paged_parity.rs:33).
  * n_kv_head is any positive count; the GQA ratio n_head / n_kv_head of the
  * attention calls is any positive integer (repeat_kv, attention.rs:113,
- * 128-136).  The pool is plain device memory from hipMalloc. */
+ * 128-136).  The pool is plain device memory from hipMalloc, allocated by
+ * the library itself.  No kernel loads pool bytes that the same launch
+ * stored (the fused appends hand the new rows to the attention through
+ * LDS; a launch's copies and moves read each block before any write to it,
+ * in the same thread), so results do not depend on the pool's caching
+ * or coherence attributes. */
 int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
                     int block_size, int n_kv_head, int head_dim, int dtype,
                     int device);
