@@ -273,6 +273,9 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   }
   p->plan = static_cast<char*>(dplan);
   p->plan_host = static_cast<char*>(hplan);
+  // Compute units: the prefill kernel pairs its workgroups per CU.
+  if (hipDeviceGetAttribute(&p->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    p->n_cu = 0;
   // This device's copy of the static scratch of pkv_decode_attention_noalloc
   // (looked up once per device, with the device current).
   e = pkv::noalloc_scratch(device, &p->scratch);

@@ -36,6 +36,8 @@ struct pkv_pool {
   // this device's copy of the static scratch array of
   // pkv_decode_attention_noalloc (looked up at pool creation)
   char* scratch = nullptr;
+  // compute units of the device (workgroup placement of the prefill kernel)
+  int n_cu = 0;
   // compaction plan (chains of block moves), kept between calls: device
   // buffer and its pinned host staging copy
   char* plan = nullptr;

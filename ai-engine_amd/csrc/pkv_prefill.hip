@@ -30,8 +30,12 @@
 //
 // Workgroups are mapped XCD-aware: with at least 8 (sequence, kv head) pairs,
 // XCD x (= blockIdx % 8) serves the pairs congruent to x mod 8, so the row
-// blocks that share a pair's K/V share one L2; row blocks are dispatched
-// longest (last) first.
+// blocks that share a pair's K/V share one L2.  Within an XCD the pairs run
+// longest context first, each pair's row blocks last (longest) first, and
+// the second round of workgroups per CU runs in reverse order, so the CU
+// that holds a heavy workgroup gets a light one beside it; a workgroup's
+// time is its chain of key tiles, and the older workgroup of a CU issues
+// first.
 #include <type_traits>
 
 #include "pkv_device.h"
@@ -122,6 +126,7 @@ struct PrefillKArgs {
   int part_keys;   // keys per part: a multiple of two tiles
   int max_parts;   // parts per row block at most (1 + (max_context_len - 1) / part_keys)
   int per_xcd;     // workgroup slots per XCD (affinity mapping), 0 = plain order
+  int cpx;         // compute units per XCD (pairing of the affinity mapping), 0 = none
   int rq;          // GQA ratio n_head / n_kv_head (kernels built for a fixed ratio ignore it)
   float scale_log2;
   float* part_ml;  // split key ranges: (m, l) per (item, row)
@@ -191,14 +196,51 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const int n_sg = a.n_seqs * a.kvh;
   const int rbp = a.row_blocks * a.max_parts;
   int sg, rb, part;
+  int q0 = 0, q1 = 0, ctx = 0;  // cu_q_lens[s], cu_q_lens[s + 1], context_lens[s]
+  bool have_lens = false;
   {
     int u;
     if (a.per_xcd > 0) {
-      const int x = blockIdx.x % kXcd, slot = blockIdx.x / kXcd;
+      const int x = blockIdx.x % kXcd;
+      int slot = blockIdx.x / kXcd;
       const int nx = (n_sg - x + kXcd - 1) / kXcd;  // pairs of this XCD
       if (slot >= nx * rbp) return;
-      u = slot / nx;
-      sg = x + kXcd * (slot % nx);
+      if (nx <= 64) {
+        // Heaviest first, paired per CU.  The XCD's pairs are ranked by
+        // context length (the key count of their last row; ties by index)
+        // and their items taken pair-major, last row block first.  The
+        // XCD's workgroups fill its CUs in rounds of cpx (one per CU per
+        // round); every other full round runs in reverse, so a CU holding
+        // the k-th heaviest item of one round holds the k-th lightest of
+        // the next.  A CU's older workgroup issues first, and here it is
+        // the heavier one.
+        if (a.cpx > 0) {
+          const int round = slot / a.cpx;
+          if ((round & 1) && (round + 1) * a.cpx <= nx * rbp)
+            slot = round * a.cpx + (a.cpx - 1 - slot % a.cpx);
+        }
+        // lane j: the j-th pair of the XCD, with its sequence's lengths
+        const int ln = threadIdx.x & 63;
+        const int sj = ln < nx ? (x + kXcd * ln) / a.kvh : 0;
+        const int w = ln < nx ? a.context_lens[sj] : -1;
+        const int c0 = a.cu_q_lens[sj], c1 = a.cu_q_lens[sj + 1];
+        int rank = 0;
+        for (int j = 0; j < nx; ++j) {
+          const int wj = __builtin_amdgcn_readlane(w, j);
+          rank += (wj > w) | ((wj == w) & (j < ln));
+        }
+        const int want = slot / rbp;
+        const int jw = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(ln < nx && rank == want));
+        sg = x + kXcd * jw;
+        ctx = __builtin_amdgcn_readlane(w, jw);
+        q0 = __builtin_amdgcn_readlane(c0, jw);
+        q1 = __builtin_amdgcn_readlane(c1, jw);
+        have_lens = true;
+        u = slot % rbp;
+      } else {
+        u = slot / nx;
+        sg = x + kXcd * (slot % nx);
+      }
     } else {
       if ((int)blockIdx.x >= n_sg * rbp) return;
       u = (int)blockIdx.x / n_sg;
@@ -210,13 +252,16 @@ __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   const int g = sg % a.kvh;
   const int s = sg / a.kvh;
 
-  const int q0 = a.cu_q_lens[s];
-  const int q_len_raw = a.cu_q_lens[s + 1] - q0;
+  if (!have_lens) {
+    q0 = a.cu_q_lens[s];
+    q1 = a.cu_q_lens[s + 1];
+    ctx = a.context_lens[s];
+  }
+  const int q_len_raw = q1 - q0;
   const int q_len = min(q_len_raw, a.max_q_len);
   const bool reporter = tid == 0 && rb == 0 && g == 0;
   if (q_len_raw > a.max_q_len && reporter) atomicOr(a.err, PKV_EBIT_LENGTH);
   const int BS = 1 << a.bs_log2;
-  const int ctx = a.context_lens[s];
   if (ctx > a.max_context_len || ctx > a.mbps * BS || ctx < q_len || q_len < 0) {
     if (reporter) atomicOr(a.err, PKV_EBIT_LENGTH);
     return;
@@ -887,6 +932,7 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
   k.k_new = reinterpret_cast<const char*>(a.k_new);
   k.v_new = reinterpret_cast<const char*>(a.v_new);
   k.rq = a.n_head / p->n_kv_head;
+  k.cpx = p->n_cu >= kXcd && p->n_cu % kXcd == 0 ? p->n_cu / kXcd : 0;
   size_t ws = 0;
   prefill_plan(p, a.n_seqs, a.n_head, a.max_q_len, a.max_context_len, &k.part_keys,
                &k.max_parts, &ws);
