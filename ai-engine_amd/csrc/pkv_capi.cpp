@@ -71,37 +71,32 @@ int check_layer(pkv_pool* p, int layer) {
 }
 
 // Ensure the pool workspace (split-context partials of decode and of split
-// prefill; calls on the pool's stream use it in turn) holds `counter_bytes`
-// of counters followed by `total - counter_bytes` of partials.  Counters are zeroed on (re)allocation
-// and the kernels leave them zero.
-int ensure_workspace(pkv_pool* p, size_t total, size_t counter_bytes) {
-  size_t part_need = total - counter_bytes;
-  size_t part_have = p->ws_bytes - p->ws_counter_bytes;
-  if (p->ws && p->ws_counter_bytes >= counter_bytes && part_have >= part_need)
-    return PKV_OK;
-  size_t cb = std::max(counter_bytes, p->ws_counter_bytes);
-  size_t pb = std::max(part_need, part_have);
-  size_t bytes = cb + pb + pb / 4;  // headroom against regrowth
-  if (p->ws) {
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return hip_fail(p, e, "hipDeviceSynchronize");
-    (void)hipFree(p->ws);
-    p->ws = nullptr;
-    p->ws_bytes = p->ws_counter_bytes = 0;
-  }
+// prefill; calls on the pool's stream use it in turn) holds `bytes`.  Growth
+// never waits for the device: work already queued on any stream may still
+// read the old buffer, so it is retired rather than freed (hipFree would
+// block until the device is idle) and released by pkv_pool_destroy or by an
+// explicit reserve call, both of which synchronise anyway.
+int ensure_workspace(pkv_pool* p, size_t need) {
+  if (p->ws && p->ws_bytes >= need) return PKV_OK;
+  const size_t bytes = need + need / 4;  // headroom against regrowth
   void* ws = nullptr;
   hipError_t e = hipMalloc(&ws, bytes);
   if (e != hipSuccess)
-    return fail(p, PKV_ERR_OOM, "workspace hipMalloc(%zu): %s", bytes,
-                hipGetErrorString(e));
-  e = hipMemset(ws, 0, cb);
-  if (e != hipSuccess) {
-    (void)hipFree(ws);
-    return hip_fail(p, e, "hipMemset(workspace counters)");
-  }
+    return fail(p, PKV_ERR_OOM, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  if (p->ws) p->ws_retired.push_back(p->ws);
   p->ws = static_cast<char*>(ws);
   p->ws_bytes = bytes;
-  p->ws_counter_bytes = cb;
+  return PKV_OK;
+}
+
+// Frees retired workspaces once the device has finished with them (the
+// explicit, synchronous reserve calls).
+int release_retired(pkv_pool* p) {
+  if (p->ws_retired.empty()) return PKV_OK;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(p, e, "hipDeviceSynchronize");
+  for (char* r : p->ws_retired) (void)hipFree(r);
+  p->ws_retired.clear();
   return PKV_OK;
 }
 
@@ -300,6 +295,7 @@ int pkv_pool_destroy(pkv_pool* p) {
   if (p->base) (void)hipFree(p->base);
   if (p->err) (void)hipFree(p->err);
   if (p->ws) (void)hipFree(p->ws);
+  for (char* r : p->ws_retired) (void)hipFree(r);
   if (p->plan) (void)hipFree(p->plan);
   if (p->plan_host) (void)hipHostFree(p->plan_host);
   if (p->plan_uploaded) (void)hipEventDestroy(p->plan_uploaded);
@@ -582,7 +578,7 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
 
 size_t pkv_decode_workspace_bytes(const pkv_pool* p, int batch, int n_head, int max_context_len) {
   if (!p || batch <= 0 || n_head <= 0) return 0;
-  return pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, nullptr);
+  return pkv::decode_workspace_bytes(p, batch, n_head, max_context_len);
 }
 
 int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_len) {
@@ -591,9 +587,8 @@ int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_
     return fail(p, PKV_ERR_INVALID, "reserve_decode: bad shape (batch %d, n_head %d, max_context_len %d)",
                 batch, n_head, max_context_len);
   DeviceGuard dg(p->device);
-  size_t cb = 0;
-  size_t need = pkv::decode_workspace_bytes(p, batch, n_head, max_context_len, &cb);
-  return ensure_workspace(p, need, cb);
+  if (int rc = release_retired(p)) return rc;
+  return ensure_workspace(p, pkv::decode_workspace_bytes(p, batch, n_head, max_context_len));
 }
 
 // Timing events for the next attention call's main kernel when profiling is
@@ -640,8 +635,7 @@ static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   if (!(a.scale == a.scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
   DeviceGuard dg(p->device);
-  size_t cb = 0;
-  size_t need = pkv::decode_workspace_bytes(p, a.batch, a.n_head, a.max_context_len, &cb);
+  size_t need = pkv::decode_workspace_bytes(p, a.batch, a.n_head, a.max_context_len);
   if (noalloc) {
     if (need > pkv::noalloc_scratch_bytes())
       return fail(p, PKV_ERR_UNSUPPORTED,
@@ -653,10 +647,10 @@ static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
     if (e != hipSuccess) return hip_fail(p, e, "decode_noalloc launch");
     return PKV_OK;
   }
-  if (int rc = ensure_workspace(p, need, cb)) return rc;
+  if (int rc = ensure_workspace(p, need)) return rc;
   hipEvent_t eb = nullptr, ee = nullptr;
   if (int rc = profile_slot(p, &eb, &ee)) return rc;
-  hipError_t e = pkv::launch_decode(p, layer, a, p->ws + p->ws_counter_bytes,
+  hipError_t e = pkv::launch_decode(p, layer, a, p->ws,
                                     static_cast<hipStream_t>(stream), eb, ee);
   if (e != hipSuccess) return hip_fail(p, e, "decode launch");
   return PKV_OK;
@@ -743,7 +737,7 @@ int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype
     size_t need = 0;
     pkv::prefill_plan(p, n_seqs, n_head, max_q_len, max_context_len, &pk, &mp, &need);
     if (need)
-      if (int rc = ensure_workspace(p, p->ws_counter_bytes + need, p->ws_counter_bytes)) return rc;
+      if (int rc = ensure_workspace(p, need)) return rc;
   }
   pkv::PrefillArgs a{q, out, out_dtype, cu_q_lens, context_lens, block_tables,
                      max_blocks_per_seq, n_seqs, max_q_len, max_context_len, n_head, scale,
@@ -796,7 +790,8 @@ int pkv_pool_reserve_prefill(pkv_pool* p, int n_seqs, int n_head, int max_q_len,
   size_t need = pkv_prefill_workspace_bytes(p, n_seqs, n_head, max_q_len, max_context_len);
   if (!need) return PKV_OK;
   DeviceGuard dg(p->device);
-  return ensure_workspace(p, p->ws_counter_bytes + need, p->ws_counter_bytes);
+  if (int rc = release_retired(p)) return rc;
+  return ensure_workspace(p, need);
 }
 
 int pkv_pool_profile(pkv_pool* p, int enable) {
@@ -948,6 +943,42 @@ int pkv_sample(const void* logits, int dtype, long long row_stride, int batch, i
                                     top_k, top_p, pkv::sample_draw(seed), tokens,
                                     static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(nullptr, e, "sample launch");
+  return PKV_OK;
+}
+
+int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch, int vocab,
+                     const float* temperatures, int top_k, float top_p, uint64_t seed,
+                     int32_t* tokens, void* stream) {
+  if (batch < 0 || vocab < 0 || vocab >= (1 << 24))
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: batch %d, vocab %d (0 .. 2^24 - 1)",
+                batch, vocab);
+  if (batch == 0) return PKV_OK;
+  if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: dtype %d", dtype);
+  if (!tokens || (vocab > 0 && !logits))
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: NULL logits or tokens");
+  if (batch > 1 && row_stride < vocab)
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: row_stride %lld < vocab %d", row_stride,
+                vocab);
+  if (reinterpret_cast<uintptr_t>(logits) % pkv::dtype_bytes(dtype))
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: logits not aligned to the element size");
+  if ((reinterpret_cast<uintptr_t>(temperatures) | reinterpret_cast<uintptr_t>(tokens)) % 4)
+    return fail(nullptr, PKV_ERR_INVALID,
+                "sample_exact: temperatures and tokens must be 4-byte aligned");
+  if (top_k < 0)
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact: top_k %d < 0 (0 is None)", top_k);
+  hipError_t e = pkv::launch_sample_exact(logits, dtype, row_stride, batch, vocab, temperatures,
+                                          top_k, top_p, pkv::sample_draw(seed), tokens,
+                                          static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(nullptr, e, "sample_exact launch");
+  return PKV_OK;
+}
+
+int pkv_sample_expf(const float* in, float* out, long long n, void* stream) {
+  if (n < 0 || (n > 0 && (!in || !out)))
+    return fail(nullptr, PKV_ERR_INVALID, "sample_expf: n %lld, NULL pointer", n);
+  hipError_t e = pkv::launch_expf_glibc(in, out, n, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(nullptr, e, "sample_expf launch");
   return PKV_OK;
 }
 

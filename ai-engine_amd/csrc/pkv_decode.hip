@@ -946,17 +946,15 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
 }
 
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
-                              int max_context_len, size_t* counter_bytes) {
+                              int max_context_len) {
   int pt = 0, mp = 0;
   decode_plan(p, batch, n_head, max_context_len, &pt, &mp);
   size_t pairs = (size_t)batch * p->n_kv_head;
   size_t R = (size_t)group_width(n_head / p->n_kv_head);  // partial heads per partition
-  size_t cb = 0;  // no counters: the merge is a separate kernel
-  if (counter_bytes) *counter_bytes = cb;
   if (mp <= 1) return 256;
   size_t ml = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
   size_t po = pairs * mp * R * (size_t)p->head_dim * 4;
-  return cb + ml + po;
+  return ml + po;
 }
 
 hipError_t launch_decode(const pkv_pool* p, int layer, const DecodeArgs& a, char* partials,

@@ -28,11 +28,12 @@ struct pkv_pool {
   size_t layer_bytes = 0;  // one layer's K (or V): num_blocks * block_bytes
   char* base = nullptr;    // device slab
   uint32_t* err = nullptr; // device error word, bit set by kernels
-  // decode workspace: split-context partials (m, l, O); ws_counter_bytes is
-  // a reserved prefix (0 in this version)
+  // workspace: split-context partials (m, l, O) of decode and split prefill;
+  // buffers replaced by a larger one wait in ws_retired until the device is
+  // known to be done with them
   char* ws = nullptr;
   size_t ws_bytes = 0;
-  size_t ws_counter_bytes = 0;
+  std::vector<char*> ws_retired;
   // this device's copy of the static scratch array of
   // pkv_decode_attention_noalloc (looked up at pool creation)
   char* scratch = nullptr;
@@ -89,6 +90,12 @@ float sample_draw(uint64_t seed);
 hipError_t launch_sample(const void* logits, int dtype, long long row_stride, int batch,
                          int vocab, const float* temperatures, int top_k, float top_p,
                          float r, int32_t* tokens, hipStream_t stream);
+// The bit-exact variant (the reference's f32 arithmetic; top_p NaN = None),
+// and the exp it uses.
+hipError_t launch_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
+                               int vocab, const float* temperatures, int top_k, float top_p,
+                               float r, int32_t* tokens, hipStream_t stream);
+hipError_t launch_expf_glibc(const float* in, float* out, long long n, hipStream_t stream);
 
 // Launchers (defined in the .hip files).  They validate nothing that the
 // C-ABI layer already validated, return hipError_t and enqueue on `stream`.
@@ -154,7 +161,7 @@ struct DecodeArgs {
 void decode_plan(const pkv_pool* p, int batch, int n_head,
                  int max_context_len, int* part_tokens, int* max_parts);
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
-                              int max_context_len, size_t* counter_bytes);
+                              int max_context_len);
 bool decode_supported(const pkv_pool* p, int n_head);
 // The split-context partials go to `partials` (decode_workspace_bytes of the
 // launch).  ev_begin / ev_end (may be null) are recorded on `stream` right

@@ -938,14 +938,14 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
                &k.max_parts, &ws);
   if (k.max_parts > 1) {
     // the split's partials live in the pool workspace (sized by the caller)
-    if (!p->ws || p->ws_bytes - p->ws_counter_bytes < ws) return hipErrorInvalidValue;
+    if (!p->ws || p->ws_bytes < ws) return hipErrorInvalidValue;
     int kt = 0, rows = 0;
     prefill_shape(p->dtype, p->head_dim, &kt, &rows);
     const int R = a.n_head / p->n_kv_head;
     const size_t n = (size_t)a.n_seqs * p->n_kv_head *
                      (((size_t)a.max_q_len * R + rows - 1) / rows) * k.max_parts * rows;
-    k.part_ml = reinterpret_cast<float*>(p->ws + p->ws_counter_bytes);
-    k.part_o = reinterpret_cast<float*>(p->ws + p->ws_counter_bytes + ((n * 2 * 4 + 255) / 256) * 256);
+    k.part_ml = reinterpret_cast<float*>(p->ws);
+    k.part_o = reinterpret_cast<float*>(p->ws + ((n * 2 * 4 + 255) / 256) * 256);
   }
   int R = a.n_head / p->n_kv_head;
   hipError_t e = hipSuccess;

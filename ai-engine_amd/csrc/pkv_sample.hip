@@ -865,6 +865,431 @@ __global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs
   if (tid == 0) a.tokens[row] = tok;
 }
 
+// ---- bit-exact sample(): the reference's own f32 arithmetic -----------------
+// sample.rs:16-47 sorts y = x / T (stable, descending), keeps the first
+// top_k, takes p_i = (y_i - max).exp() with f32::exp, adds the p_i in sorted
+// order in f32, divides each by that sum, (top_p: adds them again in f32
+// until the running sum reaches top_p, truncates there and divides by the
+// truncated sum), and returns the first token at which the f32 running sum
+// reaches r.  sample_exact_kernel reproduces every one of those values bit
+// for bit, so the token is the reference's on every input, including rows
+// where f32 rounding alone moves the pick:
+//  * exp: f32::exp is the C library's expf on the reference's host (on
+//    x86-64 Linux, glibc).  expf_glibc restates glibc's expf (the algorithm
+//    of Arm's Optimized Routines, glibc >= 2.28, as built for x86-64 with
+//    FMA); it was checked against the host libm on every float <= 0, the
+//    only arguments it gets here (y - max <= 0).
+//  * order: a stable LSD radix sort of the order keys (four passes of 8 bits)
+//    keeps equal y in index order, as the reference's stable sort does.
+//  * f32 running sums: f32_run (below) gives the exact sequence of
+//    rounded sums without a 128k-long serial chain.
+// The token of the selected sorted position is found with the fast path's
+// tie walk (the n-th token of that value in index order).
+
+// glibc expf's table: 2^(i/32) rounded to double, minus i << 47 (so that
+// adding k << 47 scales it by 2^(k/32 - i/32)).
+__constant__ unsigned long long kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+// glibc's expf: x N / ln2 = k + r (N = 32, k rounded to nearest by adding
+// 1.5 * 2^52), exp(x) = 2^(k/N) * 2^(r/N), the second factor a cubic in r
+// with the published minimax coefficients, evaluated in double and rounded
+// once to float.  The reduction r = x N / ln2 - k is one fused multiply-add
+// (as GCC contracts it when glibc is built for FMA hardware); every other
+// operation is a separately rounded double operation, in glibc's order.
+__device__ __forceinline__ float expf_glibc(float x) {
+#pragma clang fp contract(off)
+  constexpr double kN = 32.0;
+  constexpr double kInvLn2N = 0x1.71547652b82fep0 * kN;
+  constexpr double kShift = 0x1.8p52;
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / kN / kN / kN;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / kN / kN;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / kN;
+  if (x != x) return x + x;
+  if (x == -INFINITY) return 0.0f;
+  if (x > 0x1.62e42ep6f) return INFINITY;  // overflow (arguments here are <= 0)
+  if (x < -0x1.9fe368p6f) return 0.0f;     // below half the smallest subnormal
+  const double xd = (double)x;
+  const double z = kInvLn2N * xd;
+  double kd = z + kShift;
+  const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
+  kd -= kShift;
+  const double r = __builtin_fma(kInvLn2N, xd, -kd);
+  const unsigned long long t = kExp2Tab[ki % 32] + (ki << 47);
+  const double s = __longlong_as_double((long long)t);
+  const double zz = __builtin_fma(kC0, r, kC1);
+  const double r2 = r * r;
+  double y = __builtin_fma(kC2, r, 1.0);
+  y = __builtin_fma(zz, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+constexpr int kXBits = 8;             // radix sort: bits per pass
+constexpr int kXR = 1 << kXBits;      // buckets per pass
+constexpr int kNoDelta = INT_MIN;     // f32_run: chunk without a precomputed delta
+constexpr int kDeltaCap = (1 << 24) + 1;  // deltas this large always leave the binade
+
+struct ExactSmem {
+  unsigned int off[kSW][kXR];  // radix pass: per-wave digit counts, then positions
+  unsigned int wtot[kSW];
+  double dsum[kST];            // f32_run: chunk sums, then their exclusive prefix
+  int ce[kST];                 // f32_run: binade the chunk's delta assumes
+  int cd0[kST], cd1[kST];      // f32_run: its delta for an even / odd start
+  float s;                     // f32_run result: the sum reached
+  int pos;                     //   and the number of elements it took
+  int flag;
+};
+
+// One stable pass of the LSD radix sort: src[0, n) -> dst by key bits
+// [shift, shift + 8).  Wave w owns a contiguous segment, read 64 keys at a
+// time in order; a key's rank among the keys of its batch with the same
+// digit comes from eight ballots, its base from the wave's running position
+// for the digit (per-wave counts, scanned digit-major, wave-minor).  When
+// every key has the same digit the pass would move nothing: it returns
+// false and leaves dst alone.  Ends with a barrier.
+__device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, int n, int shift) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int seg = ((n + kSW - 1) / kSW + 63) / 64 * 64;
+  const int w0 = min(n, wv * seg), w1 = min(n, w0 + seg);
+  for (int i = tid; i < kSW * kXR; i += kST) (&xs.off[0][0])[i] = 0u;
+  if (tid == 0) xs.flag = 0;
+  __syncthreads();
+  for (int i = w0 + lane; i < w1; i += 64) atomicAdd(&xs.off[wv][(src[i] >> shift) & (kXR - 1)], 1u);
+  __syncthreads();
+  unsigned int c = 0, incl = 0;
+  if (tid < kXR) {  // digit tid: prefix over the waves, then over the digits
+    for (int w = 0; w < kSW; ++w) {
+      const unsigned int h = xs.off[w][tid];
+      xs.off[w][tid] = c;
+      c += h;
+    }
+    incl = c;
+    for (int d = 1; d < 64; d <<= 1) {
+      const unsigned int o = (unsigned int)__shfl_up((int)incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) xs.wtot[wv] = incl;
+    if (c == (unsigned int)n) xs.flag = 1;
+  }
+  __syncthreads();
+  const bool uniform = xs.flag;
+  __syncthreads();  // every thread has read the flag before the next pass clears it
+  if (uniform) return false;
+  if (tid < kXR) {
+    unsigned int base = incl - c;
+    for (int w = 0; w < wv; ++w) base += xs.wtot[w];
+    for (int w = 0; w < kSW; ++w) xs.off[w][tid] += base;
+  }
+  __syncthreads();
+  for (int i0 = w0; i0 < w1; i0 += 64) {
+    const int i = i0 + lane;
+    const bool valid = i < w1;
+    const uint32_t k = valid ? src[i] : 0u;
+    const uint32_t d = (k >> shift) & (kXR - 1);
+    unsigned long long match = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kXBits; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const unsigned long long bal = __ballot(bit);
+      match &= bit ? bal : ~bal;
+    }
+    const unsigned int rank = (unsigned int)__popcll(match & ((1ull << lane) - 1ull));
+    const unsigned int cnt = (unsigned int)__popcll(match);
+    const unsigned int base = xs.off[wv][d];
+    if (valid) {
+      dst[base + rank] = k;
+      if (rank + 1u == cnt) xs.off[wv][d] = base + cnt;
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
+// In binade e (sums s in [2^e, 2^(e+1)), spacing u = 2^(e-23)), adding v >= 0
+// to s = n u gives (n + a + rnd) u, or for a tie (v / u = a + 1/2 exactly)
+// the even one of (n + a) u and (n + a + 1) u, while the result stays below
+// 2^(e+1).  a is capped at kDeltaCap (such a step always leaves the binade).
+__device__ __forceinline__ void split_at(float v, int e, int& a, int& rnd, bool& tie) {
+  const uint32_t b = __float_as_uint(v);
+  const int E = (int)((b >> 23) & 255u);
+  const uint32_t mant = E ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
+  const int k = (E ? E - 150 : -149) - e + 23;  // v / u = mant * 2^k
+  rnd = 0;
+  tie = false;
+  if (k >= 0) {
+    a = k >= 7 ? kDeltaCap : (int)min(mant << k, (uint32_t)kDeltaCap);
+  } else if (k < -25) {
+    a = 0;  // v < u / 4
+  } else {
+    const int sh = -k;
+    a = (int)(mant >> sh);
+    const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    rnd = rem > half;
+    tie = rem == half;
+  }
+}
+
+// The f32 running sum s_{i+1} = fl(s_i + v_i), s_0 = 0, over v[0, len) (in
+// global memory, written before the call), up to and including the first i
+// with s_{i+1} >= thr (use_thr).  Result in xs.s (the sum reached) and
+// xs.pos (elements taken: that i + 1, or len).
+//
+// While the sum stays in one binade e, every step is an integer addition in
+// units of u = 2^(e-23) (split_at), so a run of steps is the sum of their
+// increments -- except at exact ties, where round-half-even makes the step
+// depend on the parity of the running count; a chunk is therefore described
+// by two deltas, one per start parity, and deltas compose.  Each thread
+// takes a contiguous chunk, guesses the binade its running sum starts in
+// from the exact (double) prefix sum, and computes its deltas for that
+// binade.  Wave 0 then walks the chunks in order, applying runs of chunks
+// whose guess matches the actual sum by a composition scan, provided the
+// result stays in the binade and below thr; any other chunk (first chunk,
+// wrong guess, a binade crossing or the threshold inside it, a value that is
+// not finite) is walked element by element with real f32 additions.  The
+// guesses only decide the speed: every delta used is checked against the
+// actual running sum.  Call from all threads; ends with a barrier.
+__device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, float thr) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int L = (len + kST - 1) / kST;
+  const int lo = min(len, tid * L), hi = min(len, lo + L);
+  double sum = 0.0;
+  bool finite = true;
+  for (int i = lo; i < hi; ++i) {
+    const float x = v[i];
+    finite &= x >= 0.0f && x <= 3.402823466e38f;
+    sum += (double)x;
+  }
+  // exclusive prefix of the chunk sums
+  double incl = sum;
+  for (int d = 1; d < 64; d <<= 1) {
+    const double o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) xs.dsum[wv] = incl;
+  __syncthreads();
+  double pre = incl - sum;
+  for (int w = 0; w < wv; ++w) pre += xs.dsum[w];
+  __syncthreads();
+  // Chunks past the threshold (with a margin far above any f32 drift) are
+  // never reached by the walk before it stops; they get no delta.
+  int e = kNoDelta, d0 = 0, d1 = 0;
+  if (finite && hi > lo && pre > 0.0 && !(use_thr && pre > (double)thr * 1.0625 + 1e-30)) {
+    int ex;
+    (void)frexp(pre, &ex);
+    e = ex - 1;
+    int p0 = 0, p1 = 1;
+    for (int i = lo; i < hi && d0 < kDeltaCap && d1 < kDeltaCap; ++i) {
+      int a, rnd;
+      bool tie;
+      split_at(v[i], e, a, rnd, tie);
+      const int q0 = tie ? a + ((p0 + a) & 1) : a + rnd;
+      const int q1 = tie ? a + ((p1 + a) & 1) : a + rnd;
+      d0 = min(d0 + q0, kDeltaCap);
+      d1 = min(d1 + q1, kDeltaCap);
+      p0 = (p0 + q0) & 1;
+      p1 = (p1 + q1) & 1;
+    }
+    if (d0 >= kDeltaCap || d1 >= kDeltaCap) e = kNoDelta;
+  }
+  xs.ce[tid] = e;
+  xs.cd0[tid] = d0;
+  xs.cd1[tid] = d1;
+  __syncthreads();
+
+  if (wv == 0) {
+    float s = 0.0f;
+    int pos = len;
+    bool done = false;
+    // element-by-element walk of chunk c (wave-uniform)
+    auto walk = [&](int c) {
+      const int clo = min(len, c * L), chi = min(len, clo + L);
+      for (int i0 = clo; i0 < chi && !done; i0 += 64) {
+        const float x = i0 + lane < chi ? v[i0 + lane] : 0.0f;
+        const int m = min(64, chi - i0);
+        for (int j = 0; j < m; ++j) {
+          s = s + readlane_f(x, j);
+          if (use_thr && s >= thr) {
+            pos = i0 + j + 1;
+            done = true;
+            break;
+          }
+        }
+      }
+    };
+    for (int g = 0; g < kST && g * L < len && !done; g += 64) {
+      const int ec = xs.ce[g + lane], c0 = xs.cd0[g + lane], c1 = xs.cd1[g + lane];
+      int start = 0;
+      while (start < 64 && !done) {
+        const uint32_t sb = __float_as_uint(s);
+        const int sE = (int)((sb >> 23) & 255u);
+        const bool s_normal = sE >= 1 && sE <= 254 && !(sb >> 31);
+        const int es = sE - 127;
+        const unsigned long long rm = __ballot(s_normal && lane >= start && ec == es) >> start;
+        const int run = ~rm ? __builtin_ctzll(~rm) : 64;
+        if (run == 0) {
+          walk(g + start);
+          ++start;
+          continue;
+        }
+        // composed deltas of chunks start .. lane (identity outside the run)
+        const bool in = lane >= start && lane < start + run;
+        int a0 = in ? c0 : 0, a1 = in ? c1 : 0;
+        for (int k = 1; k < 64; k <<= 1) {
+          const int b0 = __shfl_up(a0, k, 64), b1 = __shfl_up(a1, k, 64);
+          if (lane >= k) {
+            const int n0 = b0 + ((b0 & 1) ? a1 : a0);
+            const int n1 = b1 + ((b1 & 1) ? a0 : a1);
+            a0 = min(n0, kDeltaCap);
+            a1 = min(n1, kDeltaCap);
+          }
+        }
+        const int n = (int)((sb & 0x7fffffu) | 0x800000u);
+        const long long nend = (long long)n + ((n & 1) ? a1 : a0);
+        const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
+        const unsigned long long bad =
+            __ballot(in && (nend >= (1ll << 24) || (use_thr && send >= thr)));
+        if (!bad) {
+          s = readlane_f(send, start + run - 1);
+          start += run;
+          continue;
+        }
+        const int l = __builtin_ctzll(bad);
+        if (l > start) s = readlane_f(send, l - 1);
+        walk(g + l);
+        start = l + 1;
+      }
+    }
+    if (lane == 0) {
+      xs.s = s;
+      xs.pos = pos;
+    }
+  }
+  __syncthreads();
+}
+
+// Sorts the keys in a[0, n) ascending (b: scratch of n keys); returns the
+// array that holds the result.
+__device__ uint32_t* radix_sort(ExactSmem& xs, uint32_t* a, uint32_t* b, int n) {
+  for (int shift = 0; shift < 32; shift += kXBits) {
+    if (radix_pass(xs, a, b, n, shift)) {
+      uint32_t* t = a;
+      a = b;
+      b = t;
+    }
+  }
+  return a;
+}
+
+struct ExactArgs {
+  const char* logits;
+  long long stride_bytes;
+  int vocab;
+  const float* temps;
+  int top_k;         // 0: None
+  float top_p;       // NaN: None
+  float r;
+  int32_t* tokens;
+  uint32_t* scratch;  // 2 * vocab keys per row of the launch
+  int row0;           // first row of this launch
+};
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
+  __shared__ SampleSmem sm;
+  __shared__ ExactSmem xs;
+  const int row = a.row0 + blockIdx.x;
+  const int tid = threadIdx.x;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || V <= 1) {  // sample.rs:13-15
+    float bv;
+    int bi;
+    block_argmax<DT, VEC>(sm, x, 0, V, bv, bi);
+    if (tid == 0) a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    return;
+  }
+  uint32_t* ka = a.scratch + (size_t)blockIdx.x * 2 * (size_t)V;
+  uint32_t* kb = ka + V;
+  // descending y = ascending complemented order key; -0.0 and +0.0 share a key
+  for_each<DT, VEC>(x, V, [&](int i, float v) { ka[i] = ~order_key(v / T); });
+  __syncthreads();
+  const uint32_t* sk = radix_sort(xs, ka, kb, V);
+  float* p = reinterpret_cast<float*>(sk == ka ? kb : ka);
+
+  int len = a.top_k > 0 && a.top_k < V ? a.top_k : V;  // probs.truncate(k)
+  const float max_x = key_value(~sk[0]);
+  for (int i = tid; i < len; i += kST) p[i] = expf_glibc(key_value(~sk[i]) - max_x);
+  __syncthreads();
+  f32_run(xs, p, len, false, 0.0f);  // sum += p
+  const float sum = xs.s;
+  for (int i = tid; i < len; i += kST) p[i] = p[i] / sum;
+  __syncthreads();
+  if (a.top_p == a.top_p) {  // Some(top_p)
+    f32_run(xs, p, len, true, a.top_p);
+    const int cutoff = xs.pos;
+    const float s = xs.s;  // equals the f32 sum of the kept probabilities
+    len = cutoff;
+    for (int i = tid; i < len; i += kST) p[i] = p[i] / s;
+    __syncthreads();
+  }
+  f32_run(xs, p, len, true, a.r);  // acc += prob until r <= acc
+  const int j = xs.pos - 1;  // xs.pos = len when acc never reaches r: probs.last()
+  // the token at sorted position j: its value's first sorted position, then
+  // that many tokens further among the equal ones, in index order
+  const uint32_t kj = sk[j];
+  int lo = 0, hi = j;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (sk[mid] < kj) lo = mid + 1;
+    else hi = mid;
+  }
+  Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
+  const int tok = nth_tied<false>(sm, rw, ~kj, (unsigned long long)(j - lo + 1));
+  if (tid == 0) a.tokens[row] = tok;
+}
+
+// The exp the exact path uses, for verification: out[i] = expf_glibc(in[i]).
+__global__ void expf_glibc_kernel(const float* in, float* out, long long n) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long long)gridDim.x * blockDim.x)
+    out[i] = expf_glibc(in[i]);
+}
+
+// Rows per launch of the exact path: the key scratch (8 bytes per logit)
+// stays within kExactScratch bytes.
+constexpr size_t kExactScratch = 512ull << 20;
+
+template <int DT, bool VEC>
+hipError_t launch_exact_dt(const ExactArgs& a0, int batch, hipStream_t stream) {
+  if (!a0.temps || a0.vocab <= 1) {  // every row is argmax: no scratch
+    sample_exact_kernel<DT, VEC><<<batch, kST, 0, stream>>>(a0);
+    return hipGetLastError();
+  }
+  const size_t per_row = (size_t)2 * (size_t)a0.vocab * sizeof(uint32_t);
+  const int rows = (int)std::max<size_t>(1, std::min<size_t>(batch, kExactScratch / per_row));
+  void* p = nullptr;
+  hipError_t e = hipMallocAsync(&p, per_row * rows, stream);
+  if (e != hipSuccess) return e;
+  ExactArgs a = a0;
+  a.scratch = static_cast<uint32_t*>(p);
+  for (int r0 = 0; r0 < batch; r0 += rows) {
+    a.row0 = r0;
+    sample_exact_kernel<DT, VEC><<<std::min(rows, batch - r0), kST, 0, stream>>>(a);
+  }
+  e = hipGetLastError();
+  const hipError_t f = hipFreeAsync(p, stream);
+  return e != hipSuccess ? e : f;
+}
+
 // Workgroups per row for the split path (1: one workgroup per row).  Rows
 // without temperatures are all greedy: one pass, one launch.
 int split_groups(int batch, int vocab, const float* temps, int top_k, float top_p) {
@@ -915,6 +1340,28 @@ hipError_t launch_sample(const void* logits, int dtype, long long row_stride, in
                                     : launch_dt<PKV_BF16, false>(a, batch, stream);
   return vec ? launch_dt<PKV_F16, true>(a, batch, stream)
              : launch_dt<PKV_F16, false>(a, batch, stream);
+}
+
+hipError_t launch_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
+                               int vocab, const float* temperatures, int top_k, float top_p,
+                               float r, int32_t* tokens, hipStream_t stream) {
+  const long long sb = row_stride * (long long)dtype_bytes(dtype);
+  ExactArgs a{static_cast<const char*>(logits), sb, vocab, temperatures, top_k, top_p, r,
+              tokens, nullptr, 0};
+  const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (batch == 1 || sb % 16 == 0);
+  if (dtype == PKV_F32) return vec ? launch_exact_dt<PKV_F32, true>(a, batch, stream)
+                                   : launch_exact_dt<PKV_F32, false>(a, batch, stream);
+  if (dtype == PKV_BF16) return vec ? launch_exact_dt<PKV_BF16, true>(a, batch, stream)
+                                    : launch_exact_dt<PKV_BF16, false>(a, batch, stream);
+  return vec ? launch_exact_dt<PKV_F16, true>(a, batch, stream)
+             : launch_exact_dt<PKV_F16, false>(a, batch, stream);
+}
+
+hipError_t launch_expf_glibc(const float* in, float* out, long long n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const long long blocks = std::min<long long>((n + 255) / 256, 65536);
+  expf_glibc_kernel<<<(unsigned)blocks, 256, 0, stream>>>(in, out, n);
+  return hipGetLastError();
 }
 
 }  // namespace pkv

@@ -155,10 +155,14 @@ def sample_draw(seed: int = 42) -> float:
 
 
 def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | None = None,
-           seed: int = 42, out=None, stream=None):
+           seed: int = 42, out=None, stream=None, exact: bool = True):
     """Token per logits row on the device: argmax / sample() of sample.rs:12-55.
     logits: (batch, vocab) f32/f16/bf16 with unit stride along vocab;
     temperatures: (batch,) float32 on the device (None: all greedy).
+    exact=True (pkv_sample_exact): the reference's f32 arithmetic bit for bit,
+    so the token is the reference's on every row.  exact=False (pkv_sample):
+    faster; sums the probabilities exactly, so a row can differ where the
+    reference's f32 running sum lands within its rounding of r or top_p.
     Returns (batch,) int32 on the device."""
     import torch
     if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
@@ -173,6 +177,10 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
     s = cur if stream is None else stream
     if s != cur:
         s.wait_stream(cur)
+    if exact:  # top_p None is NaN; any other value is Some(top_p)
+        fn, tp = lib().pkv_sample_exact, float("nan") if top_p is None else float(top_p)
+    else:      # top_p None is 1.0 (no cut in exact arithmetic)
+        fn, tp = lib().pkv_sample, 1.0 if top_p is None else float(top_p)
     with torch.cuda.stream(s):
         if out is None:
             out = torch.empty(B, dtype=torch.int32, device=dev)
@@ -181,11 +189,23 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
             t = torch.as_tensor(temperatures, dtype=torch.float32).to(dev).contiguous()
             if t.numel() != B:
                 raise ValueError("temperatures must have one value per row")
-        check(lib().pkv_sample(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
-                               logits.stride(0) if B > 1 else V, B, V,
-                               _dev_ptr(t) if t is not None else None, top_k or 0,
-                               1.0 if top_p is None else float(top_p), seed, _dev_ptr(out),
-                               _stream_ptr(s)), None)
+        check(fn(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
+                 logits.stride(0) if B > 1 else V, B, V,
+                 _dev_ptr(t) if t is not None else None, top_k or 0, tp, seed, _dev_ptr(out),
+                 _stream_ptr(s)), None)
+    return out
+
+
+def sample_expf(x):
+    """expf as the exact sampler computes it (glibc's algorithm) for a float32
+    device tensor; returns a new tensor."""
+    import torch
+    x = x.contiguous()
+    if x.dtype != torch.float32:
+        raise ValueError("float32 input expected")
+    out = torch.empty_like(x)
+    check(lib().pkv_sample_expf(_dev_ptr(x), _dev_ptr(out), x.numel(),
+                                _stream_ptr(torch.cuda.current_stream(x.device))), None)
     return out
 
 

@@ -83,6 +83,9 @@ SIGNATURES: dict[str, tuple] = {
                              ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "pkv_sample": (_I, [_P, _I, ctypes.c_longlong, _I, _I, _P, _I, ctypes.c_float,
                         ctypes.c_uint64, _P, _P]),
+    "pkv_sample_exact": (_I, [_P, _I, ctypes.c_longlong, _I, _I, _P, _I, ctypes.c_float,
+                              ctypes.c_uint64, _P, _P]),
+    "pkv_sample_expf": (_I, [_P, _P, ctypes.c_longlong, _P]),
     "pkv_sample_draw": (ctypes.c_float, [ctypes.c_uint64]),
     "pkv_pool_profile": (_I, [_P, _I]),
     "pkv_pool_profile_read": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),

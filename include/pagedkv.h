@@ -218,9 +218,12 @@ int pkv_decode_attention(pkv_pool* pool, int layer, const void* q, void* out,
                          void* stream);
 
 /* Workspace that pkv_decode_attention needs for a given batch/length; the
- * pool grows its internal workspace on demand (hipMalloc + device sync).
+ * pool grows its internal workspace on demand with a hipMalloc and no
+ * synchronisation (the buffer it replaces stays allocated until the next
+ * reserve call or pkv_pool_destroy, since queued work may still read it).
  * Callers that must not allocate later (stream capture, serving loops)
- * reserve the largest shape they will use up front. */
+ * reserve the largest shape they will use up front; the reserve calls
+ * synchronise the device when they free replaced buffers. */
 size_t pkv_decode_workspace_bytes(const pkv_pool* pool, int batch, int n_head,
                                   int max_context_len);
 int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,
@@ -396,6 +399,27 @@ int pkv_append_rope(pkv_pool* pool, int layer, const pkv_rope* rope,
 int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
                int vocab, const float* temperatures, int top_k, float top_p,
                uint64_t seed, int32_t* tokens, void* stream);
+/* sample() of crates/ai-engine-runtime/src/sample.rs:12-48 with the
+ * reference's own f32 arithmetic, bit for bit: the token equals the
+ * reference's on every row, including rows where its f32 rounding alone
+ * moves the pick (pkv_sample matches those only to within that rounding).
+ * Same arguments as pkv_sample except top_p: NaN is None and any other value
+ * is Some(top_p), as in the reference, where Some(1.0) still truncates once
+ * the f32 running sum reaches 1.  Exponentials are glibc's expf (what
+ * f32::exp calls on x86-64 Linux), restated on the device and equal to the
+ * host libm on every argument the path uses (<= 0); the sort is a stable
+ * radix sort; every f32 running sum (the softmax denominator, top_p's
+ * cumulative sum, the r threshold) takes exactly the reference's rounding
+ * steps.  Scratch: 8 bytes per logit per row, at most 512 MB per launch
+ * (larger batches run in several launches), in a stream-ordered allocation
+ * on `stream`.  One 1024-thread workgroup per row. */
+int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
+                     int vocab, const float* temperatures, int top_k, float top_p,
+                     uint64_t seed, int32_t* tokens, void* stream);
+/* The exp pkv_sample_exact uses, exposed for verification (no reference
+ * counterpart): out[i] = expf(in[i]) as glibc computes it; device arrays of
+ * n floats, on `stream`. */
+int pkv_sample_expf(const float* in, float* out, long long n, void* stream);
 /* StdRng::seed_from_u64(seed).gen::<f32>() (sample.rs:41-42; host only). */
 float pkv_sample_draw(uint64_t seed);
 

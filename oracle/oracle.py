@@ -100,6 +100,15 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_sample.restype = ctypes.c_int64
     L.orc_threads.argtypes = [ctypes.c_int]
     L.orc_threads.restype = ctypes.c_int
+    L.orc_expf_host.argtypes = [_P, _P, _SZ]
+    L.orc_expf_host.restype = None
+    L.orc_expf_glibc.argtypes = [ctypes.c_float]
+    L.orc_expf_glibc.restype = ctypes.c_float
+    L.orc_exp2_tab_entry.argtypes = [ctypes.c_int]
+    L.orc_exp2_tab_entry.restype = ctypes.c_uint64
+    L.orc_expf_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      ctypes.POINTER(ctypes.c_uint32)]
+    L.orc_expf_mismatches.restype = ctypes.c_int64
 
 
 def _p(a: np.ndarray) -> int:
@@ -426,3 +435,29 @@ def sample(logits, temperature: float, top_k: int | None = None, top_p: float | 
                            0 if top_p is None else 1, 0.0 if top_p is None else top_p, seed,
                            1 if precise else 0, ctypes.byref(m))
     return int(tok), float(m.value)
+
+
+def expf_host(x) -> np.ndarray:
+    """The host C library's expf, element by element (what the reference's
+    f32::exp calls); numpy's float32 exp is a different implementation."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_expf_host(_p(x), _p(out), x.size)
+    return out
+
+
+def expf_glibc(x: float) -> float:
+    """The device's restatement of glibc's expf, evaluated on the host."""
+    return float(lib().orc_expf_glibc(x))
+
+
+def exp2_tab_entry(i: int) -> int:
+    return int(lib().orc_exp2_tab_entry(i))
+
+
+def expf_mismatches(lo: int, hi: int, step: int = 1) -> tuple[int, int]:
+    """(count, first bit pattern) of inputs lo, lo + step, ... <= hi (float
+    bit patterns) where the restatement and the host expf differ."""
+    f = ctypes.c_uint32()
+    n = lib().orc_expf_mismatches(lo, hi, step, ctypes.byref(f))
+    return int(n), int(f.value)

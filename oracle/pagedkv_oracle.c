@@ -46,6 +46,10 @@
  *                           pick floor(r * V), two-token logistic, top-k and
  *                           top-p renormalisation), first-maximum and NaN
  *                           rules of argmax.
+ *   orc_expf_glibc        - the device restatement of glibc's expf (what the
+ *                           exact sampler uses), checked here against the
+ *                           host libm's expf on every float <= 0
+ *                           (orc_expf_mismatches).
  *   orc_chacha_block      - the public ChaCha20 and ChaCha12 all-zero key
  *                           test vectors; orc_pcg32_output - the pcg32
  *                           reference demo sequence (initstate 42, initseq
@@ -954,4 +958,77 @@ int64_t orc_sample(const float* logits, size_t n, float temperature, int top_k, 
     free(idx);
     free(p);
     return tok;
+}
+
+/* ------------------------------------------------------------------------ */
+/* expf.  The reference's f32::exp is the C library's expf on its host; on   */
+/* x86-64 Linux that is glibc's (the algorithm of Arm's Optimized Routines,  */
+/* glibc >= 2.28, built for FMA hardware).  orc_expf_host evaluates the      */
+/* host libm itself.  orc_expf_glibc restates the algorithm as the GPU's     */
+/* exact sampler computes it (pkv_sample.hip, expf_glibc): x N / ln2 = k + r */
+/* (N = 32, k by the 1.5 * 2^52 shift), r by one fused multiply-add,          */
+/* exp(x) = 2^(k/N) (table of 2^(i/32) rounded to double) times a cubic in r */
+/* with the published minimax coefficients, in double, rounded once.         */
+/* orc_expf_mismatches counts the inputs where the two disagree, so a test  */
+/* can pin the restatement to the host libm on every float <= 0.             */
+/* ------------------------------------------------------------------------ */
+void orc_expf_host(const float* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = expf(x[i]);
+}
+
+static const uint64_t orc_exp2_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+uint64_t orc_exp2_tab_entry(int i) { return orc_exp2_tab[i & 31]; }
+
+float orc_expf_glibc(float x) {
+    const double N = 32.0;
+    const double inv_ln2_n = 0x1.71547652b82fep0 * N, shift = 0x1.8p52;
+    const double c0 = 0x1.c6af84b912394p-5 / N / N / N, c1 = 0x1.ebfce50fac4f3p-3 / N / N;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / N;
+    if (x != x) return x + x;
+    if (x == -INFINITY) return 0.0f;
+    if (x > 0x1.62e42ep6f) return INFINITY;
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    double xd = (double)x, z = inv_ln2_n * xd, kd = z + shift;
+    uint64_t ki, t;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    double r = fma(inv_ln2_n, xd, -kd);
+    t = orc_exp2_tab[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    double zz = fma(c0, r, c1), r2 = r * r, y = fma(c2, r, 1.0);
+    y = fma(zz, r2, y);
+    return (float)(y * s);
+}
+
+/* Inputs with bit patterns lo, lo + step, ... <= hi where orc_expf_glibc
+ * and the host expf differ; *first gets the first one (0: none). */
+int64_t orc_expf_mismatches(uint32_t lo, uint32_t hi, uint32_t step, uint32_t* first) {
+    int64_t bad = 0;
+    uint32_t f = 0;
+    const int64_t n = ((int64_t)hi - (int64_t)lo) / (int64_t)step + 1;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (int64_t j = 0; j < n; ++j) {
+        uint32_t b = lo + (uint32_t)(j * (int64_t)step);
+        float x, a, m;
+        memcpy(&x, &b, 4);
+        a = expf(x);
+        m = orc_expf_glibc(x);
+        if (memcmp(&a, &m, 4) != 0) {
+            ++bad;
+#pragma omp critical
+            if (!f || b < f) f = b;
+        }
+    }
+    if (first) *first = f;
+    return bad;
 }

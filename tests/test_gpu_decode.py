@@ -260,6 +260,38 @@ def test_batched_equals_solo(gpu):
     c.close()
 
 
+def test_workspace_grows_under_queued_work(gpu):
+    # Calls queued back to back without synchronising, each needing a larger
+    # workspace than the last: the growth replaces the buffer while earlier
+    # launches may still read the old one, which must stay valid until the
+    # reserve call frees it.  Every call's rows match the oracle.
+    ctx = list(wl.randint(41, 24, 200, 6000))
+    c = Case(gpu, wl.F16, 32, 8, 64, 16, ctx, seed=41)
+    ref = c.reference()[0]
+    pool = c.cache.layer(0)
+    q = _to_dev(c.q, c.dt, gpu)
+    tables = torch.from_numpy(c.tables).to(gpu)
+    lens = torch.from_numpy(c.context_lens).to(gpu)
+    outs = []
+    for n, mcl in ((2, 1000), (8, 3000), (24, int(c.context_lens.max()))):
+        sub = torch.from_numpy(np.minimum(c.context_lens[:n], mcl)).to(gpu)
+        outs.append((n, mcl, pool.decode_attention(q[:n], tables[:n], sub, max_context_len=mcl,
+                                                   scale=c.scale, out_dtype=torch.float32)))
+    c.cache.reserve_decode(24, 32, 8192)  # frees the replaced buffers after a device sync
+    torch.cuda.synchronize()
+    c.cache.check()
+    for n, mcl, out in outs:
+        if mcl >= int(c.context_lens[:n].max()):
+            _close(out.cpu().numpy(), ref[:n], f"batch {n}")
+        else:  # rows clamped to mcl keys: compare with the oracle over those keys
+            kp, vp = c.kp, c.vp
+            r = oracle.paged_attention_f64(kp, vp, c.dt, c.bs, c.tables[:n].astype(np.uint32),
+                                           np.minimum(c.context_lens[:n], mcl).astype(np.int32),
+                                           wl.widen(c.q[:n], c.dt), c.scale)
+            _close(out.cpu().numpy(), r, f"batch {n} clamped to {mcl}")
+    c.close()
+
+
 def test_profile_hook_times_main_kernel(gpu):
     c = Case(gpu, wl.BF16, 32, 8, 128, 16, list(wl.randint(3, 16, 100, 2000)), seed=31)
     c.cache.profile(True)

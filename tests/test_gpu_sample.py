@@ -1,12 +1,16 @@
-"""GPU parity of token selection (pkv_sample) against the CPU oracle's
-restatement of sample() / argmax() (crates/ai-engine-runtime/src/sample.rs:
-12-55).  Greedy rows are exact.  The kernel sums probability mass exactly
-(integers), so sampled rows are compared with the oracle's restatement in
-exact arithmetic (float64 exp and running sums over the reference's f32
-values): the token must be equal unless that restatement's running sum lies
-within 1e-6 of r or top_p.  Against the oracle's f32 restatement (the
-reference's own rounding), a row may differ only where that rounding alone
-moves the pick, i.e. where the f32 and float64 restatements differ."""
+"""GPU parity of token selection against the CPU oracle's restatement of
+sample() / argmax() (crates/ai-engine-runtime/src/sample.rs:12-55).
+
+pkv_sample_exact (pagedkv.sample, the default): the token equals the
+oracle's f32 restatement -- the reference's own arithmetic -- on every row.
+
+pkv_sample (exact=False): greedy rows are exact; the kernel sums probability
+mass exactly (integers), so sampled rows are compared with the oracle's
+restatement in exact arithmetic (float64 exp and running sums over the
+reference's f32 values): the token must be equal unless that restatement's
+running sum lies within 1e-6 of r or top_p.  Against the f32 restatement, a
+row may differ only where that rounding alone moves the pick, i.e. where the
+f32 and float64 restatements differ."""
 import math
 
 import numpy as np
@@ -51,14 +55,15 @@ def _check_rows(x32, temps, top_k, top_p, got, seed=42):
     return differ
 
 
-def test_reference_kats_on_device(gpu):
+@pytest.mark.parametrize("exact", [True, False])
+def test_reference_kats_on_device(gpu, exact):
     cases = [([0.1, 5.0, 2.0, -1.0], 0.0, None, None, 1),
              ([1.0, 5.0, 2.0], 0.0, None, None, 1),
              ([1.0, 1.0, 1.0, 1.0, 100.0], 1.0, 1, None, 4),
              ([1.0, 1.0, 100.0, 1.0], 1.0, None, 0.5, 2)]
     for x, t, k, p, want in cases:
         lg = torch.tensor([x], dtype=torch.float32, device=gpu)
-        tok = pagedkv.sample(lg, torch.tensor([t]), top_k=k, top_p=p, seed=0)
+        tok = pagedkv.sample(lg, torch.tensor([t]), top_k=k, top_p=p, seed=0, exact=exact)
         assert int(tok.item()) == want
 
 
@@ -73,7 +78,7 @@ def test_sample_matches_oracle(gpu, dt, V, top_k, top_p):
     lg = torch.from_numpy(x).to(gpu).to(TD[dt])
     x32 = lg.float().cpu().numpy()          # the values the kernel sees
     temps = np.array([[0.0, 0.7, 1.0, 1.6, -1.0, 0.3][b % 6] for b in range(B)], np.float32)
-    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
+    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p, exact=False)
     torch.cuda.synchronize()
     _check_rows(x32, temps, top_k, top_p, got.cpu().numpy())
 
@@ -83,28 +88,30 @@ def test_uniform_rows_closed_form(gpu):
     r = pagedkv.sample_draw(42)
     for V in (10, 100, 1000, 4096, 50000):
         lg = torch.zeros((3, V), dtype=torch.bfloat16, device=gpu)
-        tok = pagedkv.sample(lg, torch.tensor([1.0, 0.5, 2.0]))
+        tok = pagedkv.sample(lg, torch.tensor([1.0, 0.5, 2.0]), exact=False)
         assert tok.cpu().tolist() == [math.floor(r * V)] * 3
     lg = torch.zeros((1, 1000), device=gpu)
-    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_k=10).item()) == math.floor(10 * r)
-    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_p=0.5).item()) == math.floor(500 * r)
+    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_k=10, exact=False).item()) == math.floor(10 * r)
+    assert int(pagedkv.sample(lg, torch.tensor([1.0]), top_p=0.5, exact=False).item()) == math.floor(500 * r)
 
 
-def test_greedy_rules_on_device(gpu):
+@pytest.mark.parametrize("exact", [True, False])
+def test_greedy_rules_on_device(gpu, exact):
     nan, inf = math.nan, math.inf
     rows = [[1.0, 5.0, 5.0, 2.0], [nan, 1.0, 3.0, 3.0], [-inf, -inf, -inf, -inf],
             [nan, -inf, nan, nan], [2.0, nan, 2.0, 9.0]]
     lg = torch.tensor(rows, device=gpu)
-    tok = pagedkv.sample(lg)                 # no temperatures: every row greedy
+    tok = pagedkv.sample(lg, exact=exact)    # no temperatures: every row greedy
     assert tok.cpu().tolist() == [oracle.argmax(r) for r in rows] == [1, 2, 0, 0, 3]
     # one logit: argmax even when sampling; no logits: token 0
-    assert int(pagedkv.sample(torch.tensor([[4.0]], device=gpu), torch.tensor([1.0])).item()) == 0
-    assert int(pagedkv.sample(torch.zeros((1, 0), device=gpu)).item()) == 0
+    one = torch.tensor([[4.0]], device=gpu)
+    assert int(pagedkv.sample(one, torch.tensor([1.0]), exact=exact).item()) == 0
+    assert int(pagedkv.sample(torch.zeros((1, 0), device=gpu), exact=exact).item()) == 0
     # a large greedy row: first maximum by index
     x = torch.randn((4, 128256), device=gpu)
     x[:, 77777] = 50.0
     x[:, 99999] = 50.0
-    assert pagedkv.sample(x).cpu().tolist() == [77777] * 4
+    assert pagedkv.sample(x, exact=exact).cpu().tolist() == [77777] * 4
 
 
 def test_strided_rows_and_determinism(gpu):
@@ -112,8 +119,8 @@ def test_strided_rows_and_determinism(gpu):
     big = torch.from_numpy(rng.standard_normal((16, 40000)).astype(np.float32)).to(gpu)
     lg = big[:, 1000:33000]                  # row stride 40000, vocab 32000
     temps = torch.full((16,), 0.8)
-    a = pagedkv.sample(lg, temps)
-    b = pagedkv.sample(lg, temps)
+    a = pagedkv.sample(lg, temps, exact=False)
+    b = pagedkv.sample(lg, temps, exact=False)
     assert torch.equal(a, b)
     _check_rows(lg.cpu().numpy(), temps.numpy(), None, None, a.cpu().numpy())
 
@@ -121,14 +128,15 @@ def test_strided_rows_and_determinism(gpu):
 def test_seed_changes_draw(gpu):
     lg = torch.zeros((1, 1000), device=gpu)
     for seed in (0, 1, 42, 12345):
-        tok = int(pagedkv.sample(lg, torch.tensor([1.0]), seed=seed).item())
+        tok = int(pagedkv.sample(lg, torch.tensor([1.0]), seed=seed, exact=False).item())
         assert tok == math.floor(pagedkv.sample_draw(seed) * 1000)
 
 
-def test_invalid_arguments(gpu):
+@pytest.mark.parametrize("exact", [True, False])
+def test_invalid_arguments(gpu, exact):
     lg = torch.zeros((2, 10), device=gpu)
     with pytest.raises(pagedkv.PagedKvError):
-        pagedkv.sample(lg, torch.ones(2), top_k=-1)
+        pagedkv.sample(lg, torch.ones(2), top_k=-1, exact=exact)
 
 
 # -- batches of at most 128 rows split each row over several workgroups --------
@@ -148,8 +156,9 @@ def test_split_rows_equal_one_workgroup_rows(gpu, dt):
     temps = np.array([[0.0, 0.7, 1.0, 1.6, -1.0, 0.3, 0.8, 2.0][b % 8] for b in range(B)],
                      np.float32)
     lg = torch.from_numpy(x).to(gpu).to(TD[dt])
-    small = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu))
-    big = pagedkv.sample(lg.repeat(16, 1), torch.from_numpy(np.tile(temps, 16)).to(gpu))
+    small = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), exact=False)
+    big = pagedkv.sample(lg.repeat(16, 1), torch.from_numpy(np.tile(temps, 16)).to(gpu),
+                         exact=False)
     torch.cuda.synchronize()
     assert torch.equal(big.view(16, B), small.view(1, B).expand(16, B))
     _check_rows(lg.float().cpu().numpy(), temps, None, None, small.cpu().numpy())
@@ -164,7 +173,7 @@ def test_split_ragged_vocab_and_strides(gpu, B):
     big = torch.from_numpy(_rows(rng, B, V + 3)).to(gpu).to(torch.bfloat16)
     lg = big[:, 1:V + 1]                       # row stride V + 3, misaligned start
     temps = np.array([[0.9, 0.0, 1.3, 0.6][b % 4] for b in range(B)], np.float32)
-    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu))
+    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), exact=False)
     torch.cuda.synchronize()
     _check_rows(lg.float().cpu().numpy(), temps, None, None, got.cpu().numpy())
 
@@ -180,7 +189,7 @@ def test_split_greedy_rows(gpu, with_temps):
         x[b, pos] = 40.0
     x[5, 90000] = 40.0                         # a later equal maximum loses
     temps = torch.zeros(B, device=gpu) if with_temps else None
-    assert pagedkv.sample(x, temps).cpu().tolist() == [0, 4095, 4096, 65000, 128255, 100]
+    assert pagedkv.sample(x, temps, exact=False).cpu().tolist() == [0, 4095, 4096, 65000, 128255, 100]
 
 
 def test_split_path_replays_in_a_graph(gpu):
@@ -191,18 +200,135 @@ def test_split_path_replays_in_a_graph(gpu):
     B, V = 8, 128256
     lg = torch.from_numpy(_rows(rng, B, V)).to(gpu).to(torch.bfloat16)
     temps = torch.full((B,), 0.9, device=gpu)
-    ref = pagedkv.sample(lg, temps).clone()
+    ref = pagedkv.sample(lg, temps, exact=False).clone()
     out = torch.empty(B, dtype=torch.int32, device=gpu)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):               # warm-up on a side stream
+        pagedkv.sample(lg, temps, out=out, exact=False)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pagedkv.sample(lg, temps, out=out, exact=False)
+    for i in range(4):
+        out.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        eager = pagedkv.sample(lg[:3], temps[:3], exact=False)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref[:3])
+
+
+# -- pkv_sample_exact: the reference's f32 arithmetic, bit for bit -----------
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_expf_on_device_equals_host_libm(gpu):
+    # every 64th float from -0.0 to -104 (the exact sampler's arguments are
+    # y - max <= 0; below -103.97 the result is 0), every float in [-2^-20,
+    # 0] and around the input where an unfused reduction rounds differently,
+    # and the special values
+    pats = [np.arange(0x80000000, 0xC2D00000, 64, dtype=np.uint64),
+            np.arange(0x80000000, 0xB5800000, 977, dtype=np.uint64),
+            np.arange(0xC27C65D9 - 4096, 0xC27C65D9 + 4096, dtype=np.uint64),
+            np.array([0x00000000, 0x80000000, 0xFF800000, 0xC2CFF1B4, 0xC2CFF1B5], np.uint64)]
+    x = np.concatenate(pats).astype(np.uint32).view(np.float32)
+    want = oracle.expf_host(x)
+    got = pagedkv.sample_expf(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    bad = np.flatnonzero(_bits(got) != _bits(want))
+    assert bad.size == 0, [(hex(int(_bits(x)[i])), float(got[i]), float(want[i])) for i in bad[:5]]
+    assert math.isnan(float(pagedkv.sample_expf(torch.tensor([math.nan], device=gpu)).item()))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("V", [2, 7, 1000, 32000, 128256])
+@pytest.mark.parametrize("top_k,top_p", [(None, None), (40, None), (None, 0.9), (5, 0.5),
+                                         (None, 1.0)])
+def test_exact_equals_reference_f32(gpu, dt, V, top_k, top_p):
+    # every row's token is the f32 restatement's (top_p 1.0 is Some(1.0):
+    # it truncates where the f32 running sum reaches 1)
+    rng = np.random.default_rng(V + 7 * (top_k or 0) + int(100 * (top_p or 0)))
+    kinds = ["normal", "ties", "flat", "spiky"]
+    B = 24
+    x = np.stack([_logits(rng, kinds[b % 4], V) for b in range(B)])
+    lg = torch.from_numpy(x).to(gpu).to(TD[dt])
+    x32 = lg.float().cpu().numpy()
+    temps = np.array([[0.0, 0.7, 1.0, 1.6, -1.0, 0.3][b % 6] for b in range(B)], np.float32)
+    got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
+    torch.cuda.synchronize()
+    want = [oracle.sample(x32[b], float(temps[b]), top_k=top_k, top_p=top_p)[0]
+            for b in range(B)]
+    assert got.cpu().tolist() == want
+
+
+def test_exact_follows_f32_rounding_on_flat_rows(gpu):
+    # equal logits: the reference's f32 running sum drifts from (k + 1) / V,
+    # which moves its pick off the exact-arithmetic one (ceil(r V) - 1); the
+    # exact path takes the reference's token, the fast path the other
+    for V, f32_pick, exact_pick in ((2616, 349, 348), (3493, 465, 466),
+                                    (128256, 17114, 17110), (139990, 18673, 18676)):
+        for dt in (torch.float32, torch.bfloat16):
+            lg = torch.full((3, V), 1.25, dtype=dt, device=gpu)
+            temps = torch.tensor([1.0, 0.5, 3.0], device=gpu)
+            assert pagedkv.sample(lg, temps).cpu().tolist() == [f32_pick] * 3, (V, dt)
+            assert pagedkv.sample(lg, temps, exact=False).cpu().tolist() == [exact_pick] * 3
+
+
+def test_exact_spiky_and_tied_rows_with_cuts(gpu):
+    # a few dominant tokens over a flat or tied tail, with top_k cutting
+    # inside a tie group and top_p thresholds the f32 running sum reaches
+    # early; every row against the f32 restatement
+    rng = np.random.default_rng(21)
+    V, B = 50000, 16
+    x = rng.integers(-2, 2, (B, V)).astype(np.float32)
+    for b in range(B):
+        x[b, rng.integers(0, V, 1 + b % 5)] = 6.0 + (b % 3)
+    temps = np.array([0.5, 1.0, 2.0, 4.0] * 4, np.float32)
+    lg = torch.from_numpy(x).to(gpu)
+    for top_k, top_p in ((None, None), (3, None), (20000, None), (None, 0.5), (None, 0.999),
+                         (100, 0.8)):
+        got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
+        want = [oracle.sample(x[b], float(temps[b]), top_k=top_k, top_p=top_p)[0]
+                for b in range(B)]
+        assert got.cpu().tolist() == want, (top_k, top_p)
+
+
+def test_exact_batch_over_several_launches(gpu):
+    # 8 bytes of scratch per logit and at most 512 MB per launch: rows of
+    # 2^20 logits run 64 per launch, so 70 rows take two launches
+    rng = np.random.default_rng(4)
+    B, V = 70, 1 << 20
+    lg = torch.randn((B, V), device=gpu, dtype=torch.bfloat16) * 2
+    temps = torch.from_numpy(rng.choice([0.0, 0.8, 1.0, 1.5], B).astype(np.float32)).to(gpu)
+    got = pagedkv.sample(lg, temps).cpu().tolist()
+    x32 = lg.float().cpu().numpy()
+    t = temps.cpu().numpy()
+    for b in (0, 1, 62, 63, 64, 65, 69):
+        assert got[b] == oracle.sample(x32[b], float(t[b]))[0], b
+
+
+def test_exact_replays_in_a_graph(gpu):
+    # the stream-ordered scratch allocation and the launch as graph nodes,
+    # replayed with eager work in between: every replay gives the eager tokens
+    rng = np.random.default_rng(10)
+    B, V = 8, 128256
+    lg = torch.from_numpy(_rows(rng, B, V)).to(gpu).to(torch.bfloat16)
+    temps = torch.full((B,), 0.9, device=gpu)
+    ref = pagedkv.sample(lg, temps).clone()
+    out = torch.empty(B, dtype=torch.int32, device=gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
         pagedkv.sample(lg, temps, out=out)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         pagedkv.sample(lg, temps, out=out)
-    for i in range(4):
+    for i in range(3):
         out.fill_(-1)
         graph.replay()
         torch.cuda.synchronize()
@@ -210,3 +336,5 @@ def test_split_path_replays_in_a_graph(gpu):
         eager = pagedkv.sample(lg[:3], temps[:3])
         torch.cuda.synchronize()
         assert torch.equal(eager, ref[:3])
+    x32 = lg.float().cpu().numpy()
+    assert ref.cpu().tolist() == [oracle.sample(x32[b], 0.9)[0] for b in range(B)]

@@ -2,8 +2,11 @@
 argmax() (crates/ai-engine-runtime/src/sample.rs:12-55) pinned by the
 reference's four KATs (crates/ai-engine-runtime/tests/sample.rs), closed
 forms and the public test vectors of the random-number primitives; and the
-library's host-side draw checked against it."""
+library's host-side draw checked against it; and the restatement of glibc's
+expf that the device's exact sampler uses, checked against the host libm on
+every float <= 0."""
 import math
+import struct
 
 import numpy as np
 import pytest
@@ -159,3 +162,52 @@ def test_vocab_of_two_to_the_24_is_refused():
     rc = L.pkv_sample(None, pagedkv.F32, 1 << 24, 1, 1 << 24, None, 0, 1.0, 42, None, None)
     assert rc == _lib.PKV_ERR_INVALID
     assert b"2^24" in L.pkv_last_error(None)
+
+
+# -- expf: the reference's f32::exp is the host C library's expf ------------
+def test_exp2_table_is_two_to_the_i_over_32():
+    # the restatement's table: 2^(i/32) rounded to double, minus i << 47
+    from decimal import Decimal, getcontext
+    getcontext().prec = 60
+    ln2 = Decimal(2).ln()
+    for i in range(32):
+        d = float((Decimal(i) / 32 * ln2).exp())  # correctly rounded
+        bits = struct.unpack("<Q", struct.pack("<d", d))[0]
+        assert oracle.exp2_tab_entry(i) == (bits - (i << 47)) % (1 << 64), i
+
+
+def test_expf_restatement_equals_host_libm_on_every_nonpositive_float():
+    # all 2^31 - 2^23 + 1 patterns from -0.0 to -inf: the sampler only
+    # evaluates exp(y - max) <= 0
+    n, first = oracle.expf_mismatches(0x80000000, 0xFF800000)
+    assert n == 0, hex(first)
+    # positive finite arguments, every 61st pattern
+    n, first = oracle.expf_mismatches(0, 0x7F7FFFFF, 61)
+    assert n == 0, hex(first)
+
+
+def test_expf_reduction_is_one_fused_multiply_add():
+    # the one non-positive input where computing r = x N / ln2 - k from the
+    # rounded product instead (an unfused build) rounds the result the other
+    # way: the host libm gives 0x1.f45326p-92, the correctly rounded value
+    # is 0x1.f45324p-92
+    x = struct.unpack("<f", struct.pack("<I", 0xC27C65D9))[0]
+    host = float(oracle.expf_host(np.array([x], np.float32))[0])
+    assert host == float.fromhex("0x1.f45326p-92") == oracle.expf_glibc(x)
+
+
+def test_flat_rows_where_f32_rounding_moves_the_pick():
+    # Equal logits: p = 1 each, the sum is V, each probability fl(1/V), and
+    # the f32 running sum drifts from (k + 1) / V.  The oracle's f32 pick
+    # equals numpy's sequential float32 cumulative sum; the exact pick is
+    # ceil(r V) - 1.  These rows tell the reference's arithmetic apart.
+    r = np.float32(R42)
+    for V, f32_pick, exact_pick in ((2616, 349, 348), (3493, 465, 466),
+                                    (128256, 17114, 17110), (139990, 18673, 18676)):
+        acc = np.add.accumulate(np.full(V, np.float32(1) / np.float32(V), np.float32),
+                                dtype=np.float32)
+        assert int(np.argmax(acc >= r)) == f32_pick
+        assert math.ceil(float(r) * V) - 1 == exact_pick
+        x = np.full(V, 1.25, np.float32)
+        assert oracle.sample(x, 1.0)[0] == f32_pick
+        assert oracle.sample(x, 1.0, precise=True)[0] == exact_pick
