@@ -936,25 +936,60 @@ constexpr int kXBits = 8;             // radix sort: bits per pass
 constexpr int kXR = 1 << kXBits;      // buckets per pass
 constexpr int kNoDelta = INT_MIN;     // f32_run: chunk without a precomputed delta
 constexpr int kDeltaCap = (1 << 24) + 1;  // deltas this large always leave the binade
+constexpr int kRunChunks = 2048;      // f32_run: chunks at most
+constexpr int kXU = 8;                // 64-element batches of loads in flight per wave
 
 struct ExactSmem {
-  unsigned int off[kSW][kXR];  // radix pass: per-wave digit counts, then positions
+  unsigned int off[kSW][kXR];       // radix pass: per-wave digit counts, then positions
   unsigned int wtot[kSW];
-  double dsum[kST];            // f32_run: chunk sums, then their exclusive prefix
-  int ce[kST];                 // f32_run: binade the chunk's delta assumes
-  int cd0[kST], cd1[kST];      // f32_run: its delta for an even / odd start
-  float s;                     // f32_run result: the sum reached
-  int pos;                     //   and the number of elements it took
+  float wsum[kSW];
+  float csum[kRunChunks];           // f32_run: chunk sums, then exclusive prefixes
+  int ce[kRunChunks];               // binade the chunk's delta assumes (kNoDelta: none)
+  int cd0[kRunChunks], cd1[kRunChunks];  // its delta for an even / odd start
+  float s;                          // f32_run result: the sum reached
+  int pos;                          //   and the number of elements it took
   int flag;
 };
 
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+// Sums over the wave; every lane receives the total (DPP row rotations, then
+// the gfx950 permlane swaps across rows).
+__device__ __forceinline__ int wsum_i32(int x) {
+  x += dpp_i<0x128>(x);
+  x += dpp_i<0x124>(x);
+  x += dpp_i<0x122>(x);
+  x += dpp_i<0x121>(x);
+  const auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  x = (int)(a[0] + a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return (int)(b[0] + b[1]);
+}
+__device__ __forceinline__ float wsum_f32(float x) { return swap32_sum(swap16_sum(row_sum16(x))); }
+
+// Lanes of the batch whose key has this lane's digit d (valid lanes only).
+__device__ __forceinline__ unsigned long long digit_match(uint32_t d, bool valid) {
+  unsigned long long match = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < kXBits; ++b) {
+    const bool bit = (d >> b) & 1u;
+    const unsigned long long bal = __ballot(bit);
+    match &= bit ? bal : ~bal;
+  }
+  return match;
+}
+
 // One stable pass of the LSD radix sort: src[0, n) -> dst by key bits
 // [shift, shift + 8).  Wave w owns a contiguous segment, read 64 keys at a
-// time in order; a key's rank among the keys of its batch with the same
-// digit comes from eight ballots, its base from the wave's running position
-// for the digit (per-wave counts, scanned digit-major, wave-minor).  When
-// every key has the same digit the pass would move nothing: it returns
-// false and leaves dst alone.  Ends with a barrier.
+// time in order.  Within a batch, the keys sharing a digit are found with
+// eight ballots: the group's highest lane adds the group's size to the
+// wave's count for the digit (no contended atomics), and in the scatter a
+// key's rank in its group plus the wave's running position for the digit
+// (counts scanned digit-major, wave-minor) gives its place.  When every key
+// has the same digit the pass would move nothing: it returns false and
+// leaves dst alone.  Ends with a barrier.
 __device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, int n, int shift) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int seg = ((n + kSW - 1) / kSW + 63) / 64 * 64;
@@ -962,7 +997,21 @@ __device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, in
   for (int i = tid; i < kSW * kXR; i += kST) (&xs.off[0][0])[i] = 0u;
   if (tid == 0) xs.flag = 0;
   __syncthreads();
-  for (int i = w0 + lane; i < w1; i += 64) atomicAdd(&xs.off[wv][(src[i] >> shift) & (kXR - 1)], 1u);
+  for (int i0 = w0; i0 < w1; i0 += 64 * kXU) {
+    uint32_t kk[kXU];
+#pragma unroll
+    for (int u = 0; u < kXU; ++u) {
+      const int i = i0 + 64 * u + lane;
+      kk[u] = i < w1 ? src[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kXU; ++u) {
+      const bool valid = i0 + 64 * u + lane < w1;
+      const uint32_t d = (kk[u] >> shift) & (kXR - 1);
+      const unsigned long long match = digit_match(d, valid);
+      if (valid && (match >> lane) == 1ull) xs.off[wv][d] += (unsigned int)__popcll(match);
+    }
+  }
   __syncthreads();
   unsigned int c = 0, incl = 0;
   if (tid < kXR) {  // digit tid: prefix over the waves, then over the digits
@@ -989,28 +1038,42 @@ __device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, in
     for (int w = 0; w < kSW; ++w) xs.off[w][tid] += base;
   }
   __syncthreads();
-  for (int i0 = w0; i0 < w1; i0 += 64) {
-    const int i = i0 + lane;
-    const bool valid = i < w1;
-    const uint32_t k = valid ? src[i] : 0u;
-    const uint32_t d = (k >> shift) & (kXR - 1);
-    unsigned long long match = __ballot(valid);
+  for (int i0 = w0; i0 < w1; i0 += 64 * kXU) {
+    uint32_t kk[kXU];
 #pragma unroll
-    for (int b = 0; b < kXBits; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const unsigned long long bal = __ballot(bit);
-      match &= bit ? bal : ~bal;
+    for (int u = 0; u < kXU; ++u) {
+      const int i = i0 + 64 * u + lane;
+      kk[u] = i < w1 ? src[i] : 0u;
     }
-    const unsigned int rank = (unsigned int)__popcll(match & ((1ull << lane) - 1ull));
-    const unsigned int cnt = (unsigned int)__popcll(match);
-    const unsigned int base = xs.off[wv][d];
-    if (valid) {
-      dst[base + rank] = k;
-      if (rank + 1u == cnt) xs.off[wv][d] = base + cnt;
+#pragma unroll
+    for (int u = 0; u < kXU; ++u) {
+      const bool valid = i0 + 64 * u + lane < w1;
+      const uint32_t k = kk[u];
+      const uint32_t d = (k >> shift) & (kXR - 1);
+      const unsigned long long match = digit_match(d, valid);
+      const unsigned int rank = (unsigned int)__popcll(match & ((1ull << lane) - 1ull));
+      const unsigned int base = xs.off[wv][d];
+      if (valid) {
+        dst[base + rank] = k;
+        if ((match >> lane) == 1ull) xs.off[wv][d] = base + rank + 1u;
+      }
     }
   }
   __syncthreads();
   return true;
+}
+
+// Sorts the keys in a[0, n) ascending by their low `bits` bits (the others
+// are zero); b is scratch of n keys.  Returns the array holding the result.
+__device__ uint32_t* radix_sort(ExactSmem& xs, uint32_t* a, uint32_t* b, int n, int bits) {
+  for (int shift = 0; shift < bits; shift += kXBits) {
+    if (radix_pass(xs, a, b, n, shift)) {
+      uint32_t* t = a;
+      a = b;
+      b = t;
+    }
+  }
+  return a;
 }
 
 // In binade e (sums s in [2^e, 2^(e+1)), spacing u = 2^(e-23)), adding v >= 0
@@ -1037,6 +1100,15 @@ __device__ __forceinline__ void split_at(float v, int e, int& a, int& rnd, bool&
   }
 }
 
+// (d0, d1) then (b0, b1): the deltas of two consecutive runs composed, for
+// an even / odd start (the second run starts at the parity the first left).
+__device__ __forceinline__ void compose(int& d0, int& d1, int b0, int b1) {
+  const int n0 = d0 + ((d0 & 1) ? b1 : b0);
+  const int n1 = d1 + ((d1 & 1) ? b0 : b1);
+  d0 = min(n0, kDeltaCap);
+  d1 = min(n1, kDeltaCap);
+}
+
 // The f32 running sum s_{i+1} = fl(s_i + v_i), s_0 = 0, over v[0, len) (in
 // global memory, written before the call), up to and including the first i
 // with s_{i+1} >= thr (use_thr).  Result in xs.s (the sum reached) and
@@ -1045,63 +1117,135 @@ __device__ __forceinline__ void split_at(float v, int e, int& a, int& rnd, bool&
 // While the sum stays in one binade e, every step is an integer addition in
 // units of u = 2^(e-23) (split_at), so a run of steps is the sum of their
 // increments -- except at exact ties, where round-half-even makes the step
-// depend on the parity of the running count; a chunk is therefore described
-// by two deltas, one per start parity, and deltas compose.  Each thread
-// takes a contiguous chunk, guesses the binade its running sum starts in
-// from the exact (double) prefix sum, and computes its deltas for that
-// binade.  Wave 0 then walks the chunks in order, applying runs of chunks
-// whose guess matches the actual sum by a composition scan, provided the
-// result stays in the binade and below thr; any other chunk (first chunk,
-// wrong guess, a binade crossing or the threshold inside it, a value that is
-// not finite) is walked element by element with real f32 additions.  The
-// guesses only decide the speed: every delta used is checked against the
-// actual running sum.  Call from all threads; ends with a barrier.
+// depend on the parity of the running count; a run is therefore described
+// by two deltas, one per start parity, and such deltas compose.  The
+// sequence is cut into chunks of C consecutive elements (C a multiple of
+// 64, at most kRunChunks chunks), each handled by one wave with coalesced
+// loads: a first sweep sums the chunks (float, only for guesses), a scan
+// gives each chunk a guess of the binade its running sum starts in, and a
+// second sweep computes the chunk's deltas for that binade (a wave sum of
+// the increments per 64 elements; a composition scan across the lanes when
+// the 64 hold a tie).  Wave 0 then walks the chunks in order, applying runs
+// of chunks whose guess matches the actual sum by a composition scan across
+// lanes, provided the result stays in the binade and below thr; any other
+// chunk (the first, a wrong guess, a binade crossing or the threshold inside
+// it, a value that is not finite) is walked element by element with real
+// f32 additions.  The guesses only decide the speed: every delta used is
+// checked against the actual running sum.  Call from all threads; ends with
+// a barrier.
 __device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, float thr) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int L = (len + kST - 1) / kST;
-  const int lo = min(len, tid * L), hi = min(len, lo + L);
-  double sum = 0.0;
-  bool finite = true;
-  for (int i = lo; i < hi; ++i) {
-    const float x = v[i];
-    finite &= x >= 0.0f && x <= 3.402823466e38f;
-    sum += (double)x;
-  }
-  // exclusive prefix of the chunk sums
-  double incl = sum;
-  for (int d = 1; d < 64; d <<= 1) {
-    const double o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) xs.dsum[wv] = incl;
-  __syncthreads();
-  double pre = incl - sum;
-  for (int w = 0; w < wv; ++w) pre += xs.dsum[w];
-  __syncthreads();
-  // Chunks past the threshold (with a margin far above any f32 drift) are
-  // never reached by the walk before it stops; they get no delta.
-  int e = kNoDelta, d0 = 0, d1 = 0;
-  if (finite && hi > lo && pre > 0.0 && !(use_thr && pre > (double)thr * 1.0625 + 1e-30)) {
-    int ex;
-    (void)frexp(pre, &ex);
-    e = ex - 1;
-    int p0 = 0, p1 = 1;
-    for (int i = lo; i < hi && d0 < kDeltaCap && d1 < kDeltaCap; ++i) {
-      int a, rnd;
-      bool tie;
-      split_at(v[i], e, a, rnd, tie);
-      const int q0 = tie ? a + ((p0 + a) & 1) : a + rnd;
-      const int q1 = tie ? a + ((p1 + a) & 1) : a + rnd;
-      d0 = min(d0 + q0, kDeltaCap);
-      d1 = min(d1 + q1, kDeltaCap);
-      p0 = (p0 + q0) & 1;
-      p1 = (p1 + q1) & 1;
+  const int C = max(64, ((len + kRunChunks - 1) / kRunChunks + 63) / 64 * 64);
+  const int nch = (len + C - 1) / C;
+  // Wave w owns the contiguous chunks [cw0, cw1) and streams them kXU
+  // batches of 64 at a time; batch b of the range belongs to chunk
+  // cw0 + b / (C / 64).
+  const int cpw = (nch + kSW - 1) / kSW;
+  const int cw0 = min(nch, wv * cpw), cw1 = min(nch, cw0 + cpw);
+  const int bpc = C / 64;  // batches per chunk
+  const int nb = (cw1 - cw0) * bpc;
+  // sweep 1: chunk sums (-1: the chunk holds a value that is not finite)
+  {
+    float acc = 0.0f;
+    bool fin = true;
+    for (int b0 = 0; b0 < nb; b0 += kXU) {
+      float xv[kXU];
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        const int i = cw0 * C + (b0 + u) * 64 + lane;
+        xv[u] = b0 + u < nb && i < len ? v[i] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        if (b0 + u >= nb) break;  // uniform
+        fin &= xv[u] >= 0.0f && xv[u] <= 3.402823466e38f;
+        acc += xv[u];
+        if ((b0 + u + 1) % bpc == 0) {  // the chunk's last batch
+          const float t = wsum_f32(acc);
+          if (lane == 0) xs.csum[cw0 + (b0 + u) / bpc] = __ballot(!fin) ? -1.0f : t;
+          acc = 0.0f;
+          fin = true;
+        }
+      }
     }
-    if (d0 >= kDeltaCap || d1 >= kDeltaCap) e = kNoDelta;
   }
-  xs.ce[tid] = e;
-  xs.cd0[tid] = d0;
-  xs.cd1[tid] = d1;
+  __syncthreads();
+  // exclusive prefix over the chunks (a non-finite chunk poisons the rest:
+  // their guesses become -1, i.e. no delta)
+  {
+    const int c0 = 2 * tid;
+    const float x0 = c0 < nch ? xs.csum[c0] : 0.0f, x1 = c0 + 1 < nch ? xs.csum[c0 + 1] : 0.0f;
+    const float mine = (x0 < 0.0f || x1 < 0.0f) ? -INFINITY : x0 + x1;
+    float in = mine;
+    for (int d = 1; d < 64; d <<= 1) {
+      const float o = __shfl_up(in, d, 64);
+      if (lane >= d) in += o;
+    }
+    if (lane == 63) xs.wsum[wv] = in;
+    __syncthreads();
+    float pre = in - mine;
+    for (int w = 0; w < wv; ++w) pre += xs.wsum[w];
+    if (!(mine > -INFINITY)) pre = -INFINITY;
+    if (c0 < nch) xs.csum[c0] = pre;
+    if (c0 + 1 < nch) xs.csum[c0 + 1] = x0 < 0.0f ? -INFINITY : pre + x0;
+    __syncthreads();
+  }
+  // sweep 2: each chunk's deltas for its guessed binade (chunks past the
+  // threshold, by a margin far above any f32 drift, are never reached
+  // before the walk stops: no delta)
+  {
+    int e = kNoDelta, d0 = 0, d1 = 0;
+    for (int b0 = 0; b0 < nb; b0 += kXU) {
+      float xv[kXU];
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        const int i = cw0 * C + (b0 + u) * 64 + lane;
+        xv[u] = b0 + u < nb && i < len ? v[i] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        const int b = b0 + u;
+        if (b >= nb) break;  // uniform
+        const int c = cw0 + b / bpc;
+        if (b % bpc == 0) {  // the chunk's first batch: its guess
+          const float pre = xs.csum[c];
+          e = pre > 0.0f && pre < 3.402823466e38f && !(use_thr && pre > thr * 1.0625f)
+                  ? (int)((__float_as_uint(pre) >> 23) & 255u) - 127
+                  : kNoDelta;
+          d0 = d1 = 0;
+        }
+        if (e != kNoDelta && d0 < kDeltaCap && d1 < kDeltaCap) {
+          int a, rnd;
+          bool tie;
+          split_at(xv[u], e, a, rnd, tie);
+          int q0, q1;
+          if (!__ballot(tie)) {
+            q0 = q1 = min(wsum_i32(a + rnd), kDeltaCap);  // 64 (2^24 + 2) < 2^31
+          } else {  // composition scan across the lanes: lane 63 holds the batch
+            int p0 = tie ? a + (a & 1) : a + rnd;
+            int p1 = tie ? a + ((a + 1) & 1) : a + rnd;
+            for (int k = 1; k < 64; k <<= 1) {
+              const int r0 = __shfl_up(p0, k, 64), r1 = __shfl_up(p1, k, 64);
+              if (lane >= k) {
+                int n0 = r0, n1 = r1;
+                compose(n0, n1, p0, p1);
+                p0 = n0;
+                p1 = n1;
+              }
+            }
+            q0 = readlane_i(p0, 63);
+            q1 = readlane_i(p1, 63);
+          }
+          compose(d0, d1, q0, q1);
+        }
+        if ((b + 1) % bpc == 0 && lane == 0) {  // the chunk's last batch
+          xs.ce[c] = (d0 >= kDeltaCap || d1 >= kDeltaCap) ? kNoDelta : e;
+          xs.cd0[c] = d0;
+          xs.cd1[c] = d1;
+        }
+      }
+    }
+  }
   __syncthreads();
 
   if (wv == 0) {
@@ -1110,7 +1254,7 @@ __device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, fl
     bool done = false;
     // element-by-element walk of chunk c (wave-uniform)
     auto walk = [&](int c) {
-      const int clo = min(len, c * L), chi = min(len, clo + L);
+      const int clo = c * C, chi = min(len, clo + C);
       for (int i0 = clo; i0 < chi && !done; i0 += 64) {
         const float x = i0 + lane < chi ? v[i0 + lane] : 0.0f;
         const int m = min(64, chi - i0);
@@ -1124,10 +1268,13 @@ __device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, fl
         }
       }
     };
-    for (int g = 0; g < kST && g * L < len && !done; g += 64) {
-      const int ec = xs.ce[g + lane], c0 = xs.cd0[g + lane], c1 = xs.cd1[g + lane];
+    for (int g = 0; g < nch && !done; g += 64) {
+      const bool have = g + lane < nch;
+      const int ec = have ? xs.ce[g + lane] : kNoDelta;
+      const int c0 = have ? xs.cd0[g + lane] : 0, c1 = have ? xs.cd1[g + lane] : 0;
+      const int gend = min(64, nch - g);
       int start = 0;
-      while (start < 64 && !done) {
+      while (start < gend && !done) {
         const uint32_t sb = __float_as_uint(s);
         const int sE = (int)((sb >> 23) & 255u);
         const bool s_normal = sE >= 1 && sE <= 254 && !(sb >> 31);
@@ -1145,10 +1292,10 @@ __device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, fl
         for (int k = 1; k < 64; k <<= 1) {
           const int b0 = __shfl_up(a0, k, 64), b1 = __shfl_up(a1, k, 64);
           if (lane >= k) {
-            const int n0 = b0 + ((b0 & 1) ? a1 : a0);
-            const int n1 = b1 + ((b1 & 1) ? a0 : a1);
-            a0 = min(n0, kDeltaCap);
-            a1 = min(n1, kDeltaCap);
+            int n0 = b0, n1 = b1;
+            compose(n0, n1, a0, a1);
+            a0 = n0;
+            a1 = n1;
           }
         }
         const int n = (int)((sb & 0x7fffffu) | 0x800000u);
@@ -1175,17 +1322,29 @@ __device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, fl
   __syncthreads();
 }
 
-// Sorts the keys in a[0, n) ascending (b: scratch of n keys); returns the
-// array that holds the result.
-__device__ uint32_t* radix_sort(ExactSmem& xs, uint32_t* a, uint32_t* b, int n) {
-  for (int shift = 0; shift < 32; shift += kXBits) {
-    if (radix_pass(xs, a, b, n, shift)) {
-      uint32_t* t = a;
-      a = b;
-      b = t;
-    }
+// Sort key of a logit for the exact path (the logit negated when T < 0, so
+// that larger keys give larger y = x / T): larger value -> larger key, -0
+// and +0 equal; 16 significant bits for 16-bit logits.
+template <int DT>
+__device__ __forceinline__ uint32_t xkey(float x) {
+  if constexpr (DT == PKV_F32) {
+    return order_key(x);
+  } else {
+    uint32_t b = DT == PKV_BF16 ? (__float_as_uint(x) >> 16)
+                                : (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+    if ((b & 0x7fffu) == 0u) b = 0u;
+    return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
   }
-  return a;
+}
+template <int DT>
+__device__ __forceinline__ float xkey_value(uint32_t k) {
+  if constexpr (DT == PKV_F32) {
+    return key_value(k);
+  } else {
+    const uint32_t b = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+    return DT == PKV_BF16 ? __uint_as_float(b << 16)
+                          : (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+  }
 }
 
 struct ExactArgs {
@@ -1219,41 +1378,68 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   }
   uint32_t* ka = a.scratch + (size_t)blockIdx.x * 2 * (size_t)V;
   uint32_t* kb = ka + V;
-  // descending y = ascending complemented order key; -0.0 and +0.0 share a key
-  for_each<DT, VEC>(x, V, [&](int i, float v) { ka[i] = ~order_key(v / T); });
+  // The logits sorted descending (ascending complemented keys; negated for
+  // T < 0).  y = fl(x / T) is monotone in x, so the sorted logits give the
+  // reference's sequence of y values (equal y adjacent), and only the values
+  // enter the sums; no division is needed to sort.
+  constexpr int kBits = DT == PKV_F32 ? 32 : 16;
+  constexpr uint32_t kMask = DT == PKV_F32 ? 0xffffffffu : 0xffffu;
+  const bool neg = T < 0.0f;
+  for_each<DT, VEC>(x, V, [&](int i, float v) { ka[i] = kMask & ~xkey<DT>(neg ? -v : v); });
   __syncthreads();
-  const uint32_t* sk = radix_sort(xs, ka, kb, V);
+  const uint32_t* sk = radix_sort(xs, ka, kb, V, kBits);
   float* p = reinterpret_cast<float*>(sk == ka ? kb : ka);
+  auto y_at = [&](int i) {
+    const float xp = xkey_value<DT>(kMask & ~sk[i]);
+    return (neg ? -xp : xp) / T;
+  };
 
   int len = a.top_k > 0 && a.top_k < V ? a.top_k : V;  // probs.truncate(k)
-  const float max_x = key_value(~sk[0]);
-  for (int i = tid; i < len; i += kST) p[i] = expf_glibc(key_value(~sk[i]) - max_x);
+  const float max_x = y_at(0);
+  for (int i0 = tid; i0 < len; i0 += kXU * kST) {
+    uint32_t kk[kXU];
+#pragma unroll
+    for (int u = 0; u < kXU; ++u) kk[u] = i0 + u * kST < len ? sk[i0 + u * kST] : 0u;
+#pragma unroll
+    for (int u = 0; u < kXU; ++u) {
+      if (i0 + u * kST >= len) break;
+      const float xp = xkey_value<DT>(kMask & ~kk[u]);
+      p[i0 + u * kST] = expf_glibc((neg ? -xp : xp) / T - max_x);
+    }
+  }
   __syncthreads();
   f32_run(xs, p, len, false, 0.0f);  // sum += p
-  const float sum = xs.s;
-  for (int i = tid; i < len; i += kST) p[i] = p[i] / sum;
-  __syncthreads();
+  // p /= divisor over [0, n), kXU loads in flight per thread
+  auto divide = [&](int n, float divisor) {
+    for (int i0 = tid; i0 < n; i0 += kXU * kST) {
+      float pv[kXU];
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) pv[u] = i0 + u * kST < n ? p[i0 + u * kST] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < kXU; ++u)
+        if (i0 + u * kST < n) p[i0 + u * kST] = pv[u] / divisor;
+    }
+    __syncthreads();
+  };
+  divide(len, xs.s);
   if (a.top_p == a.top_p) {  // Some(top_p)
     f32_run(xs, p, len, true, a.top_p);
-    const int cutoff = xs.pos;
-    const float s = xs.s;  // equals the f32 sum of the kept probabilities
-    len = cutoff;
-    for (int i = tid; i < len; i += kST) p[i] = p[i] / s;
-    __syncthreads();
+    len = xs.pos;     // cutoff
+    divide(len, xs.s);  // xs.s equals the f32 sum of the kept probabilities
   }
   f32_run(xs, p, len, true, a.r);  // acc += prob until r <= acc
   const int j = xs.pos - 1;  // xs.pos = len when acc never reaches r: probs.last()
-  // the token at sorted position j: its value's first sorted position, then
-  // that many tokens further among the equal ones, in index order
-  const uint32_t kj = sk[j];
+  // the token at sorted position j: the first sorted position of its y,
+  // then that many tokens further among the equal ones, in index order
+  const uint32_t kj = order_key(y_at(j));
   int lo = 0, hi = j;
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (sk[mid] < kj) lo = mid + 1;
+    if (order_key(y_at(mid)) > kj) lo = mid + 1;
     else hi = mid;
   }
   Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
-  const int tok = nth_tied<false>(sm, rw, ~kj, (unsigned long long)(j - lo + 1));
+  const int tok = nth_tied<false>(sm, rw, kj, (unsigned long long)(j - lo + 1));
   if (tid == 0) a.tokens[row] = tok;
 }
 

@@ -625,13 +625,15 @@ def gather_bench(args, dev) -> int:
 
 
 def sample_bench(args, dev) -> int:
-    """Token selection on the device (pkv_sample; sample.rs:12-55 as the
-    engine calls it, engine.rs:145-162): 256 rows of Llama-3's 128,256-entry
-    vocabulary in bf16, every row sampled at temperature 0.8 (seed 42, no
-    top-k / top-p, as the engine's sample_cfg).  value = rows/s; roofline =
-    one read of the logits per launch against HBM peak (the kernel makes
-    several passes over each row, from L2 / the Infinity Cache); greedy rows
-    are timed beside it."""
+    """Token selection on the device (sample.rs:12-55 as the engine calls it,
+    engine.rs:145-162): 256 rows of Llama-3's 128,256-entry vocabulary in
+    bf16, every row sampled at temperature 0.8 (seed 42, no top-k / top-p, as
+    the engine's sample_cfg).  value = rows/s of pkv_sample_exact, which
+    reproduces sample.rs's f32 arithmetic bit for bit (checked against the
+    oracle's f32 restatement); the faster pkv_sample (exact probability mass,
+    equal tokens except where the reference's f32 rounding alone moves the
+    pick) and greedy rows are timed beside it.  roofline = one read of the
+    logits per launch against HBM peak."""
     import numpy as np
     import torch
 
@@ -647,25 +649,28 @@ def sample_bench(args, dev) -> int:
     lib = pagedkv.lib()
     sp = int(torch.cuda.current_stream(dev).cuda_stream) or None
 
-    def run(t):
-        rc = lib.pkv_sample(logits.data_ptr(), pagedkv.BF16, V, B, V,
-                            t.data_ptr() if t is not None else None, 0, 1.0, 42,
-                            out.data_ptr(), sp)
+    def run(t, exact=False, rows=B, o=None):
+        fn = lib.pkv_sample_exact if exact else lib.pkv_sample
+        rc = fn(logits.data_ptr(), pagedkv.BF16, V, rows, V,
+                t.data_ptr() if t is not None else None, 0, float("nan") if exact else 1.0, 42,
+                (o if o is not None else out).data_ptr(), sp)
         if rc:
             pagedkv._lib.check(rc, None)
 
-    def time_it(t):
+    def time_it(t, exact=False, rows=B, o=None):
         for _ in range(max(1, args.warmup)):
-            run(t)
+            run(t, exact, rows, o)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(args.steps):
-            run(t)
+            run(t, exact, rows, o)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps
 
+    ms_exact = time_it(temps, exact=True)
+    got_exact = out.cpu().numpy().copy()
     ms = time_it(temps)
     got = out.cpu().numpy().copy()
     ms_greedy = time_it(None)
@@ -673,43 +678,33 @@ def sample_bench(args, dev) -> int:
     x32 = logits.float().cpu().numpy()
     # parity on a few rows: greedy exact; sampled equal to the exact-arithmetic
     # restatement unless its running sum is within 1e-6 of r
+    # and the exact path equal to the f32 restatement (the reference's arithmetic)
     ok = True
     for b in range(0, B, 37):
         ok &= int(greedy[b]) == oracle.argmax(x32[b])
         tok, margin = oracle.sample(x32[b], 0.8, precise=True)
         ok &= int(got[b]) == tok or margin < 1e-6
-    log(f"[bench] sample: {ms * 1e3:.1f} us sampled, {ms_greedy * 1e3:.1f} us greedy "
-        f"for {B} x {V} bf16 rows; oracle check {'ok' if ok else 'FAILED'}")
+        ok &= int(got_exact[b]) == oracle.sample(x32[b], 0.8)[0]
+    log(f"[bench] sample: exact {ms_exact * 1e3:.1f} us, fast {ms * 1e3:.1f} us sampled, "
+        f"{ms_greedy * 1e3:.1f} us greedy for {B} x {V} bf16 rows; "
+        f"oracle check {'ok' if ok else 'FAILED'}")
     if not ok:
         print(json.dumps({"error": "token selection differs from the oracle"}))
         return 1
     rbytes = B * V * 2 + B * 4
     # small batches (the split path: each row over several workgroups), the
     # first rows of the same logits; checked against the full batch's tokens
-    small = {}
+    small, small_exact = {}, {}
     for sb in (1, 8, 32):
         o2 = torch.empty(sb, dtype=torch.int32, device=dev)
-
-        def run_small(sb=sb, o2=o2):
-            rc = lib.pkv_sample(logits.data_ptr(), pagedkv.BF16, V, sb, V, temps.data_ptr(), 0,
-                                1.0, 42, o2.data_ptr(), sp)
-            if rc:
-                pagedkv._lib.check(rc, None)
-        for _ in range(max(1, args.warmup)):
-            run_small()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            run_small()
-        e1.record()
-        torch.cuda.synchronize()
-        same = bool(np.array_equal(o2.cpu().numpy(), got[:sb]))
-        small[str(sb)] = {"us": round(e0.elapsed_time(e1) / args.steps * 1e3, 2),
-                          "same_tokens_as_full_batch": same}
-        ok &= same
+        for exact, dst, ref in ((False, small, got), (True, small_exact, got_exact)):
+            us = time_it(temps, exact, sb, o2) * 1e3
+            same = bool(np.array_equal(o2.cpu().numpy(), ref[:sb]))
+            dst[str(sb)] = {"us": round(us, 2), "same_tokens_as_full_batch": same}
+            ok &= same
     log(f"[bench] sample, small batches (us): "
-        + ", ".join(f"{k} rows {v['us']}" for k, v in small.items()))
+        + ", ".join(f"{k} rows exact {small_exact[k]['us']} / fast {v['us']}"
+                    for k, v in small.items()))
     if not ok:
         print(json.dumps({"error": "small-batch tokens differ from the full batch's"}))
         return 1
@@ -723,20 +718,26 @@ def sample_bench(args, dev) -> int:
                          f"sample.rs) of one {V}-entry row, {n} passes of {per * 1e3:.1f} ms"}
     res = {
         "metric": "on-device token selection rows/s (sample.rs at T=0.8), Llama-3 vocabulary, 1 GPU",
-        "value": round(B / (ms / 1e3), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "value": round(B / (ms_exact / 1e3), 1), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_exact, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0, 9) logits)",
         "config": {"workload": f"sample: {B} rows x {V} logits, temperature 0.8, seed 42",
+                   "entry_point": "pkv_sample_exact (bit-identical to sample.rs)",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(rbytes / (ms / 1e3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(rbytes / (ms_exact / 1e3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(rbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "pkv::sample_kernel", "kernel_avg_us": round(ms * 1e3, 2),
+                     "frac": round(rbytes / (ms_exact / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "pkv::sample_exact_kernel",
+                     "kernel_avg_us": round(ms_exact * 1e3, 2),
                      "algorithmic_bytes_per_launch": rbytes},
+        "small_batches_exact": small_exact,
+        "fast": {"entry_point": "pkv_sample (exact probability mass; equal tokens except where "
+                                "the reference's f32 rounding alone moves the pick)",
+                 "us": round(ms * 1e3, 2), "rows_per_s": round(B / (ms / 1e3), 1),
+                 "GBps": round(rbytes / (ms / 1e3) / 1e9, 1), "small_batches": small},
         "greedy": {"us": round(ms_greedy * 1e3, 2),
                    "GBps": round(rbytes / (ms_greedy / 1e3) / 1e9, 1)},
-        "small_batches_sampled": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
