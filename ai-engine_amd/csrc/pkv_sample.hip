@@ -396,7 +396,7 @@ __device__ Sel select_low(SampleSmem& sm, const Row<DT, VEC>& rw, unsigned long 
 // block-wide exclusive scan of the per-thread counts, in index order, finds
 // the thread holding the n-th match.
 template <bool FILTER, int DT, bool VEC>
-__device__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
+__device__ __forceinline__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, uint32_t key,
                         unsigned long long n, int lo = 0, int hi = -1) {
   if (hi < 0) hi = rw.V;  // the walk covers [lo, hi); lo is a multiple of 8
   constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
@@ -481,7 +481,7 @@ __device__ __forceinline__ unsigned long long ties_needed(const Sel& s) {
 // maximum wins; NaN is never taken): (value, index), index INT_MAX when no
 // value exceeds -inf.  The result is valid in thread 0.
 template <int DT, bool VEC>
-__device__ void block_argmax(SampleSmem& sm, const char* x, int lo, int hi, float& bv, int& bi) {
+__device__ __forceinline__ void block_argmax(SampleSmem& sm, const char* x, int lo, int hi, float& bv, int& bi) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   bv = -INFINITY;
   bi = INT_MAX;
@@ -990,7 +990,7 @@ __device__ __forceinline__ unsigned long long digit_match(uint32_t d, bool valid
 // (counts scanned digit-major, wave-minor) gives its place.  When every key
 // has the same digit the pass would move nothing: it returns false and
 // leaves dst alone.  Ends with a barrier.
-__device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, int n, int shift) {
+__device__ __forceinline__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, int n, int shift) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int seg = ((n + kSW - 1) / kSW + 63) / 64 * 64;
   const int w0 = min(n, wv * seg), w1 = min(n, w0 + seg);
@@ -1065,7 +1065,7 @@ __device__ bool radix_pass(ExactSmem& xs, const uint32_t* src, uint32_t* dst, in
 
 // Sorts the keys in a[0, n) ascending by their low `bits` bits (the others
 // are zero); b is scratch of n keys.  Returns the array holding the result.
-__device__ uint32_t* radix_sort(ExactSmem& xs, uint32_t* a, uint32_t* b, int n, int bits) {
+__device__ __forceinline__ uint32_t* radix_sort(ExactSmem& xs, uint32_t* a, uint32_t* b, int n, int bits) {
   for (int shift = 0; shift < bits; shift += kXBits) {
     if (radix_pass(xs, a, b, n, shift)) {
       uint32_t* t = a;
@@ -1133,7 +1133,7 @@ __device__ __forceinline__ void compose(int& d0, int& d1, int b0, int b1) {
 // f32 additions.  The guesses only decide the speed: every delta used is
 // checked against the actual running sum.  Call from all threads; ends with
 // a barrier.
-__device__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, float thr) {
+__device__ __forceinline__ void f32_run(ExactSmem& xs, const float* v, int len, bool use_thr, float thr) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int C = max(64, ((len + kRunChunks - 1) / kRunChunks + 63) / 64 * 64);
   const int nch = (len + C - 1) / C;
