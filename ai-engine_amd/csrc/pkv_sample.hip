@@ -1443,6 +1443,426 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   if (tid == 0) a.tokens[row] = tok;
 }
 
+// ---- 16-bit logits: the sorted sequence as runs of equal values -------------
+// A 16-bit logit takes one of 65,536 values, so the descending sequence the
+// reference sorts is, without sorting, the list of distinct values (an LDS
+// histogram of the 16-bit sort keys, read from the largest key down), each
+// repeated as often as it occurs: a run.  Everything after the sort is a
+// function of that sequence: the maximum, p = exp(y - max) once per run, and
+// the f32 running sums, where c copies of one value added while the sum stays
+// in one binade are c equal integer steps (for a tie, a first step that
+// depends on the parity of the running count, then c - 1 equal even steps),
+// so a run has closed-form deltas (run_delta) and its binade crossings and
+// its threshold crossing are found by arithmetic (run_step).  f32_runs walks
+// runs as f32_run walks elements.  A bf16 row of N(0, 9) logits has ~3k
+// runs for 128k logits.
+
+constexpr int kHalfKeys = 32768;  // histogram: one half of the 16-bit key space per pass
+constexpr int kMaxRuns = 65536;
+
+struct RunSmem {
+  float csum[kRunChunks];  // chunk sums, then exclusive prefixes (guesses)
+  int ce[kRunChunks];      // binade the chunk's delta assumes (kNoDelta: none)
+  int cd0[kRunChunks], cd1[kRunChunks];
+  float wsum[kSW];
+  float s;    // f32_runs result: the sum reached,
+  int r_end;  //   the run where the threshold stopped it (R: not reached)
+  int k_end;  //   and how many copies of that run it took
+  int R;
+};
+union RunLds {
+  unsigned int hist[kHalfKeys];
+  struct {
+    SampleSmem sm;
+    RunSmem rs;
+  } x;
+};
+
+// A row's runs in descending order of value (global scratch, kMaxRuns each).
+struct RunArrays {
+  uint32_t* key;    // 16-bit order key of the (sign-adjusted) logit
+  uint32_t* cnt;    // copies
+  uint32_t* start;  // position of the first copy in the sorted sequence
+  float* val;       // what the current running sum adds per copy
+};
+
+// Exclusive prefix of one value per thread over the workgroup; wtmp: kSW
+// scratch words outside any buffer the caller is using.  Ends with a barrier.
+__device__ __forceinline__ unsigned int block_excl_scan(unsigned int v, unsigned int* wtmp,
+                                                        unsigned int& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  unsigned int in = v;
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned int o = (unsigned int)__shfl_up((int)in, d, 64);
+    if (lane >= d) in += o;
+  }
+  if (lane == 63) wtmp[wv] = in;
+  __syncthreads();
+  unsigned int pre = in - v;
+  total = 0;
+  for (int w = 0; w < kSW; ++w) {
+    const unsigned int t = wtmp[w];
+    if (w < wv) pre += t;
+    total += t;
+  }
+  __syncthreads();
+  return pre;
+}
+
+// Exclusive prefix of the chunk sums csum[0, nch) (nch <= 2 kST), in place;
+// a negative entry (a chunk that is not finite) makes every later prefix
+// -inf (no guess).  Ends with a barrier.
+__device__ __forceinline__ void chunk_prefix(float* csum, float* wsum, int nch) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c0 = 2 * tid;
+  const float x0 = c0 < nch ? csum[c0] : 0.0f, x1 = c0 + 1 < nch ? csum[c0 + 1] : 0.0f;
+  const float mine = (x0 < 0.0f || x1 < 0.0f) ? -INFINITY : x0 + x1;
+  float in = mine;
+  for (int d = 1; d < 64; d <<= 1) {
+    const float o = __shfl_up(in, d, 64);
+    if (lane >= d) in += o;
+  }
+  if (lane == 63) wsum[wv] = in;
+  __syncthreads();
+  float pre = in - mine;
+  for (int w = 0; w < wv; ++w) pre += wsum[w];
+  if (!(mine > -INFINITY)) pre = -INFINITY;
+  if (c0 < nch) csum[c0] = pre;
+  if (c0 + 1 < nch) csum[c0 + 1] = x0 < 0.0f ? -INFINITY : pre + x0;
+  __syncthreads();
+}
+
+// Deltas (even / odd start, units of 2^(e-23)) of c >= 1 copies of v added
+// in binade e; kDeltaCap when they leave it.  A tie's first copy rounds the
+// count to even, after which every copy adds the even a + (a & 1).
+__device__ __forceinline__ void run_delta(float v, unsigned int c, int e, int& d0, int& d1) {
+  int a, rnd;
+  bool tie;
+  split_at(v, e, a, rnd, tie);
+  long long x0, x1;
+  if (!tie) {
+    x0 = x1 = (long long)c * (a + rnd);
+  } else {
+    const long long rest = (long long)(c - 1u) * (a + (a & 1));
+    x0 = a + (a & 1) + rest;
+    x1 = a + ((a + 1) & 1) + rest;
+  }
+  d0 = x0 >= kDeltaCap ? kDeltaCap : (int)x0;
+  d1 = x1 >= kDeltaCap ? kDeltaCap : (int)x1;
+}
+
+// Adds c copies of v to s with f32 semantics, a binade at a time, stopping
+// after the first copy that brings s to thr or beyond (use_thr; s < thr on
+// entry).  Returns the copies taken; *hit whether it stopped.  Uniform
+// arguments give uniform results (no lane exchange).
+__device__ __forceinline__ unsigned int run_step(float& s, float v, unsigned int c, bool use_thr,
+                                                 float thr, bool& hit) {
+  unsigned int k = 0;
+  hit = false;
+  while (k < c) {
+    const uint32_t sb = __float_as_uint(s);
+    const int sE = (int)((sb >> 23) & 255u);
+    if (!(sE >= 1 && sE <= 254 && !(sb >> 31)) || !(v >= 0.0f && v <= 3.402823466e38f)) {
+      // zero, subnormal, inf or NaN involved: one real addition
+      s = s + v;
+      ++k;
+      if (use_thr && s >= thr) {
+        hit = true;
+        return k;
+      }
+      if (s != s) return c;  // NaN: every later sum is NaN and below nothing
+      continue;
+    }
+    const int e = sE - 127;
+    long long n = (long long)((sb & 0x7fffffu) | 0x800000u);
+    int a, rnd;
+    bool tie;
+    split_at(v, e, a, rnd, tie);
+    long long q = a + rnd;
+    if (tie) {
+      const long long n1 = n + a + ((n + a) & 1);
+      ++k;
+      if (n1 >= (1ll << 24)) {
+        s = s + v;  // leaves the binade: the real addition
+      } else {
+        n = n1;
+        s = ldexpf((float)n, e - 23);
+      }
+      if (use_thr && s >= thr) {
+        hit = true;
+        return k;
+      }
+      if (n1 >= (1ll << 24) || k >= c) continue;
+      q = a + (a & 1);
+    }
+    if (q == 0) return c;  // the remaining copies change nothing
+    long long take = min((long long)(c - k), ((1ll << 24) - 1 - n) / q);
+    if (use_thr) {
+      // the first copy j with (n + j q) 2^(e-23) >= thr, i.e. n + j q >= ceil(thr / u)
+      const long long need =
+          max((long long)ceil(ldexp((double)thr, 23 - e)) - n, 1ll);
+      const long long j = (need + q - 1) / q;
+      if (j <= take) {
+        n += j * q;
+        k += (unsigned int)j;
+        s = ldexpf((float)n, e - 23);
+        hit = true;
+        return k;
+      }
+    }
+    n += take * q;
+    k += (unsigned int)take;
+    s = ldexpf((float)n, e - 23);
+    if (k < c) {  // the next copy leaves the binade: the real addition
+      s = s + v;
+      ++k;
+      if (use_thr && s >= thr) {
+        hit = true;
+        return k;
+      }
+    }
+  }
+  return c;
+}
+
+// The f32 running sum over runs [0, R) of ra (cnt[r] copies of val[r]), the
+// way f32_run takes elements: chunks of G consecutive runs (at most
+// kRunChunks chunks), a guessed binade per chunk from float prefix sums,
+// composed closed-form deltas per chunk, and wave 0 walking the chunks,
+// applying runs of chunks whose guess matches the actual sum and stepping
+// any other chunk run by run (run_step).  Results in rs.s, rs.r_end and
+// rs.k_end.  Call from all threads; ends with a barrier.
+__device__ __forceinline__ void f32_runs(RunSmem& rs, const RunArrays& ra, int R, bool use_thr,
+                                         float thr) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int G = max(1, (R + kRunChunks - 1) / kRunChunks);
+  const int nch = (R + G - 1) / G;
+  for (int c = tid; c < nch; c += kST) {
+    float acc = 0.0f;
+    bool fin = true;
+    for (int r = c * G; r < min(R, (c + 1) * G); ++r) {
+      const float v = ra.val[r];
+      fin &= v >= 0.0f && v <= 3.402823466e38f;
+      acc += v * (float)ra.cnt[r];
+    }
+    rs.csum[c] = fin ? acc : -1.0f;
+  }
+  __syncthreads();
+  chunk_prefix(rs.csum, rs.wsum, nch);
+  for (int c = tid; c < nch; c += kST) {
+    const float pre = rs.csum[c];
+    int e = kNoDelta, d0 = 0, d1 = 0;
+    if (pre > 0.0f && pre < 3.402823466e38f && !(use_thr && pre > thr * 1.0625f)) {
+      e = (int)((__float_as_uint(pre) >> 23) & 255u) - 127;
+      for (int r = c * G; r < min(R, (c + 1) * G) && d0 < kDeltaCap && d1 < kDeltaCap; ++r) {
+        int b0, b1;
+        run_delta(ra.val[r], ra.cnt[r], e, b0, b1);
+        compose(d0, d1, b0, b1);
+      }
+      if (d0 >= kDeltaCap || d1 >= kDeltaCap) e = kNoDelta;
+    }
+    rs.ce[c] = e;
+    rs.cd0[c] = d0;
+    rs.cd1[c] = d1;
+  }
+  __syncthreads();
+
+  if (wv == 0) {
+    float s = 0.0f;
+    int r_end = R, k_end = 0;
+    bool done = false;
+    auto walk = [&](int c) {  // chunk c run by run (wave-uniform)
+      for (int r = c * G; r < min(R, (c + 1) * G) && !done; ++r) {
+        bool hit;
+        const unsigned int k = run_step(s, ra.val[r], ra.cnt[r], use_thr, thr, hit);
+        if (hit) {
+          done = true;
+          r_end = r;
+          k_end = (int)k;
+        }
+      }
+    };
+    for (int g = 0; g < nch && !done; g += 64) {
+      const bool have = g + lane < nch;
+      const int ec = have ? rs.ce[g + lane] : kNoDelta;
+      const int c0 = have ? rs.cd0[g + lane] : 0, c1 = have ? rs.cd1[g + lane] : 0;
+      const int gend = min(64, nch - g);
+      int start = 0;
+      while (start < gend && !done) {
+        const uint32_t sb = __float_as_uint(s);
+        const int sE = (int)((sb >> 23) & 255u);
+        const bool s_normal = sE >= 1 && sE <= 254 && !(sb >> 31);
+        const int es = sE - 127;
+        const unsigned long long rm = __ballot(s_normal && lane >= start && ec == es) >> start;
+        const int run = ~rm ? __builtin_ctzll(~rm) : 64;
+        if (run == 0) {
+          walk(g + start);
+          ++start;
+          continue;
+        }
+        const bool in = lane >= start && lane < start + run;
+        int a0 = in ? c0 : 0, a1 = in ? c1 : 0;
+        for (int k = 1; k < 64; k <<= 1) {
+          const int b0 = __shfl_up(a0, k, 64), b1 = __shfl_up(a1, k, 64);
+          if (lane >= k) {
+            int n0 = b0, n1 = b1;
+            compose(n0, n1, a0, a1);
+            a0 = n0;
+            a1 = n1;
+          }
+        }
+        const int n = (int)((sb & 0x7fffffu) | 0x800000u);
+        const long long nend = (long long)n + ((n & 1) ? a1 : a0);
+        const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
+        const unsigned long long bad =
+            __ballot(in && (nend >= (1ll << 24) || (use_thr && send >= thr)));
+        if (!bad) {
+          s = readlane_f(send, start + run - 1);
+          start += run;
+          continue;
+        }
+        const int l = __builtin_ctzll(bad);
+        if (l > start) s = readlane_f(send, l - 1);
+        walk(g + l);
+        start = l + 1;
+      }
+    }
+    if (lane == 0) {
+      rs.s = s;
+      rs.r_end = r_end;
+      rs.k_end = k_end;
+    }
+  }
+  __syncthreads();
+}
+
+// sample_exact_kernel for 16-bit logits, on runs instead of a sorted copy.
+// Scratch: 4 kMaxRuns words per row (keys, counts, starts, values).
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
+  static_assert(DT != PKV_F32, "runs of equal values need 16-bit logits");
+  __shared__ RunLds u;
+  __shared__ unsigned int wtmp[kSW];
+  SampleSmem& sm = u.x.sm;
+  RunSmem& rs = u.x.rs;
+  const int row = a.row0 + blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || V <= 1) {  // sample.rs:13-15
+    float bv;
+    int bi;
+    block_argmax<DT, VEC>(sm, x, 0, V, bv, bi);
+    if (tid == 0) a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    return;
+  }
+  uint32_t* base = a.scratch + (size_t)blockIdx.x * 4 * kMaxRuns;
+  const RunArrays ra{base, base + kMaxRuns, base + 2 * kMaxRuns,
+                     reinterpret_cast<float*>(base + 3 * kMaxRuns)};
+  const bool neg = T < 0.0f;
+
+  // runs: the larger half of the key space first, each half's bins from the
+  // largest key down
+  int R = 0;
+  for (int half = 1; half >= 0; --half) {
+    for (int b = tid; b < kHalfKeys; b += kST) u.hist[b] = 0u;
+    __syncthreads();
+    for_each<DT, VEC>(x, V, [&](int, float v) {
+      const uint32_t k = xkey<DT>(neg ? -v : v);
+      const bool mine = (int)(k >> 15) == half;
+      const unsigned long long act = __ballot(true);
+      const uint32_t k0 = __builtin_amdgcn_readfirstlane(k);
+      if (__ballot(k == k0) == act) {  // one key across the wave: one addition
+        if (mine && lane == __builtin_ctzll(act)) atomicAdd(&u.hist[k & 0x7fffu], (unsigned)__popcll(act));
+      } else if (mine) {
+        atomicAdd(&u.hist[k & 0x7fffu], 1u);
+      }
+    });
+    __syncthreads();
+    const int bhi = kHalfKeys - 1 - 32 * tid;  // this thread's 32 bins, descending
+    unsigned int nz = 0;
+    for (int j = 0; j < 32; ++j) nz += u.hist[bhi - j] != 0u;
+    unsigned int total;
+    unsigned int at = (unsigned int)R + block_excl_scan(nz, wtmp, total);
+    for (int j = 0; j < 32; ++j) {
+      const unsigned int h = u.hist[bhi - j];
+      if (h) {
+        ra.key[at] = ((uint32_t)half << 15) | (uint32_t)(bhi - j);
+        ra.cnt[at] = h;
+        ++at;
+      }
+    }
+    R += (int)total;
+    __syncthreads();  // every thread has read the histogram before it is cleared or reused
+  }
+  // start positions; top_k cuts the sequence at len (probs.truncate(k))
+  {
+    const int RP = (R + kST - 1) / kST;
+    const int r0 = min(R, tid * RP), r1 = min(R, r0 + RP);
+    unsigned int sum = 0;
+    for (int r = r0; r < r1; ++r) sum += ra.cnt[r];
+    unsigned int total;
+    unsigned int st = block_excl_scan(sum, wtmp, total);
+    const unsigned int len = a.top_k > 0 && a.top_k < V ? (unsigned int)a.top_k : (unsigned int)V;
+    if (tid == 0) rs.R = R;
+    __syncthreads();
+    for (int r = r0; r < r1; ++r) {
+      const unsigned int c = ra.cnt[r];
+      ra.start[r] = st;
+      if (st < len && len <= st + c) {
+        ra.cnt[r] = len - st;
+        rs.R = r + 1;
+      }
+      st += c;
+    }
+    __syncthreads();
+    R = rs.R;
+  }
+  auto y_of = [&](int r) {
+    const float xp = xkey_value<DT>(ra.key[r]);
+    return (neg ? -xp : xp) / T;
+  };
+  const float max_x = y_of(0);
+  for (int r = tid; r < R; r += kST) ra.val[r] = expf_glibc(y_of(r) - max_x);
+  __syncthreads();
+  f32_runs(rs, ra, R, false, 0.0f);  // sum += p
+  const float sum = rs.s;
+  for (int r = tid; r < R; r += kST) ra.val[r] = ra.val[r] / sum;
+  __syncthreads();
+  if (a.top_p == a.top_p) {  // Some(top_p): cut after the first copy reaching it
+    f32_runs(rs, ra, R, true, a.top_p);
+    const float s_top = rs.s;  // the f32 sum of the kept probabilities
+    if (rs.r_end < R) {
+      const int rc = rs.r_end, kc = rs.k_end;
+      __syncthreads();
+      if (tid == 0) ra.cnt[rc] = (uint32_t)kc;
+      R = rc + 1;
+    }
+    for (int r = tid; r < R; r += kST) ra.val[r] = ra.val[r] / s_top;
+    __syncthreads();
+  }
+  f32_runs(rs, ra, R, true, a.r);  // acc += prob until r <= acc
+  int rj, j;
+  if (rs.r_end < R) {
+    rj = rs.r_end;
+    j = (int)ra.start[rj] + rs.k_end - 1;
+  } else {  // probs.last()
+    rj = R - 1;
+    j = (int)(ra.start[rj] + ra.cnt[rj]) - 1;
+  }
+  // the token at sorted position j: the first position of its y (runs of
+  // different logits can share a y), then that many tokens further among
+  // the equal ones, in index order
+  const float yj = y_of(rj);
+  const uint32_t kj = order_key(yj);
+  int rf = rj;
+  while (rf > 0 && order_key(y_of(rf - 1)) == kj) --rf;
+  Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
+  const int tok = nth_tied<false>(sm, rw, kj, (unsigned long long)(j - (int)ra.start[rf] + 1));
+  if (tid == 0) a.tokens[row] = tok;
+}
+
 // The exp the exact path uses, for verification: out[i] = expf_glibc(in[i]).
 __global__ void expf_glibc_kernel(const float* in, float* out, long long n) {
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -1455,12 +1875,23 @@ __global__ void expf_glibc_kernel(const float* in, float* out, long long n) {
 constexpr size_t kExactScratch = 512ull << 20;
 
 template <int DT, bool VEC>
+void launch_exact_rows(const ExactArgs& a, int rows, hipStream_t stream) {
+  if constexpr (DT == PKV_F32)
+    sample_exact_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
+  else
+    sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
+}
+
+template <int DT, bool VEC>
 hipError_t launch_exact_dt(const ExactArgs& a0, int batch, hipStream_t stream) {
   if (!a0.temps || a0.vocab <= 1) {  // every row is argmax: no scratch
-    sample_exact_kernel<DT, VEC><<<batch, kST, 0, stream>>>(a0);
+    launch_exact_rows<DT, VEC>(a0, batch, stream);
     return hipGetLastError();
   }
-  const size_t per_row = (size_t)2 * (size_t)a0.vocab * sizeof(uint32_t);
+  // scratch per row: f32 logits, two key arrays of the radix sort; 16-bit
+  // logits, the runs (keys, counts, starts, values)
+  const size_t per_row = DT == PKV_F32 ? (size_t)2 * (size_t)a0.vocab * sizeof(uint32_t)
+                                       : (size_t)4 * kMaxRuns * sizeof(uint32_t);
   const int rows = (int)std::max<size_t>(1, std::min<size_t>(batch, kExactScratch / per_row));
   void* p = nullptr;
   hipError_t e = hipMallocAsync(&p, per_row * rows, stream);
@@ -1469,7 +1900,7 @@ hipError_t launch_exact_dt(const ExactArgs& a0, int batch, hipStream_t stream) {
   a.scratch = static_cast<uint32_t*>(p);
   for (int r0 = 0; r0 < batch; r0 += rows) {
     a.row0 = r0;
-    sample_exact_kernel<DT, VEC><<<std::min(rows, batch - r0), kST, 0, stream>>>(a);
+    launch_exact_rows<DT, VEC>(a, std::min(rows, batch - r0), stream);
   }
   e = hipGetLastError();
   const hipError_t f = hipFreeAsync(p, stream);

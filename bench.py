@@ -728,7 +728,7 @@ def sample_bench(args, dev) -> int:
         "roofline": {"bound": "hbm", "achieved": round(rbytes / (ms_exact / 1e3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(rbytes / (ms_exact / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "pkv::sample_exact_kernel",
+                     "traffic": None, "kernel": "pkv::sample_runs_kernel",
                      "kernel_avg_us": round(ms_exact * 1e3, 2),
                      "algorithmic_bytes_per_launch": rbytes},
         "small_batches_exact": small_exact,

@@ -277,37 +277,63 @@ def test_exact_follows_f32_rounding_on_flat_rows(gpu):
             assert pagedkv.sample(lg, temps, exact=False).cpu().tolist() == [exact_pick] * 3
 
 
-def test_exact_spiky_and_tied_rows_with_cuts(gpu):
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_exact_spiky_and_tied_rows_with_cuts(gpu, dt):
     # a few dominant tokens over a flat or tied tail, with top_k cutting
     # inside a tie group and top_p thresholds the f32 running sum reaches
-    # early; every row against the f32 restatement
+    # early; every row against the f32 restatement (f32 logits take the
+    # radix sort, 16-bit logits the runs of equal values)
     rng = np.random.default_rng(21)
     V, B = 50000, 16
     x = rng.integers(-2, 2, (B, V)).astype(np.float32)
     for b in range(B):
         x[b, rng.integers(0, V, 1 + b % 5)] = 6.0 + (b % 3)
     temps = np.array([0.5, 1.0, 2.0, 4.0] * 4, np.float32)
-    lg = torch.from_numpy(x).to(gpu)
+    lg = torch.from_numpy(x).to(gpu).to(TD[dt])
+    x32 = lg.float().cpu().numpy()
     for top_k, top_p in ((None, None), (3, None), (20000, None), (None, 0.5), (None, 0.999),
-                         (100, 0.8)):
+                         (100, 0.8), (None, 1.0)):
         got = pagedkv.sample(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
-        want = [oracle.sample(x[b], float(temps[b]), top_k=top_k, top_p=top_p)[0]
+        want = [oracle.sample(x32[b], float(temps[b]), top_k=top_k, top_p=top_p)[0]
                 for b in range(B)]
         assert got.cpu().tolist() == want, (top_k, top_p)
 
 
 def test_exact_batch_over_several_launches(gpu):
-    # 8 bytes of scratch per logit and at most 512 MB per launch: rows of
-    # 2^20 logits run 64 per launch, so 70 rows take two launches
+    # at most 512 MB of scratch per launch: f32 rows of 2^20 logits take
+    # 8 MB each (64 rows per launch), 16-bit rows 1 MB each (512 per launch)
     rng = np.random.default_rng(4)
     B, V = 70, 1 << 20
-    lg = torch.randn((B, V), device=gpu, dtype=torch.bfloat16) * 2
+    lg = torch.randn((B, V), device=gpu) * 2
+    temps = torch.from_numpy(rng.choice([0.0, 0.8, 1.0, 1.5], B).astype(np.float32)).to(gpu)
+    got = pagedkv.sample(lg, temps).cpu().tolist()
+    x32 = lg.cpu().numpy()
+    t = temps.cpu().numpy()
+    for b in (0, 1, 62, 63, 64, 65, 69):
+        assert got[b] == oracle.sample(x32[b], float(t[b]))[0], b
+    B, V = 600, 3000
+    lg = (torch.randn((B, V), device=gpu) * 2).to(torch.bfloat16)
     temps = torch.from_numpy(rng.choice([0.0, 0.8, 1.0, 1.5], B).astype(np.float32)).to(gpu)
     got = pagedkv.sample(lg, temps).cpu().tolist()
     x32 = lg.float().cpu().numpy()
     t = temps.cpu().numpy()
-    for b in (0, 1, 62, 63, 64, 65, 69):
+    for b in (0, 1, 510, 511, 512, 513, 599):
         assert got[b] == oracle.sample(x32[b], float(t[b]))[0], b
+
+
+def test_exact_16bit_edge_values(gpu):
+    # signed zeros (one key), subnormal and largest finite f16 values, and
+    # every value of a row equal except one; T < 0 reverses the order
+    rows = [[0.0, -0.0, 0.0, -0.0, 1e-7, -1e-7] * 50,
+            [65504.0, -65504.0, 6e-8, -6e-8, 0.0] * 40,
+            [3.0] * 999 + [3.0009765625]]
+    for dt in (torch.float16, torch.bfloat16):
+        for T in (1.0, -0.7, 1e-3):
+            for r in rows:
+                lg = torch.tensor([r], dtype=dt, device=gpu)
+                got = int(pagedkv.sample(lg, torch.tensor([T])).item())
+                want = oracle.sample(lg.float().cpu().numpy()[0], T)[0]
+                assert got == want, (dt, T, r[:6])
 
 
 def test_exact_replays_in_a_graph(gpu):
