@@ -596,8 +596,12 @@ int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_
 static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
   if (!p->prof_on) return PKV_OK;
   if (p->prof_used == p->prof_events.size()) {
+    // Timing-only events: no system-scope fence at record, so the events do
+    // not add a cache writeback and invalidation inside the window they time
+    // (pkv_pool_profile_read only reads their timestamps).
     hipEvent_t x = nullptr, y = nullptr;
-    if (hipEventCreate(&x) != hipSuccess || hipEventCreate(&y) != hipSuccess)
+    if (hipEventCreateWithFlags(&x, hipEventDisableSystemFence) != hipSuccess ||
+        hipEventCreateWithFlags(&y, hipEventDisableSystemFence) != hipSuccess)
       return fail(p, PKV_ERR_HIP, "profile: hipEventCreate failed");
     p->prof_events.emplace_back(x, y);
   }
