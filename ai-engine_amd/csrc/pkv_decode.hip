@@ -709,12 +709,14 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       __builtin_nontemporal_store(f32x4{o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]},
                                   reinterpret_cast<f32x4*>(po + h * HD + c * C::EPL + e));
   }
-  if (lane == 0) {
+  // (m, l) of the R heads: one store instruction from lanes 0 .. 2R-1 (a
+  // contiguous 8R-byte write) rather than 2R separate 4-byte writes.
+  if (lane < 2 * R) {
+    float v = 0.0f;
 #pragma unroll
-    for (int h = 0; h < R; ++h) {
-      __builtin_nontemporal_store(mh[h], ml + 2 * h);
-      __builtin_nontemporal_store(lh[h], ml + 2 * h + 1);
-    }
+    for (int h = 0; h < R; ++h)
+      if ((lane >> 1) == h) v = (lane & 1) ? lh[h] : mh[h];
+    __builtin_nontemporal_store(v, ml + lane);
   }
 }
 
