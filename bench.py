@@ -176,6 +176,9 @@ def main() -> int:
                     help="pool replicas rotated across steps so that every step reads its K/V "
                          "from HBM, not the 256 MB Infinity Cache (0 = auto: >= 1 GB per "
                          "rotation)")
+    ap.add_argument("--no-secondary", dest="secondary", action="store_false",
+                    help="cfg3: skip the in-process runs of cfg1, cfg2 and cfg4 reported under "
+                         "'secondary' in the same line")
     ap.add_argument("--graph", choices=["auto", "on", "off"], default="auto",
                     help="replay each step as a captured HIP graph (auto: when a layer's "
                          "launch moves < 128 MB, i.e. launch overhead would show)")
@@ -202,13 +205,73 @@ def main() -> int:
     if args.config == "cfg5":
         return churn(args, dev)
     if args.config == "cfg2":
-        return mix(args, dev)
+        return emit(mix(args, dev))
     if args.config == "sample":
         return sample_bench(args, dev)
     if args.config == "gather":
         return gather_bench(args, dev)
     if args.config == "append":
         return append_bench(args, dev)
+    res = decode_bench(args, dev)
+    if (args.config == "cfg3" and args.secondary and "error" not in res
+            and not (args.rope or args.kv_dtype)):
+        res["secondary"] = secondary(args, dev)
+    return emit(res)
+
+
+def emit(res: dict) -> int:
+    """Prints the one result line; exit status 1 when it carries an error."""
+    print(json.dumps(res), flush=True)
+    return 1 if "error" in res else 0
+
+
+def secondary(args, dev) -> dict:
+    """The other hot-path workloads, timed in the same process right after
+    the headline: cfg1 and cfg4 decode and the cfg2 prefill+decode mix, each
+    with its own pool (the previous one freed), up to 10 timed steps after 2
+    warmup steps, no CPU baseline.  A failure is recorded under that config's
+    name and does not touch the headline figures."""
+    import torch
+
+    out = {}
+    for name in ("cfg1", "cfg2", "cfg4"):
+        a = argparse.Namespace(**vars(args))
+        a.config, a.steps, a.warmup, a.cpu_layers = name, max(1, min(args.steps, 10)), 2, 0
+        a.replicas, a.graph = 0, "auto"
+        t0 = time.time()
+        try:
+            r = mix(a, dev) if name == "cfg2" else decode_bench(a, dev)
+        except Exception as e:  # recorded, the headline stands
+            r = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        if "error" in r:
+            out[name] = {"error": r["error"]}
+            continue
+        keep = ("bound", "achieved", "unit", "frac", "kernel", "kernel_avg_us")
+        out[name] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                     "steps": r["steps"], "warmup": r["warmup"], "dtype": r["dtype"],
+                     "workload": r["config"]["workload"],
+                     "roofline": {k: r["roofline"][k] for k in keep},
+                     "wall_s": round(time.time() - t0, 1)}
+        if "roofline_decode" in r:
+            out[name]["roofline_decode"] = {k: r["roofline_decode"][k] for k in keep}
+        log(f"[bench] secondary {name}: {r['value']} {r['unit']}, "
+            f"{r['roofline']['kernel']} frac {r['roofline']['frac']}")
+    return out
+
+
+def decode_bench(args, dev) -> dict:
+    """Decode configs (cfg1, cfg2d, cfg3, cfg4): every layer of one decode
+    step over the batch as pkv_decode_attention calls (fused append of the
+    new token), replayed as HIP graphs when launches are small.  Returns
+    the result line as a dict ({"error": ...} on a failed check)."""
+    import numpy as np
+    import torch
+
+    import pagedkv
+    from pagedkv import workload as wl
+
     shape_attr, B, lo, hi, desc = CONFIGS[args.config]
     shape = getattr(wl, shape_attr)
     if args.kv_dtype:
@@ -313,8 +376,8 @@ def main() -> int:
         graph_ok = bool(torch.equal(ref_out.view(torch.int16), out.view(torch.int16)))
         log(f"[bench] graph replay == eager launch: {graph_ok}")
         if not graph_ok:
-            print(json.dumps({"error": "graph replay differs from eager launches"}))
-            return 1
+            cache.close()
+            return {"error": "graph replay differs from eager launches"}
 
     ms_step, step_dist = timed_steps(step, args.steps, stream)
 
@@ -385,9 +448,10 @@ def main() -> int:
                      "frac_of_copy_ceiling": round(gbps_kernel / ceiling["GBps"], 4)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(result), flush=True)
+    if rope is not None:
+        rope.close()
     cache.close()
-    return 0
+    return result
 
 
 def append_bench(args, dev) -> int:
@@ -810,7 +874,7 @@ def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):
     return res_cpu
 
 
-def mix(args, dev) -> int:
+def mix(args, dev) -> dict:
     """TinyLlama-1.1B continuous-batching mix (22
     layers, 32q/4kv heads, hd 64, bs 16, f16).  Per layer: the 8 sequences
     in chunked prefill store their 256-token chunk (pkv_append) and attend
@@ -998,8 +1062,10 @@ def mix(args, dev) -> int:
         g_step.replay()
         torch.cuda.synchronize()
         if not (torch.equal(outp, ref_p) and torch.equal(outd, ref_d)):
-            print(json.dumps({"error": "graph replay differs from eager launches"}))
-            return 1
+            if rope is not None:
+                rope.close()
+            cache.close()
+            return {"error": "graph replay differs from eager launches"}
         del ref_p, ref_d
         ms_graph_serial = time_steps(g_serial.replay)
         step_fn = g_step.replay
@@ -1113,11 +1179,10 @@ def mix(args, dev) -> int:
         "ms_per_step_graph_serial": None if ms_graph_serial is None else round(ms_graph_serial, 4),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     if rope is not None:
         rope.close()
     cache.close()
-    return 0
+    return res
 
 
 def mix_faithful(m, tables, kp, vp, chunk_rows, decode_rows, NP, C, ND, L, scale):
