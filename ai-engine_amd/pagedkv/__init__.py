@@ -355,6 +355,9 @@ class PagedKvCache:
         check(lib().pkv_pool_profile_read(self._h, ctypes.byref(ms), ctypes.byref(n)), self._h)
         return float(ms.value), int(n.value)
 
+    def decode_workspace_bytes(self, batch: int, n_head: int, max_context_len: int) -> int:
+        return int(lib().pkv_decode_workspace_bytes(self._h, batch, n_head, max_context_len))
+
     def reserve_decode(self, batch: int, n_head: int, max_context_len: int) -> None:
         check(lib().pkv_pool_reserve_decode(self._h, batch, n_head, max_context_len), self._h)
 
