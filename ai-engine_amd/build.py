@@ -31,6 +31,7 @@ SOURCES = [
     "pkv_kvcopy.hip",
     "pkv_decode.hip",
     "pkv_prefill.hip",
+    "pkv_mixed.hip",
     "pkv_rope.hip",
     "pkv_sample.hip",
 ]
@@ -46,9 +47,11 @@ COMMON = [
 
 
 # Per-source extras.  Prefill keeps its MFMA accumulators in ordinary VGPRs
-# (no AGPR round trips for the softmax rescale; measured faster on gfx950).
+# (no AGPR round trips for the softmax rescale; measured faster on gfx950);
+# so does the mixed launch, which runs the same prefill body.
 EXTRA = {
     "pkv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "pkv_mixed.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -614,11 +614,8 @@ static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
 // Shared validation and launch of pkv_decode_attention(_rope, _noalloc).
 // noalloc: the partials go to the static scratch array, and nothing is
 // allocated (no workspace growth, no profile events).
-static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
-                       bool noalloc = false) {
-  if (int rc = check_layer(p, layer)) return rc;
-  if (a.batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", a.batch);
-  if (a.batch == 0) return PKV_OK;
+// Argument checks of a decode call with batch > 0 (PKV_OK or the failure).
+static int decode_validate(pkv_pool* p, const pkv::DecodeArgs& a) {
   if (!a.q || !a.out || !a.block_tables || !a.context_lens)
     return fail(p, PKV_ERR_INVALID, "q, out, block_tables and context_lens must be non-NULL");
   if ((a.k_new == nullptr) != (a.v_new == nullptr))
@@ -638,6 +635,15 @@ static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
   if (a.out_dtype != PKV_F32 && a.out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   if (!(a.scale == a.scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
+  return PKV_OK;
+}
+
+static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
+                       bool noalloc = false) {
+  if (int rc = check_layer(p, layer)) return rc;
+  if (a.batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", a.batch);
+  if (a.batch == 0) return PKV_OK;
+  if (int rc = decode_validate(p, a)) return rc;
   DeviceGuard dg(p->device);
   size_t need = pkv::decode_workspace_bytes(p, a.batch, a.n_head, a.max_context_len);
   if (noalloc) {
@@ -708,15 +714,12 @@ int pkv_decode_attention_rope(pkv_pool* p, int layer, const pkv_rope* rope,
 }
 
 namespace {
-int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
-                 const int32_t* cu_q_lens, const int32_t* context_lens,
-                 const int32_t* block_tables, int max_blocks_per_seq, int n_seqs, int max_q_len,
-                 int max_context_len, int n_head, float scale, const void* k_new,
-                 const void* v_new, void* stream) {
-  CHECK_POOL(p);
-  if (int rc = check_layer(p, layer)) return rc;
-  if (n_seqs < 0) return fail(p, PKV_ERR_INVALID, "n_seqs %d < 0", n_seqs);
-  if (n_seqs == 0 || max_q_len == 0) return PKV_OK;
+// Argument checks of a prefill call with n_seqs > 0 and max_q_len != 0.
+int prefill_validate(pkv_pool* p, const void* q, const void* out, int out_dtype,
+                     const int32_t* cu_q_lens, const int32_t* context_lens,
+                     const int32_t* block_tables, int max_blocks_per_seq, int max_q_len,
+                     int max_context_len, int n_head, float scale, const void* k_new,
+                     const void* v_new) {
   if (!q || !out || !cu_q_lens || !context_lens || !block_tables)
     return fail(p, PKV_ERR_INVALID, "q, out, cu_q_lens, context_lens, block_tables must be non-NULL");
   if (!aligned16(q) || !aligned16(out))
@@ -735,6 +738,22 @@ int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype
     return fail(p, PKV_ERR_INVALID, "prefill: scale must be positive and finite");
   if (out_dtype != PKV_F32 && out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
+  return PKV_OK;
+}
+
+int prefill_call(pkv_pool* p, int layer, const void* q, void* out, int out_dtype,
+                 const int32_t* cu_q_lens, const int32_t* context_lens,
+                 const int32_t* block_tables, int max_blocks_per_seq, int n_seqs, int max_q_len,
+                 int max_context_len, int n_head, float scale, const void* k_new,
+                 const void* v_new, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  if (n_seqs < 0) return fail(p, PKV_ERR_INVALID, "n_seqs %d < 0", n_seqs);
+  if (n_seqs == 0 || max_q_len == 0) return PKV_OK;
+  if (int rc = prefill_validate(p, q, out, out_dtype, cu_q_lens, context_lens, block_tables,
+                                max_blocks_per_seq, max_q_len, max_context_len, n_head, scale,
+                                k_new, v_new))
+    return rc;
   DeviceGuard dg(p->device);
   {
     int pk = 0, mp = 0;
@@ -796,6 +815,85 @@ int pkv_pool_reserve_prefill(pkv_pool* p, int n_seqs, int n_head, int max_q_len,
   DeviceGuard dg(p->device);
   if (int rc = release_retired(p)) return rc;
   return ensure_workspace(p, need);
+}
+
+// ---- mixed prefill + decode batch --------------------------------------
+namespace {
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace of a mixed call with both batches present: the decode partials,
+// then the prefill split partials.
+void mixed_ws(const pkv_pool* p, int n_head, const pkv_prefill_batch& pb,
+              const pkv_decode_batch& db, size_t* dbytes, size_t* pbytes) {
+  *dbytes = round256(pkv::decode_workspace_bytes(p, db.batch, n_head, db.max_context_len));
+  int pk = 0, mp = 0;
+  pkv::prefill_plan(p, pb.n_seqs, n_head, pb.max_q_len, pb.max_context_len, &pk, &mp, pbytes);
+}
+}  // namespace
+
+size_t pkv_mixed_workspace_bytes(const pkv_pool* p, int n_head, const pkv_prefill_batch* pb,
+                                 const pkv_decode_batch* db) {
+  if (!p || n_head <= 0 || n_head % p->n_kv_head) return 0;
+  const bool hp = pb && pb->n_seqs > 0 && pb->max_q_len > 0;
+  const bool hd = db && db->batch > 0;
+  if (hp && hd) {
+    size_t d = 0, q = 0;
+    mixed_ws(p, n_head, *pb, *db, &d, &q);
+    return d + q;
+  }
+  if (hd) return pkv::decode_workspace_bytes(p, db->batch, n_head, db->max_context_len);
+  if (hp)
+    return pkv_prefill_workspace_bytes(p, pb->n_seqs, n_head, pb->max_q_len, pb->max_context_len);
+  return 0;
+}
+
+int pkv_mixed_attention(pkv_pool* p, int layer, const pkv_prefill_batch* pb,
+                        const pkv_decode_batch* db, int n_head, float scale, void* stream) {
+  CHECK_POOL(p);
+  if (int rc = check_layer(p, layer)) return rc;
+  const bool hp = pb && !(pb->n_seqs == 0 || pb->max_q_len == 0);
+  const bool hd = db && db->batch != 0;
+  auto prefill_only = [&]() {
+    return prefill_call(p, layer, pb->q, pb->out, pb->out_dtype, pb->cu_q_lens,
+                        pb->context_lens, pb->block_tables, pb->max_blocks_per_seq, pb->n_seqs,
+                        pb->max_q_len, pb->max_context_len, n_head, scale, pb->k_new,
+                        pb->v_new, stream);
+  };
+  auto decode_only = [&]() {
+    pkv::DecodeArgs a{db->q, db->out, db->out_dtype, db->block_tables, db->max_blocks_per_seq,
+                      db->context_lens, db->max_context_len, db->batch, n_head, scale,
+                      db->k_new, db->v_new};
+    return decode_call(p, layer, a, stream);
+  };
+  // one batch (or an invalid count, which the single call reports)
+  if (!hp || !hd || pb->n_seqs < 0 || db->batch < 0 || !pkv::mixed_supported(p, n_head, false)) {
+    int rc = PKV_OK;
+    if (pb) rc = prefill_only();
+    if (rc == PKV_OK && db) rc = decode_only();
+    return rc;
+  }
+  if (int rc = prefill_validate(p, pb->q, pb->out, pb->out_dtype, pb->cu_q_lens,
+                                pb->context_lens, pb->block_tables, pb->max_blocks_per_seq,
+                                pb->max_q_len, pb->max_context_len, n_head, scale, pb->k_new,
+                                pb->v_new))
+    return rc;
+  pkv::DecodeArgs da{db->q, db->out, db->out_dtype, db->block_tables, db->max_blocks_per_seq,
+                     db->context_lens, db->max_context_len, db->batch, n_head, scale,
+                     db->k_new, db->v_new};
+  if (int rc = decode_validate(p, da)) return rc;
+  DeviceGuard dg(p->device);
+  size_t dbytes = 0, pbytes = 0;
+  mixed_ws(p, n_head, *pb, *db, &dbytes, &pbytes);
+  if (int rc = ensure_workspace(p, dbytes + pbytes)) return rc;
+  pkv::PrefillArgs pa{pb->q, pb->out, pb->out_dtype, pb->cu_q_lens, pb->context_lens,
+                      pb->block_tables, pb->max_blocks_per_seq, pb->n_seqs, pb->max_q_len,
+                      pb->max_context_len, n_head, scale, pb->k_new, pb->v_new};
+  hipEvent_t eb = nullptr, ee = nullptr;
+  if (int rc = profile_slot(p, &eb, &ee)) return rc;
+  hipError_t e = pkv::launch_mixed(p, layer, pa, da, p->ws, p->ws + dbytes,
+                                   static_cast<hipStream_t>(stream), eb, ee);
+  if (e != hipSuccess) return hip_fail(p, e, "mixed launch");
+  return PKV_OK;
 }
 
 int pkv_pool_profile(pkv_pool* p, int enable) {

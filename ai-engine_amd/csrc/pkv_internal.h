@@ -201,4 +201,16 @@ hipError_t launch_prefill(const pkv_pool* p, int layer, const PrefillArgs& a,
                           hipStream_t stream, hipEvent_t ev_begin = nullptr,
                           hipEvent_t ev_end = nullptr);
 
+// One launch for a layer's prefill batch and decode batch (pkv_mixed.hip):
+// same results as launch_prefill then launch_decode, with the decode
+// partials at decode_partials and the prefill split partials at
+// prefill_partials (disjoint).  ev_begin / ev_end bracket the combined
+// kernel.  hipErrorNotSupported, with nothing enqueued, for shapes without a
+// combined kernel (mixed_supported false, or different n_head).
+bool mixed_supported(const pkv_pool* p, int n_head, bool rope);
+hipError_t launch_mixed(const pkv_pool* p, int layer, const PrefillArgs& pa,
+                        const DecodeArgs& da, char* decode_partials, char* prefill_partials,
+                        hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                        hipEvent_t ev_end = nullptr);
+
 }  // namespace pkv

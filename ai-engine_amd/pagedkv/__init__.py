@@ -594,6 +594,67 @@ class KvPool:
             check(lib().pkv_prefill_attention(*args, _stream_ptr(stream)), self._h)
         return out
 
+    # -- a layer's mixed batch -------------------------------------------------
+    def mixed_attention(self, prefill: dict, decode: dict, scale: float | None = None,
+                        stream=None):
+        """pkv_mixed_attention: the prefill batch (keys of prefill_attention:
+        q, cu_q_lens, context_lens, block_tables, max_q_len, max_context_len,
+        optional k_new, v_new, out_dtype, out) and the decode batch (keys of
+        decode_attention: q, block_tables, context_lens, optional
+        max_context_len, k_new, v_new, out_dtype, out) of one layer in one
+        call; results identical to the two calls.  Returns (prefill out,
+        decode out)."""
+        import torch
+        c = self.cache
+        pq, dq = prefill["q"].contiguous(), decode["q"].contiguous()
+        H, hd = pq.shape[1], pq.shape[2]
+        if dq.shape[1:] != (H, hd) or hd != c.head_dim:
+            raise ValueError("prefill and decode q must be (n, n_head, head_dim) of the pool")
+        if pq.dtype != c.dtype or dq.dtype != c.dtype:
+            raise TypeError("q must have the pool dtype")
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        keep = []  # tensors the structs point into, alive until the call returns
+
+        def dev(t):
+            keep.append(t)
+            return _dev_ptr(t)
+
+        rows = {}
+        for side, d in (("prefill", prefill), ("decode", decode)):
+            for key in ("k_new", "v_new"):
+                if d.get(key) is not None:
+                    self._check_rows(d[key], key)
+            n = (d["q"].shape[0])
+            out = d.get("out")
+            if out is None:
+                out = torch.empty((n, H * hd), dtype=d.get("out_dtype") or c.dtype,
+                                  device=c.device)
+            rows[side] = out
+        pcu = _i32(prefill["cu_q_lens"], c.device)
+        pcl = _i32(prefill["context_lens"], c.device)
+        pbt = _i32(prefill["block_tables"], c.device)
+        dcl = _i32(decode["context_lens"], c.device)
+        dbt = _i32(decode["block_tables"], c.device)
+        dmax = decode.get("max_context_len")
+        if dmax is None:
+            dmax = int(dcl.max().item()) if dcl.numel() else 1
+        pk, pv = prefill.get("k_new"), prefill.get("v_new")
+        dk, dv = decode.get("k_new"), decode.get("v_new")
+        pb = _lib.PrefillBatch(dev(pq), dev(rows["prefill"]), pkv_dtype(rows["prefill"].dtype),
+                               dev(pcu), dev(pcl), dev(pbt), pbt.shape[1], pcl.numel(),
+                               int(prefill["max_q_len"]), int(prefill["max_context_len"]),
+                               dev(pk) if pk is not None else None,
+                               dev(pv) if pv is not None else None)
+        db = _lib.DecodeBatch(dev(dq), dev(rows["decode"]), pkv_dtype(rows["decode"].dtype),
+                              dev(dbt), dbt.shape[1], dev(dcl), int(dmax), dcl.numel(),
+                              dev(dk) if dk is not None else None,
+                              dev(dv) if dv is not None else None)
+        check(lib().pkv_mixed_attention(self._h, self.layer_index, ctypes.byref(pb),
+                                        ctypes.byref(db), H, float(scale),
+                                        _stream_ptr(stream)), self._h)
+        return rows["prefill"], rows["decode"]
+
     def _check_rows(self, t, name: str) -> None:
         c = self.cache
         if t.dtype != c.dtype:

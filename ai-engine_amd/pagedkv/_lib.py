@@ -28,6 +28,26 @@ _I = ctypes.c_int
 _SZ = ctypes.c_size_t
 _I32P = ctypes.POINTER(ctypes.c_int32)
 
+
+
+class PrefillBatch(ctypes.Structure):
+    """struct pkv_prefill_batch."""
+    _fields_ = [("q", _P), ("out", _P), ("out_dtype", _I), ("cu_q_lens", _P),
+                ("context_lens", _P), ("block_tables", _P), ("max_blocks_per_seq", _I),
+                ("n_seqs", _I), ("max_q_len", _I), ("max_context_len", _I), ("k_new", _P),
+                ("v_new", _P)]
+
+
+class DecodeBatch(ctypes.Structure):
+    """struct pkv_decode_batch."""
+    _fields_ = [("q", _P), ("out", _P), ("out_dtype", _I), ("block_tables", _P),
+                ("max_blocks_per_seq", _I), ("context_lens", _P), ("max_context_len", _I),
+                ("batch", _I), ("k_new", _P), ("v_new", _P)]
+
+
+_PBP = ctypes.POINTER(PrefillBatch)
+_DBP = ctypes.POINTER(DecodeBatch)
+
 # name -> (restype, argtypes); mirrors include/pagedkv.h one to one.
 SIGNATURES: dict[str, tuple] = {
     "pkv_version": (ctypes.c_char_p, []),
@@ -61,6 +81,8 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_pool_check": (_I, [_P]),
     "pkv_prefill_workspace_bytes": (_SZ, [_P, _I, _I, _I, _I]),
     "pkv_pool_reserve_prefill": (_I, [_P, _I, _I, _I, _I]),
+    "pkv_mixed_attention": (_I, [_P, _I, _PBP, _DBP, _I, ctypes.c_float, _P]),
+    "pkv_mixed_workspace_bytes": (_SZ, [_P, _I, _PBP, _DBP]),
     "pkv_rope_tables_host": (_I, [_I, ctypes.c_float, _I, _P, _P]),
     "pkv_rope_create": (_I, [ctypes.POINTER(_P), _I, ctypes.c_float, _I, _I]),
     "pkv_rope_destroy": (_I, [_P]),

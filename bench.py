@@ -15,6 +15,7 @@ decode math timed on this host on a bounded sample (see --cpu-layers).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import dataclasses
 import json
 import math
@@ -163,6 +164,9 @@ def main() -> int:
                          "a HIP graph with each layer's decode on a second stream)")
     ap.add_argument("--unfused", action="store_true",
                     help="cfg2: store the chunk's K/V with a separate pkv_append launch")
+    ap.add_argument("--separate", action="store_true",
+                    help="cfg2: separate prefill and decode launches per layer (default: one "
+                         "pkv_mixed_attention launch per layer)")
     ap.add_argument("--kv-dtype", choices=["f32", "f16", "bf16"], default=None,
                     help="decode configs: pool dtype instead of the config's (f32 is the "
                          "reference's KvPool dtype)")
@@ -254,8 +258,9 @@ def secondary(args, dev) -> dict:
                      "workload": r["config"]["workload"],
                      "roofline": {k: r["roofline"][k] for k in keep},
                      "wall_s": round(time.time() - t0, 1)}
-        if "roofline_decode" in r:
-            out[name]["roofline_decode"] = {k: r["roofline_decode"][k] for k in keep}
+        for extra in ("roofline_prefill", "roofline_decode"):
+            if extra in r:
+                out[name][extra] = {k: r[extra][k] for k in keep}
         log(f"[bench] secondary {name}: {r['value']} {r['unit']}, "
             f"{r['roofline']['kernel']} frac {r['roofline']['frac']}")
     return out
@@ -1018,6 +1023,26 @@ def mix(args, dev) -> dict:
     # split prefill would share: overlap only when the prefill does not split
     overlap_ok = cache.prefill_workspace_bytes(NP, H, C, max_p) == 0
 
+    # One launch per layer for both batches (pkv_mixed_attention): the
+    # prefill and decode workgroups share the CUs.  The argument structs are
+    # built once; the stream is the call's own argument.
+    use_mixed = not args.serial and not args.separate and fused_store
+    pbs = [pagedkv._lib.PrefillBatch(qp[l].data_ptr(), outp[l].data_ptr(), odt, cu.data_ptr(),
+                                     pctx.data_ptr(), ptab.data_ptr(), mbps, NP, C, max_p,
+                                     kc[l].data_ptr(), vc[l].data_ptr()) for l in range(L)]
+    dbs = [pagedkv._lib.DecodeBatch(qd[l].data_ptr(), outd[l].data_ptr(), odt, dtab.data_ptr(),
+                                    mbps, dctx.data_ptr(), max_d, ND, kd[l].data_ptr(),
+                                    vd[l].data_ptr()) for l in range(L)]
+
+    def mixed(l):
+        rc = lib.pkv_mixed_attention(h, l, ctypes.byref(pbs[l]), ctypes.byref(dbs[l]), H, sc, sp)
+        if rc:
+            chk(rc, h)
+
+    def step_mixed():
+        for l in range(L):
+            mixed(l)
+
     dists = {}
 
     def time_steps(fn):
@@ -1045,6 +1070,7 @@ def mix(args, dev) -> dict:
     ms_serial = time_steps(step_serial)   # eager, one stream
     step_fn = step_serial
     ms_graph_serial = None
+    ms_graph_separate = None
     schedule = "eager launches, one stream"
     ms_step = ms_serial
     if not args.serial:
@@ -1066,12 +1092,35 @@ def mix(args, dev) -> dict:
                 rope.close()
             cache.close()
             return {"error": "graph replay differs from eager launches"}
-        del ref_p, ref_d
         ms_graph_serial = time_steps(g_serial.replay)
         step_fn = g_step.replay
         ms_step = time_steps(step_fn)
         schedule = ("HIP graph; per layer the decode on a second stream, forked and joined "
                     "around the prefill" if overlap_ok else "HIP graph, one stream")
+        if use_mixed:
+            ms_graph_separate = ms_step
+            # one eager mixed step must equal the separate launches bit for
+            # bit, and so must a replay of its graph
+            outp.zero_()
+            outd.zero_()
+            step_mixed()
+            torch.cuda.synchronize()
+            same = torch.equal(outp, ref_p) and torch.equal(outd, ref_d)
+            g_mixed = capture(step_mixed)
+            outp.zero_()
+            outd.zero_()
+            g_mixed.replay()
+            torch.cuda.synchronize()
+            if not (same and torch.equal(outp, ref_p) and torch.equal(outd, ref_d)):
+                if rope is not None:
+                    rope.close()
+                cache.close()
+                return {"error": "mixed launches differ from separate launches"}
+            step_fn = g_mixed.replay
+            ms_step = time_steps(step_fn)
+            schedule = ("HIP graph, one pkv_mixed_attention launch per layer (prefill and "
+                        "decode workgroups in one grid, then the split-context merge)")
+        del ref_p, ref_d
     cache.check()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -1089,6 +1138,7 @@ def mix(args, dev) -> dict:
 
     pre_ms, pre_n = kernel_ms(prefill_store if fused_store else prefill)
     dec_ms, dec_n = kernel_ms(decode)
+    mix_ms = kernel_ms(mixed)[0] if use_mixed else None
     t0.record(stream)
     for _ in range(n_kt):
         for l in range(L):
@@ -1109,6 +1159,23 @@ def mix(args, dev) -> dict:
     tflops = flops / (pre_ms / 1e3) / 1e12
     dec_gbps = dbytes / (dec_ms / 1e3) / 1e9
     tok_s = (T + ND) / (ms_step / 1e3)
+    # decode flops: q.k and p.v over every key of every query head
+    dflops = 4 * H * hd * int((m.ctx + 1).sum())
+    roof_pre = {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
+                "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                "kernel": "pkv::prefill_kernel", "kernel_avg_us": round(pre_ms * 1e3, 2),
+                "algorithmic_flops_per_launch": flops, "algorithmic_bytes_per_launch": pbytes}
+    roof = roof_pre
+    if mix_ms is not None:
+        mtf = (flops + dflops) / (mix_ms / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(mtf, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                "frac": round(mtf / 2500.0, 4), "traffic": None, "kernel": "pkv::mixed_kernel",
+                "kernel_avg_us": round(mix_ms * 1e3, 2),
+                "algorithmic_flops_per_launch": flops + dflops,
+                "algorithmic_bytes_per_launch": pbytes + dbytes,
+                "hbm_GBps": round((pbytes + dbytes) / (mix_ms / 1e3) / 1e9, 1)}
+        log(f"[bench] mixed kernel {mix_ms * 1e3:.1f} us per layer ({mtf:.1f} TFLOP/s, "
+            f"{roof['hbm_GBps']:.0f} GB/s); separate launches, graph: {ms_graph_separate:.3f} ms")
     log(f"[bench] {ms_step:.3f} ms/step ({schedule}; eager serial {ms_serial:.3f}, graph serial "
         f"{ms_graph_serial if ms_graph_serial is None else round(ms_graph_serial, 3)}), "
         f"{tok_s:.0f} tok/s; per layer: prefill {pre_ms * 1e3:.1f} us "
@@ -1161,11 +1228,8 @@ def mix(args, dev) -> dict:
                                   "pkv_decode_attention_rope)" if rope is not None else ""),
                    "priors": m.prior.tolist(), "mean_decode_context": round(float(m.ctx.mean()), 1),
                    "seed": args.seed, "num_blocks": m.num_blocks, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
-                     "kernel": "pkv::prefill_kernel", "kernel_avg_us": round(pre_ms * 1e3, 2),
-                     "algorithmic_flops_per_launch": flops,
-                     "algorithmic_bytes_per_launch": pbytes},
+        "roofline": roof,
+        "roofline_prefill": roof_pre,
         "roofline_decode": {"bound": "hbm", "achieved": round(dec_gbps, 1), "peak": HBM_PEAK_GBPS,
                             "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
                             "kernel": "pkv::decode_kernel", "kernel_avg_us": round(dec_ms * 1e3, 2),
@@ -1177,6 +1241,8 @@ def mix(args, dev) -> dict:
                         if fused_store else "separate launch (append us above)"),
         "ms_per_step_eager_serial": round(ms_serial, 4),
         "ms_per_step_graph_serial": None if ms_graph_serial is None else round(ms_graph_serial, 4),
+        "ms_per_step_graph_separate": (None if ms_graph_separate is None
+                                       else round(ms_graph_separate, 4)),
         "cpu_baseline": cpu,
     }
     if rope is not None:

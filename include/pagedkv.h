@@ -300,6 +300,59 @@ size_t pkv_prefill_workspace_bytes(const pkv_pool* pool, int n_seqs, int n_head,
 int pkv_pool_reserve_prefill(pkv_pool* pool, int n_seqs, int n_head,
                              int max_q_len, int max_context_len);
 
+/* ---- a layer's mixed batch in one call (engine step of run_loop,
+ * engine.rs:62-237: some sequences prefill a prompt chunk, the others decode
+ * one token; the reference attends them one sequence at a time,
+ * transformer.rs:139-196 and 271-292) -------------------------------------
+ * The arguments of pkv_prefill_attention(_append) and of
+ * pkv_decode_attention, as two structs; n_head and scale are shared.  The
+ * result (every output row, every stored K/V row, pkv_pool_check's error
+ * bits) is identical, bit for bit, to pkv_prefill_attention(_append)
+ * followed by pkv_decode_attention on the same stream: for 16-bit pools with
+ * head_dim 64 or 128 and n_head / n_kv_head of 4 or 8 (f16 at head_dim 128:
+ * 8 only) both run in one kernel launch, their workgroups sharing the CUs
+ * (the prefill is bound by MFMA and instruction issue, the decode by HBM);
+ * other shapes run the two calls in sequence.  A NULL batch, or one with
+ * n_seqs / batch == 0, leaves just the other call.  The two batches must
+ * not share the blocks their new rows are stored in (under copy-on-write a
+ * sequence appends only to blocks it alone holds).  Workspace: the decode
+ * partials and the prefill split partials side by side
+ * (pkv_mixed_workspace_bytes). */
+typedef struct pkv_prefill_batch {
+  const void* q;               /* [total_q][n_head][head_dim], pool dtype */
+  void* out;                   /* [total_q][n_head * head_dim], out_dtype */
+  int out_dtype;
+  const int32_t* cu_q_lens;    /* [n_seqs + 1] */
+  const int32_t* context_lens; /* [n_seqs] */
+  const int32_t* block_tables; /* [n_seqs][max_blocks_per_seq] */
+  int max_blocks_per_seq;
+  int n_seqs;
+  int max_q_len;
+  int max_context_len;
+  const void* k_new;           /* chunk K/V stored by the call, or both NULL */
+  const void* v_new;
+} pkv_prefill_batch;
+
+typedef struct pkv_decode_batch {
+  const void* q;               /* [batch][n_head][head_dim], pool dtype */
+  void* out;                   /* [batch][n_head * head_dim], out_dtype */
+  int out_dtype;
+  const int32_t* block_tables; /* [batch][max_blocks_per_seq] */
+  int max_blocks_per_seq;
+  const int32_t* context_lens; /* [batch], new token included */
+  int max_context_len;
+  int batch;
+  const void* k_new;           /* new token's K/V stored by the call, or both NULL */
+  const void* v_new;
+} pkv_decode_batch;
+
+int pkv_mixed_attention(pkv_pool* pool, int layer, const pkv_prefill_batch* prefill,
+                        const pkv_decode_batch* decode, int n_head, float scale,
+                        void* stream);
+size_t pkv_mixed_workspace_bytes(const pkv_pool* pool, int n_head,
+                                 const pkv_prefill_batch* prefill,
+                                 const pkv_decode_batch* decode);
+
 /* ---- rotary position embedding (crates/ai-engine-candle/src/paged/rope.rs,
  * applied per row in the decode step, transformer.rs:252-269) ---------------
  * Tables as Rope::new (rope.rs:14-23): theta_i = 1 / freq_base^(2 i / rope_dim)
