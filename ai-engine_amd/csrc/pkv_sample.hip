@@ -120,27 +120,44 @@ __device__ __forceinline__ float logit(const char* row, int i) {
   }
 }
 
+// Vectors a thread of the exact path's row scans loads before it processes
+// them: one memory round trip per kRowBatch vectors instead of one per
+// vector (a 128k row is 16 vectors per thread).
+constexpr int kRowBatch = 8;
+
 // Calls f(i, logit) for this thread's elements of row[lo, hi), in
 // increasing i: 16-byte vectors (VEC: the row is 16-byte aligned and lo is
-// a multiple of a vector's elements), then the tail past the last vector.
-template <int DT, bool VEC, class F>
+// a multiple of a vector's elements), loaded U at a time, then the tail
+// past the last vector.
+template <int DT, bool VEC, int U = 1, class F>
 __device__ __forceinline__ void for_range(const char* row, int lo, int hi, F&& f) {
   int done = lo;
   if constexpr (VEC) {
     constexpr int E = DT == PKV_F32 ? 4 : 8;
     const int vend = hi / E;
-    for (int v = lo / E + (int)threadIdx.x; v < vend; v += kST) {
-      const u32x4 w = ld16(row + (size_t)v * 16);
-      if constexpr (DT == PKV_F32) {
+    for (int v0 = lo / E + (int)threadIdx.x; v0 < vend; v0 += U * kST) {
+      u32x4 wb[U];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) f(v * 4 + j, __uint_as_float(w[j]));
-      } else {
+      for (int u = 0; u < U; ++u) {
+        const int v = v0 + u * kST;
+        wb[u] = v < vend ? ld16(row + (size_t)v * 16) : u32x4{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lo16 = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
-          const float hi16 = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
-          f(v * 8 + 2 * j, lo16);
-          f(v * 8 + 2 * j + 1, hi16);
+      for (int u = 0; u < U; ++u) {
+        const int v = v0 + u * kST;
+        if (v >= vend) continue;  // (no break: wb stays statically indexed)
+        const u32x4 w = wb[u];
+        if constexpr (DT == PKV_F32) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) f(v * 4 + j, __uint_as_float(w[j]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float lo16 = DT == PKV_BF16 ? bf16lo(w[j]) : f16lo(w[j]);
+            const float hi16 = DT == PKV_BF16 ? bf16hi(w[j]) : f16hi(w[j]);
+            f(v * 8 + 2 * j, lo16);
+            f(v * 8 + 2 * j + 1, hi16);
+          }
         }
       }
     }
@@ -148,9 +165,9 @@ __device__ __forceinline__ void for_range(const char* row, int lo, int hi, F&& f
   }
   for (int i = done + (int)threadIdx.x; i < hi; i += kST) f(i, logit<DT>(row, i));
 }
-template <int DT, bool VEC, class F>
+template <int DT, bool VEC, int U = 1, class F>
 __device__ __forceinline__ void for_each(const char* row, int V, F&& f) {
-  for_range<DT, VEC>(row, 0, V, static_cast<F&&>(f));
+  for_range<DT, VEC, U>(row, 0, V, static_cast<F&&>(f));
 }
 
 // Larger y -> larger key; -0.0 and +0.0 compare equal, as partial_cmp has them.
@@ -436,11 +453,13 @@ __device__ __forceinline__ int nth_tied(SampleSmem& sm, const Row<DT, VEC>& rw, 
       if (k == key && (!FILTER || rw.kept(i0 + e, k))) mask |= 1u << e;
     }
     const int cnt = __popc(mask);
-    int incl = cnt;  // inclusive scan over the wave, in lane (= index) order
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    int incl = cnt;  // inclusive scan over the wave, in lane (= index) order (DPP)
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);  // row_bcast:31
     if (lane == 63) sm.red_i[wv] = incl;
     __syncthreads();
     int off = 0, tot = 0;
@@ -951,6 +970,29 @@ struct ExactSmem {
   int flag;
 };
 
+// Inclusive prefix sums across the wave in lane order on DPP: row shifts
+// within the 16-lane rows, then the row broadcasts of the lane-15 and
+// lane-31 partials (no LDS round trips).  The float version adds in a
+// different order than a serial sum (its callers use it for estimates only).
+__device__ __forceinline__ unsigned int wave_incl_add_u32(unsigned int x) {
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);
+  x += (unsigned int)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);
+  return x;
+}
+__device__ __forceinline__ float wave_incl_add_f32(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
+  return x;
+}
+
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int x) {
   return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
@@ -1020,11 +1062,7 @@ __device__ __forceinline__ bool radix_pass(ExactSmem& xs, const uint32_t* src, u
       xs.off[w][tid] = c;
       c += h;
     }
-    incl = c;
-    for (int d = 1; d < 64; d <<= 1) {
-      const unsigned int o = (unsigned int)__shfl_up((int)incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    incl = wave_incl_add_u32(c);
     if (lane == 63) xs.wtot[wv] = incl;
     if (c == (unsigned int)n) xs.flag = 1;
   }
@@ -1109,6 +1147,31 @@ __device__ __forceinline__ void compose(int& d0, int& d1, int b0, int b1) {
   d1 = min(n1, kDeltaCap);
 }
 
+// The earlier partial of a scan step: lane i gets lane i's source under DPP
+// control CTRL (rows outside ROW_MASK, and lanes without a source, get
+// (0, 0), the identity of compose).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ void dpp_compose(int& a0, int& a1) {
+  int b0 = __builtin_amdgcn_update_dpp(0, a0, CTRL, ROW_MASK, 0xf, false);
+  int b1 = __builtin_amdgcn_update_dpp(0, a1, CTRL, ROW_MASK, 0xf, false);
+  compose(b0, b1, a0, a1);
+  a0 = b0;
+  a1 = b1;
+}
+
+// Inclusive composition scan across the wave in lane order: lane i ends with
+// the deltas of lanes 0 .. i composed, earlier first.  Row shifts within the
+// 16-lane rows, then the row broadcasts of the lane-15 and lane-31 partials
+// (VALU data movement, no LDS round trips).
+__device__ __forceinline__ void compose_scan(int& a0, int& a1) {
+  dpp_compose<0x111>(a0, a1);        // row_shr:1
+  dpp_compose<0x112>(a0, a1);        // row_shr:2
+  dpp_compose<0x114>(a0, a1);        // row_shr:4
+  dpp_compose<0x118>(a0, a1);        // row_shr:8
+  dpp_compose<0x142, 0xa>(a0, a1);   // row_bcast:15 into rows 1 and 3
+  dpp_compose<0x143, 0xc>(a0, a1);   // row_bcast:31 into rows 2 and 3
+}
+
 // The f32 running sum s_{i+1} = fl(s_i + v_i), s_0 = 0, over v[0, len) (in
 // global memory, written before the call), up to and including the first i
 // with s_{i+1} >= thr (use_thr).  Result in xs.s (the sum reached) and
@@ -1176,11 +1239,7 @@ __device__ __forceinline__ void f32_run(ExactSmem& xs, const float* v, int len, 
     const int c0 = 2 * tid;
     const float x0 = c0 < nch ? xs.csum[c0] : 0.0f, x1 = c0 + 1 < nch ? xs.csum[c0 + 1] : 0.0f;
     const float mine = (x0 < 0.0f || x1 < 0.0f) ? -INFINITY : x0 + x1;
-    float in = mine;
-    for (int d = 1; d < 64; d <<= 1) {
-      const float o = __shfl_up(in, d, 64);
-      if (lane >= d) in += o;
-    }
+    const float in = wave_incl_add_f32(mine);
     if (lane == 63) xs.wsum[wv] = in;
     __syncthreads();
     float pre = in - mine;
@@ -1224,15 +1283,7 @@ __device__ __forceinline__ void f32_run(ExactSmem& xs, const float* v, int len, 
           } else {  // composition scan across the lanes: lane 63 holds the batch
             int p0 = tie ? a + (a & 1) : a + rnd;
             int p1 = tie ? a + ((a + 1) & 1) : a + rnd;
-            for (int k = 1; k < 64; k <<= 1) {
-              const int r0 = __shfl_up(p0, k, 64), r1 = __shfl_up(p1, k, 64);
-              if (lane >= k) {
-                int n0 = r0, n1 = r1;
-                compose(n0, n1, p0, p1);
-                p0 = n0;
-                p1 = n1;
-              }
-            }
+            compose_scan(p0, p1);
             q0 = readlane_i(p0, 63);
             q1 = readlane_i(p1, 63);
           }
@@ -1289,15 +1340,7 @@ __device__ __forceinline__ void f32_run(ExactSmem& xs, const float* v, int len, 
         // composed deltas of chunks start .. lane (identity outside the run)
         const bool in = lane >= start && lane < start + run;
         int a0 = in ? c0 : 0, a1 = in ? c1 : 0;
-        for (int k = 1; k < 64; k <<= 1) {
-          const int b0 = __shfl_up(a0, k, 64), b1 = __shfl_up(a1, k, 64);
-          if (lane >= k) {
-            int n0 = b0, n1 = b1;
-            compose(n0, n1, a0, a1);
-            a0 = n0;
-            a1 = n1;
-          }
-        }
+        compose_scan(a0, a1);
         const int n = (int)((sb & 0x7fffffu) | 0x800000u);
         const long long nend = (long long)n + ((n & 1) ? a1 : a0);
         const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
@@ -1385,7 +1428,7 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   constexpr int kBits = DT == PKV_F32 ? 32 : 16;
   constexpr uint32_t kMask = DT == PKV_F32 ? 0xffffffffu : 0xffffu;
   const bool neg = T < 0.0f;
-  for_each<DT, VEC>(x, V, [&](int i, float v) { ka[i] = kMask & ~xkey<DT>(neg ? -v : v); });
+  for_each<DT, VEC, kRowBatch>(x, V, [&](int i, float v) { ka[i] = kMask & ~xkey<DT>(neg ? -v : v); });
   __syncthreads();
   const uint32_t* sk = radix_sort(xs, ka, kb, V, kBits);
   float* p = reinterpret_cast<float*>(sk == ka ? kb : ka);
@@ -1470,11 +1513,17 @@ struct RunSmem {
   int k_end;  //   and how many copies of that run it took
   int R;
 };
+// Rows of at most kLdsRuns runs keep their runs in LDS after the histogram
+// (the running-sum walks read them one at a time, in order).
+constexpr int kLdsRuns = 4096;
+
 union RunLds {
   unsigned int hist[kHalfKeys];
   struct {
     SampleSmem sm;
     RunSmem rs;
+    uint32_t key[kLdsRuns], cnt[kLdsRuns], start[kLdsRuns];
+    float val[kLdsRuns];
   } x;
 };
 
@@ -1491,11 +1540,7 @@ struct RunArrays {
 __device__ __forceinline__ unsigned int block_excl_scan(unsigned int v, unsigned int* wtmp,
                                                         unsigned int& total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  unsigned int in = v;
-  for (int d = 1; d < 64; d <<= 1) {
-    const unsigned int o = (unsigned int)__shfl_up((int)in, d, 64);
-    if (lane >= d) in += o;
-  }
+  const unsigned int in = wave_incl_add_u32(v);
   if (lane == 63) wtmp[wv] = in;
   __syncthreads();
   unsigned int pre = in - v;
@@ -1517,11 +1562,7 @@ __device__ __forceinline__ void chunk_prefix(float* csum, float* wsum, int nch) 
   const int c0 = 2 * tid;
   const float x0 = c0 < nch ? csum[c0] : 0.0f, x1 = c0 + 1 < nch ? csum[c0 + 1] : 0.0f;
   const float mine = (x0 < 0.0f || x1 < 0.0f) ? -INFINITY : x0 + x1;
-  float in = mine;
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o = __shfl_up(in, d, 64);
-    if (lane >= d) in += o;
-  }
+  const float in = wave_incl_add_f32(mine);
   if (lane == 63) wsum[wv] = in;
   __syncthreads();
   float pre = in - mine;
@@ -1702,15 +1743,7 @@ __device__ __forceinline__ void f32_runs(RunSmem& rs, const RunArrays& ra, int R
         }
         const bool in = lane >= start && lane < start + run;
         int a0 = in ? c0 : 0, a1 = in ? c1 : 0;
-        for (int k = 1; k < 64; k <<= 1) {
-          const int b0 = __shfl_up(a0, k, 64), b1 = __shfl_up(a1, k, 64);
-          if (lane >= k) {
-            int n0 = b0, n1 = b1;
-            compose(n0, n1, a0, a1);
-            a0 = n0;
-            a1 = n1;
-          }
-        }
+        compose_scan(a0, a1);
         const int n = (int)((sb & 0x7fffffu) | 0x800000u);
         const long long nend = (long long)n + ((n & 1) ? a1 : a0);
         const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
@@ -1758,17 +1791,66 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     return;
   }
   uint32_t* base = a.scratch + (size_t)blockIdx.x * 4 * kMaxRuns;
-  const RunArrays ra{base, base + kMaxRuns, base + 2 * kMaxRuns,
-                     reinterpret_cast<float*>(base + 3 * kMaxRuns)};
+  RunArrays ra{base, base + kMaxRuns, base + 2 * kMaxRuns,
+               reinterpret_cast<float*>(base + 3 * kMaxRuns)};
   const bool neg = T < 0.0f;
 
-  // runs: the larger half of the key space first, each half's bins from the
-  // largest key down
+  // runs: one histogram of all 65,536 keys as 16-bit counts, two per LDS
+  // word; a count past 65,535 would carry into its neighbour (or out of the
+  // word), which only lowers the counts' total, so a total below V sends the
+  // row to the two-pass 32-bit histogram below (a value held by more than
+  // 65,535 logits).
   int R = 0;
-  for (int half = 1; half >= 0; --half) {
+  bool two_pass = false;
+  {
     for (int b = tid; b < kHalfKeys; b += kST) u.hist[b] = 0u;
     __syncthreads();
-    for_each<DT, VEC>(x, V, [&](int, float v) {
+    for_each<DT, VEC, kRowBatch>(x, V, [&](int, float v) {
+      const uint32_t k = xkey<DT>(neg ? -v : v);
+      const unsigned long long act = __ballot(true);
+      const uint32_t k0 = __builtin_amdgcn_readfirstlane(k);
+      const uint32_t sh = (k & 1u) * 16u;
+      if (__ballot(k == k0) == act) {  // one key across the wave: one addition
+        if (lane == __builtin_ctzll(act)) atomicAdd(&u.hist[k >> 1], (unsigned)__popcll(act) << sh);
+      } else {
+        atomicAdd(&u.hist[k >> 1], 1u << sh);
+      }
+    });
+    __syncthreads();
+    const int whi = kHalfKeys - 1 - 32 * tid;  // this thread's 32 words (64 keys), descending
+    unsigned int nz = 0, sum = 0;
+    for (int j = 0; j < 32; ++j) {
+      const unsigned int w = u.hist[whi - j];
+      nz += (w >> 16 != 0u) + ((w & 0xffffu) != 0u);
+      sum += (w >> 16) + (w & 0xffffu);
+    }
+    unsigned int total, counted;
+    unsigned int at = block_excl_scan(nz, wtmp, total);
+    block_excl_scan(sum, wtmp, counted);
+    if (counted == (unsigned int)V) {
+      for (int j = 0; j < 32; ++j) {
+        const unsigned int w = u.hist[whi - j];
+        const uint32_t kh = 2u * (uint32_t)(whi - j) + 1u;
+        if (w >> 16) {
+          ra.key[at] = kh;
+          ra.cnt[at] = w >> 16;
+          ++at;
+        }
+        if (w & 0xffffu) {
+          ra.key[at] = kh - 1u;
+          ra.cnt[at] = w & 0xffffu;
+          ++at;
+        }
+      }
+      R = (int)total;
+    }
+    two_pass = counted != (unsigned int)V;
+    __syncthreads();  // every thread has read the histogram before it is cleared or reused
+  }
+  for (int half = 1; half >= 0 && two_pass; --half) {
+    for (int b = tid; b < kHalfKeys; b += kST) u.hist[b] = 0u;
+    __syncthreads();
+    for_each<DT, VEC, kRowBatch>(x, V, [&](int, float v) {
       const uint32_t k = xkey<DT>(neg ? -v : v);
       const bool mine = (int)(k >> 15) == half;
       const unsigned long long act = __ballot(true);
@@ -1818,6 +1900,15 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     }
     __syncthreads();
     R = rs.R;
+  }
+  if (R <= kLdsRuns) {  // the runs move to LDS: the walks below read them one by one
+    for (int r = tid; r < R; r += kST) {
+      u.x.key[r] = ra.key[r];
+      u.x.cnt[r] = ra.cnt[r];
+      u.x.start[r] = ra.start[r];
+    }
+    __syncthreads();
+    ra = RunArrays{u.x.key, u.x.cnt, u.x.start, u.x.val};
   }
   auto y_of = [&](int r) {
     const float xp = xkey_value<DT>(ra.key[r]);
