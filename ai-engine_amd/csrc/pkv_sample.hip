@@ -1401,6 +1401,10 @@ struct ExactArgs {
   int32_t* tokens;
   uint32_t* scratch;  // 2 * vocab keys per row of the launch
   int row0;           // first row of this launch
+  // f32 logits: per row, 0 when sample_runs_kernel sampled it (every logit
+  // a bf16 value), 1 when it left the row to sample_exact_kernel; null: the
+  // exact kernel samples every row
+  int32_t* fallback;
 };
 
 template <int DT, bool VEC>
@@ -1409,6 +1413,7 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   __shared__ ExactSmem xs;
   const int row = a.row0 + blockIdx.x;
   const int tid = threadIdx.x;
+  if (a.fallback && a.fallback[row] == 0) return;  // sampled by sample_runs_kernel
   const char* x = a.logits + (long long)row * a.stride_bytes;
   const int V = a.vocab;
   const float T = a.temps ? a.temps[row] : 0.0f;
@@ -1773,7 +1778,11 @@ __device__ __forceinline__ void f32_runs(RunSmem& rs, const RunArrays& ra, int R
 // Scratch: 4 kMaxRuns words per row (keys, counts, starts, values).
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
-  static_assert(DT != PKV_F32, "runs of equal values need 16-bit logits");
+  // Keys are 16-bit: of the logits themselves, or for f32 logits of their
+  // bf16 value, which is the logit itself when its low 16 bits are zero (f32
+  // logits of a bf16 model); a row with any other f32 logit is left to
+  // sample_exact_kernel (a.fallback).
+  constexpr int KT = DT == PKV_F32 ? PKV_BF16 : DT;
   __shared__ RunLds u;
   __shared__ unsigned int wtmp[kSW];
   SampleSmem& sm = u.x.sm;
@@ -1787,7 +1796,10 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     float bv;
     int bi;
     block_argmax<DT, VEC>(sm, x, 0, V, bv, bi);
-    if (tid == 0) a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    if (tid == 0) {
+      a.tokens[row] = bi == INT_MAX ? 0 : bi;
+      if (a.fallback) a.fallback[row] = 0;
+    }
     return;
   }
   uint32_t* base = a.scratch + (size_t)blockIdx.x * 4 * kMaxRuns;
@@ -1805,8 +1817,10 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
   {
     for (int b = tid; b < kHalfKeys; b += kST) u.hist[b] = 0u;
     __syncthreads();
+    bool inexact = false;
     for_each<DT, VEC, kRowBatch>(x, V, [&](int, float v) {
-      const uint32_t k = xkey<DT>(neg ? -v : v);
+      if constexpr (DT == PKV_F32) inexact |= (__float_as_uint(v) & 0xffffu) != 0u;
+      const uint32_t k = xkey<KT>(neg ? -v : v);
       const unsigned long long act = __ballot(true);
       const uint32_t k0 = __builtin_amdgcn_readfirstlane(k);
       const uint32_t sh = (k & 1u) * 16u;
@@ -1816,7 +1830,13 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
         atomicAdd(&u.hist[k >> 1], 1u << sh);
       }
     });
-    __syncthreads();
+    if constexpr (DT == PKV_F32) {
+      const bool leave = __syncthreads_or(inexact);
+      if (tid == 0) a.fallback[row] = leave ? 1 : 0;
+      if (leave) return;  // uniform: the row needs the f32 sort
+    } else {
+      __syncthreads();
+    }
     const int whi = kHalfKeys - 1 - 32 * tid;  // this thread's 32 words (64 keys), descending
     unsigned int nz = 0, sum = 0;
     for (int j = 0; j < 32; ++j) {
@@ -1851,7 +1871,7 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     for (int b = tid; b < kHalfKeys; b += kST) u.hist[b] = 0u;
     __syncthreads();
     for_each<DT, VEC, kRowBatch>(x, V, [&](int, float v) {
-      const uint32_t k = xkey<DT>(neg ? -v : v);
+      const uint32_t k = xkey<KT>(neg ? -v : v);
       const bool mine = (int)(k >> 15) == half;
       const unsigned long long act = __ballot(true);
       const uint32_t k0 = __builtin_amdgcn_readfirstlane(k);
@@ -1911,7 +1931,7 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     ra = RunArrays{u.x.key, u.x.cnt, u.x.start, u.x.val};
   }
   auto y_of = [&](int r) {
-    const float xp = xkey_value<DT>(ra.key[r]);
+    const float xp = xkey_value<KT>(ra.key[r]);
     return (neg ? -xp : xp) / T;
   };
   const float max_x = y_of(0);
@@ -1967,10 +1987,14 @@ constexpr size_t kExactScratch = 512ull << 20;
 
 template <int DT, bool VEC>
 void launch_exact_rows(const ExactArgs& a, int rows, hipStream_t stream) {
-  if constexpr (DT == PKV_F32)
+  if constexpr (DT == PKV_F32) {
+    // rows whose logits are all bf16 values run on runs of equal values;
+    // the sort kernel takes the others (a.fallback)
+    if (a.fallback) sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
     sample_exact_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
-  else
+  } else {
     sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
+  }
 }
 
 template <int DT, bool VEC>
@@ -1979,16 +2003,22 @@ hipError_t launch_exact_dt(const ExactArgs& a0, int batch, hipStream_t stream) {
     launch_exact_rows<DT, VEC>(a0, batch, stream);
     return hipGetLastError();
   }
-  // scratch per row: f32 logits, two key arrays of the radix sort; 16-bit
-  // logits, the runs (keys, counts, starts, values)
-  const size_t per_row = DT == PKV_F32 ? (size_t)2 * (size_t)a0.vocab * sizeof(uint32_t)
-                                       : (size_t)4 * kMaxRuns * sizeof(uint32_t);
+  // scratch per row: the runs (keys, counts, starts, values); f32 logits
+  // also the two key arrays of the radix sort (the kernels run one after the
+  // other), and a fallback flag per row of the call
+  const size_t runs_row = (size_t)4 * kMaxRuns * sizeof(uint32_t);
+  const size_t per_row =
+      DT == PKV_F32 ? std::max((size_t)2 * (size_t)a0.vocab * sizeof(uint32_t), runs_row)
+                    : runs_row;
   const int rows = (int)std::max<size_t>(1, std::min<size_t>(batch, kExactScratch / per_row));
+  const size_t flags = DT == PKV_F32 ? (size_t)batch * sizeof(int32_t) : 0;
   void* p = nullptr;
-  hipError_t e = hipMallocAsync(&p, per_row * rows, stream);
+  hipError_t e = hipMallocAsync(&p, per_row * rows + flags, stream);
   if (e != hipSuccess) return e;
   ExactArgs a = a0;
   a.scratch = static_cast<uint32_t*>(p);
+  if (DT == PKV_F32)
+    a.fallback = reinterpret_cast<int32_t*>(static_cast<char*>(p) + per_row * rows);
   for (int r0 = 0; r0 < batch; r0 += rows) {
     a.row0 = r0;
     launch_exact_rows<DT, VEC>(a, std::min(rows, batch - r0), stream);
@@ -2055,7 +2085,7 @@ hipError_t launch_sample_exact(const void* logits, int dtype, long long row_stri
                                float r, int32_t* tokens, hipStream_t stream) {
   const long long sb = row_stride * (long long)dtype_bytes(dtype);
   ExactArgs a{static_cast<const char*>(logits), sb, vocab, temperatures, top_k, top_p, r,
-              tokens, nullptr, 0};
+              tokens, nullptr, 0, nullptr};
   const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (batch == 1 || sb % 16 == 0);
   if (dtype == PKV_F32) return vec ? launch_exact_dt<PKV_F32, true>(a, batch, stream)
                                    : launch_exact_dt<PKV_F32, false>(a, batch, stream);

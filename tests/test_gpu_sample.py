@@ -321,6 +321,35 @@ def test_exact_batch_over_several_launches(gpu):
         assert got[b] == oracle.sample(x32[b], float(t[b]))[0], b
 
 
+def test_exact_f32_rows_of_bf16_values(gpu):
+    # f32 logits that are bf16 values (a bf16 model's logits upcast) run on
+    # runs of equal values, the others on the radix sort, in one call: every
+    # row equals the f32 restatement, and the bf16-valued rows equal the same
+    # logits passed as bf16; batches over several launches keep each row's
+    # route (70 rows of 2^20: 64 rows per launch)
+    rng = np.random.default_rng(17)
+    for B, V in ((24, 128256), (70, 1 << 20)):
+        x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+        lg = torch.from_numpy(x).to(gpu)
+        as_bf16 = lg.to(torch.bfloat16)
+        exact_rows = [b for b in range(B) if b % 3 != 1]
+        lg[exact_rows] = as_bf16[exact_rows].float()
+        if B > 24:
+            lg[65, 12345] = 0.1  # one logit with low bits: that row takes the sort
+        temps = torch.from_numpy(rng.choice([0.0, 0.7, 1.0, -1.3], B).astype(np.float32)).to(gpu)
+        got = pagedkv.sample(lg, temps, top_p=0.95).cpu().tolist()
+        x32 = lg.cpu().numpy()
+        t = temps.cpu().numpy()
+        check = range(B) if B <= 24 else (0, 1, 2, 63, 64, 65, 66, 69)
+        for b in check:
+            assert got[b] == oracle.sample(x32[b], float(t[b]), top_p=0.95)[0], (B, b)
+        via16 = pagedkv.sample(as_bf16, temps, top_p=0.95).cpu().tolist()
+        for b in exact_rows:
+            if B > 24 and b == 65:
+                continue
+            assert got[b] == via16[b], (B, b)
+
+
 def test_exact_16bit_edge_values(gpu):
     # signed zeros (one key), subnormal and largest finite f16 values, and
     # every value of a row equal except one; T < 0 reverses the order
