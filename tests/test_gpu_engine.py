@@ -3,8 +3,9 @@ kernels the way the reference's engine thread drives its forward
 (crates/ai-engine-candle/src/paged/engine.rs:62-237, transformer.rs
 prefill/decode_step): per step, copy-on-write block copies, then per layer the
 prompt chunks' K/V appended by slot mapping and prefill attention, and decode
-attention with the new token's K/V appended inside the kernel; every so often
-the pool is compacted.  Each attention output is checked against the fp64
+attention with the new token's K/V appended inside the kernel (or, in the
+mixed runs, both batches of a layer in one pkv_mixed_attention call); every
+so often the pool is compacted.  Each attention output is checked against the fp64
 closed form over the sequence's own K/V history kept on the host (so a wrong
 block table, slot, copy or move shows up as a wrong attention row).
 Tolerance: |gpu - ref| <= 1e-3 + 2e-3 |ref|."""
@@ -72,7 +73,11 @@ class Model:
         assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} off, max err {err.max():.3g}"
         self.checked += got.shape[0]
 
-    def forward(self, p):
+    def forward(self, p, mixed=False):
+        """One plan's forward.  mixed: a step with both prompt chunks and
+        decode rows runs each layer's attention as one pkv_mixed_attention
+        call (the chunk's K/V stored by the call) instead of pkv_append,
+        pkv_prefill_attention and pkv_decode_attention."""
         g, bs = self.gpu, self.bs
         if p.n_copies:
             self.cache.copy_blocks(p.copy_src, p.copy_dst)
@@ -81,46 +86,63 @@ class Model:
         for l in range(self.L):
             pool = self.cache.layer(l)
             if T:
-                k, kf = self.rows(T, self.KVH)
-                v, vf = self.rows(T, self.KVH)
-                q, qf = self.rows(T, self.H)
-                pool.append(_dev(k, g), _dev(v, g), p.slot_mapping[:T])
-                out = pool.prefill_attention(
-                    _dev(q, g), p.cu_q_lens, p.context_lens[:p.n_prefill],
-                    np.ascontiguousarray(p.block_tables[:p.n_prefill]),
-                    int(np.diff(p.cu_q_lens).max()), int(p.context_lens[:p.n_prefill].max()),
-                    out_dtype=torch.float32).cpu().numpy()
-                for r in range(p.n_prefill):
-                    a, b = int(p.cu_q_lens[r]), int(p.cu_q_lens[r + 1])
-                    hk, hv = self.history(int(p.row_seq[r]))[l]
-                    assert len(hk) == int(p.q_start[r])
-                    hk.extend(kf[a:b])
-                    hv.extend(vf[a:b])
-                    ref = _attention_f64(qf[a:b], np.stack(hk), np.stack(hv),
-                                         np.arange(int(p.q_start[r]), len(hk)), self.scale)
-                    self.check(out[a:b], ref, f"prefill layer {l} seq {int(p.row_seq[r])}")
+                pk, pkf = self.rows(T, self.KVH)
+                pv, pvf = self.rows(T, self.KVH)
+                pq, pqf = self.rows(T, self.H)
+                pre = dict(q=_dev(pq, g), cu_q_lens=p.cu_q_lens,
+                           context_lens=p.context_lens[:p.n_prefill],
+                           block_tables=np.ascontiguousarray(p.block_tables[:p.n_prefill]),
+                           max_q_len=int(np.diff(p.cu_q_lens).max()),
+                           max_context_len=int(p.context_lens[:p.n_prefill].max()),
+                           out_dtype=torch.float32)
             if D:
-                k, kf = self.rows(D, self.KVH)
-                v, vf = self.rows(D, self.KVH)
-                q, qf = self.rows(D, self.H)
+                dk, dkf = self.rows(D, self.KVH)
+                dv, dvf = self.rows(D, self.KVH)
+                dq, dqf = self.rows(D, self.H)
                 cl = p.context_lens[p.n_prefill:]
-                out = pool.decode_attention(
-                    _dev(q, g), np.ascontiguousarray(p.block_tables[p.n_prefill:]), cl,
-                    k_new=_dev(k, g), v_new=_dev(v, g), out_dtype=torch.float32).cpu().numpy()
-                for i in range(D):
-                    hk, hv = self.history(int(p.row_seq[p.n_prefill + i]))[l]
-                    assert len(hk) == int(cl[i]) - 1
-                    hk.append(kf[i])
-                    hv.append(vf[i])
-                    ref = _attention_f64(qf[i:i + 1], np.stack(hk), np.stack(hv),
-                                         [len(hk) - 1], self.scale)
-                    self.check(out[i:i + 1], ref, f"decode layer {l} seq {int(p.row_seq[p.n_prefill + i])}")
+                dec = dict(q=_dev(dq, g), block_tables=np.ascontiguousarray(p.block_tables[p.n_prefill:]),
+                           context_lens=cl, k_new=_dev(dk, g), v_new=_dev(dv, g),
+                           out_dtype=torch.float32)
+            if mixed and T and D:
+                po, do = pool.mixed_attention(dict(pre, k_new=_dev(pk, g), v_new=_dev(pv, g)), dec)
+                pout, dout = po.cpu().numpy(), do.cpu().numpy()
+            else:
+                if T:
+                    pool.append(_dev(pk, g), _dev(pv, g), p.slot_mapping[:T])
+                    a = dict(pre)
+                    pout = pool.prefill_attention(a.pop("q"), a.pop("cu_q_lens"),
+                                                  a.pop("context_lens"), a.pop("block_tables"),
+                                                  **a).cpu().numpy()
+                if D:
+                    a = dict(dec)
+                    dout = pool.decode_attention(a.pop("q"), a.pop("block_tables"),
+                                                 a.pop("context_lens"), **a).cpu().numpy()
+            for r in range(p.n_prefill if T else 0):
+                a, b = int(p.cu_q_lens[r]), int(p.cu_q_lens[r + 1])
+                hk, hv = self.history(int(p.row_seq[r]))[l]
+                assert len(hk) == int(p.q_start[r])
+                hk.extend(pkf[a:b])
+                hv.extend(pvf[a:b])
+                ref = _attention_f64(pqf[a:b], np.stack(hk), np.stack(hv),
+                                     np.arange(int(p.q_start[r]), len(hk)), self.scale)
+                self.check(pout[a:b], ref, f"prefill layer {l} seq {int(p.row_seq[r])}")
+            for i in range(D):
+                hk, hv = self.history(int(p.row_seq[p.n_prefill + i]))[l]
+                assert len(hk) == int(cl[i]) - 1
+                hk.append(dkf[i])
+                hv.append(dvf[i])
+                ref = _attention_f64(dqf[i:i + 1], np.stack(hk), np.stack(hv),
+                                     [len(hk) - 1], self.scale)
+                self.check(dout[i:i + 1], ref, f"decode layer {l} seq {int(p.row_seq[p.n_prefill + i])}")
         torch.cuda.synchronize()
         self.cache.check()
+        return bool(mixed and T and D)
 
 
-@pytest.mark.parametrize("chunk,budget,seed", [(0, 0, 1), (48, 160, 2), (16, 0, 3)])
-def test_engine_end_to_end(gpu, chunk, budget, seed):
+@pytest.mark.parametrize("chunk,budget,seed,mixed", [(0, 0, 1, False), (48, 160, 2, False),
+                                                    (16, 0, 3, False), (48, 160, 4, True),
+                                                    (16, 0, 5, True)])
+def test_engine_end_to_end(gpu, chunk, budget, seed, mixed):
     rnd = random.Random(seed)
     bs, blocks = 16, 72
     m = Model(gpu, 2, 8, 2, 128, bs, blocks, seed)
@@ -128,12 +150,12 @@ def test_engine_end_to_end(gpu, chunk, budget, seed):
     live = set()
     for _ in range(14):
         live.add(s.submit(rnd.randint(1, 260), rnd.randint(1, 40)))
-    steps = forks = compactions = copies = 0
+    steps = forks = compactions = copies = mixed_steps = 0
     while True:
         p = s.step()
         if p.n_rows == 0:
             break
-        m.forward(p)
+        mixed_steps += m.forward(p, mixed)
         copies += p.n_copies
         toks = [EOS if rnd.random() < 0.04 else 100 + rnd.randrange(1000)
                 for _ in range(p.n_producing)]
@@ -157,5 +179,6 @@ def test_engine_end_to_end(gpu, chunk, budget, seed):
                 compactions += 1
     assert s.counts() == (0, 0, blocks)
     assert forks > 0 and copies > 0 and compactions > 0 and m.checked > 0
+    assert mixed_steps > 0 or not mixed
     m.cache.check()
     m.cache.close()
