@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     mv0[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
   }
   const int ctx = clamp_ctx(a, ctx_raw, BS);
-  const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  const int n_parts = part_count(ctx, a.part_tokens, a.sub_tokens);
   if (n_parts <= 1) return;
   // entries of partitions past n_parts hold whatever the slots held: select,
   // never multiply, them away
@@ -256,7 +256,7 @@ bool decode_supported(const pkv_pool* p, int n_head) {
 }
 
 void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
-                 int* part_tokens, int* max_parts) {
+                 int* part_tokens, int* max_parts, int* sub_tokens) {
   (void)n_head;
   long long pairs = (long long)batch * p->n_kv_head;
   int mc = max_context_len > 0 ? max_context_len : 1;
@@ -274,8 +274,27 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   // Partitions start at multiples of pt, so with block_size <= pt they are
   // block-aligned and span pt / block_size blocks (one block otherwise).
   while (pt > 64 && (pt >> ilog2i(p->block_size)) > 64) pt >>= 1;
+  int mp = (mc + pt - 1) / pt;
+  // Work-list launches of full-length partitions cut each context's last pt
+  // tokens in two (block-aligned while block_size <= pt / 2): the final
+  // round of waves then holds items of at most pt / 2 tokens instead of
+  // 0 .. pt.
+  // Measured on the Llama-3-8B layer shape (ctx U[512, 4096], bf16): 205-211
+  // against 225 us per launch at B = 128 (4096 items), within the
+  // launch-to-launch spread at B = 256 (8192 items: 396-417 against
+  // 403-405 us) and 3 % slower at B = 512, where the extra partial writes
+  // and merge reads outweigh the shorter tail.  So only lists of up to
+  // PKV_DECODE_SUB_SPLIT_MAX_ITEMS full-length items are split.
+  int sub = pt;
+  if (pt == PKV_DECODE_PART_MAX && pairs * mp > kDirectMaxItems &&
+      pairs * mp <= PKV_DECODE_SUB_SPLIT_MAX_ITEMS &&
+      p->block_size <= pt / PKV_DECODE_SUB_SPLIT) {
+    sub = pt / PKV_DECODE_SUB_SPLIT;
+    mp += PKV_DECODE_SUB_SPLIT - 1;
+  }
   *part_tokens = pt;
-  *max_parts = (mc + pt - 1) / pt;
+  *max_parts = mp;
+  if (sub_tokens) *sub_tokens = sub;
 }
 
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
@@ -292,8 +311,8 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
 
 DecodeKArgs decode_kargs(const pkv_pool* p, int layer, const DecodeArgs& a, char* partials,
                          int h0, long long* items) {
-  int pt = 0, mp = 0;
-  decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
+  int pt = 0, mp = 0, sub = 0;
+  decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp, &sub);
   size_t pairs = (size_t)a.batch * p->n_kv_head;
   const int rtot = a.n_head / p->n_kv_head;
   const int R = group_width(rtot);  // kernel width; ratios above 16 run in slices of 16
@@ -312,6 +331,7 @@ DecodeKArgs decode_kargs(const pkv_pool* p, int layer, const DecodeArgs& a, char
   k.num_blocks = p->num_blocks;
   k.bs_log2 = ilog2i(p->block_size);
   k.part_tokens = pt;
+  k.sub_tokens = sub;
   k.max_parts = mp;
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.k_new = reinterpret_cast<const char*>(a.k_new);

@@ -28,6 +28,14 @@ constexpr int kWavesPerBlock = 4;
 #ifndef PKV_DECODE_MIN_ITEMS
 #define PKV_DECODE_MIN_ITEMS 2048
 #endif
+// Work-list launches of up to PKV_DECODE_SUB_SPLIT_MAX_ITEMS full-length
+// items cut each context's last PART_MAX tokens into this many parts.
+#ifndef PKV_DECODE_SUB_SPLIT
+#define PKV_DECODE_SUB_SPLIT 2
+#endif
+#ifndef PKV_DECODE_SUB_SPLIT_MAX_ITEMS
+#define PKV_DECODE_SUB_SPLIT_MAX_ITEMS 4096
+#endif
 
 // R is the number of query heads a wave carries (1, 2, 4, 8 or 16): the
 // GQA ratio itself, or the next of these widths above it, the extra heads
@@ -75,6 +83,7 @@ struct DecodeKArgs {
   int num_blocks;
   int bs_log2;
   int part_tokens;
+  int sub_tokens;  // the last PT tokens of a context split into parts of this many
   int max_parts;
   float scale_log2;
   const char* k_new;
@@ -98,6 +107,22 @@ struct DecodeKArgs {
   // given max_parts slots (small launches); 0: the longest-first work list.
   int direct;
 };
+
+// Partitions of a context of ctx tokens: nf = (ctx - 1) / PT full
+// partitions of PT tokens, then the remaining ctx - nf PT tokens (1 .. PT)
+// in parts of SUB tokens, the last one shorter (SUB == PT: ceil(ctx / PT)
+// partitions of PT).  ctx <= 0: none.  Cutting the last PT tokens finer
+// puts short items at the end of the longest-first work list, so the
+// launch's final round of waves is short (the main kernel and the merge use
+// the same layout).
+__host__ __device__ inline int part_count(int ctx, int PT, int SUB, int* nf_out = nullptr) {
+  const int nf = ctx > 0 ? (ctx - 1) / PT : 0;
+  if (nf_out) *nf_out = nf;
+  return ctx > 0 ? nf + (ctx - nf * PT + SUB - 1) / SUB : 0;
+}
+__host__ __device__ inline int part_begin(int p, int nf, int PT, int SUB) {
+  return p < nf ? p * PT : nf * PT + (p - nf) * SUB;
+}
 
 // Context lengths of up to kCtxCache sequences are staged in LDS once per
 // workgroup; the work-list search and every item's length read them there.
@@ -230,59 +255,21 @@ struct CtxLens {
   __device__ __forceinline__ int operator[](int b) const { return b < n ? lds[b] : g[b]; }
 };
 
-// Buckets of the last partitions' lengths, (j * PT / NB, (j + 1) * PT / NB].
+// Buckets of the last partitions' lengths, (j * SUB / NB, (j + 1) * SUB / NB].
 constexpr int kLptBuckets = 16;
 
-// Work list of one launch, in dispatch order: first every full partition
-// (p < n_parts(b) - 1, PT tokens each) in sequence order, then the last,
-// shorter partition of every sequence (p = n_parts(b) - 1; p = 0 with an
-// empty context) from the longest length bucket down, sequence order within
-// a bucket.  Hardware dispatch in grid order then approximates
-// longest-processing-time-first scheduling, and the grid's surplus waves
-// (the host sizes it for the longest context) sit past the end of the list.
-// Each wave finds its (b, p) from the context lengths, 64 sequences per
-// step: a wave prefix sum of full-partition counts, per-bucket ballot
-// counts of the last partitions, and the rank of the wanted sequence within
-// its bucket.
-__device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long kpair, int lane,
-                            int BS, int& b, int& p) {
-  const int PT = a.part_tokens;
-  long long base = 0;
-  for (int b0 = 0; b0 < a.batch; b0 += 64) {
-    const int bb = b0 + lane;
-    int f = 0;
-    if (bb < a.batch) {
-      const int ctx = clamp_ctx(a, cl[bb], BS);
-      const int np = (ctx + PT - 1) / PT;
-      f = np > 1 ? np - 1 : 0;
-    }
-    const int incl = wave_incl_scan(f, lane);
-    const int excl = incl - f;
-    const unsigned long long hit = __ballot(kpair >= base + excl && kpair < base + incl);
-    if (hit) {
-      const int hl = __ffsll((long long)hit) - 1;
-      b = b0 + hl;
-      p = (int)(kpair - base - readlane_i(excl, hl));
-      return true;
-    }
-    base += readlane_i(incl, 63);
-  }
-  long long k2 = kpair - base;
-  if (k2 >= a.batch) return false;
-
-  // Last partition of sequence bb: its bucket and partition index.
-  auto last_of = [&](int bb, int& np) -> int {
-    const int ctx = clamp_ctx(a, cl[bb], BS);
-    np = (ctx + PT - 1) / PT;
-    const int len = ctx - (np > 0 ? np - 1 : 0) * PT;  // 0 (empty context) .. PT
-    return len <= 0 ? 0 : (len - 1) * kLptBuckets / PT;
-  };
+// The sequence of rank k (0-based) when the batch is ordered by bucket
+// (bucket_of(b) in [0, kLptBuckets), highest bucket first) and by sequence
+// index within a bucket: per-bucket ballot counts over the batch, then the
+// rank of the wanted sequence within its bucket.  Wave-uniform.
+template <typename BucketOf>
+__device__ __forceinline__ bool nth_by_bucket(int batch, long long k, int lane,
+                                              BucketOf bucket_of, int& b) {
   int cnt[kLptBuckets];
 #pragma unroll
   for (int j = 0; j < kLptBuckets; ++j) cnt[j] = 0;
-  for (int b0 = 0; b0 < a.batch; b0 += 64) {
-    int np = 0;
-    const int bk = b0 + lane < a.batch ? last_of(b0 + lane, np) : -1;
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const int bk = b0 + lane < batch ? bucket_of(b0 + lane) : -1;
 #pragma unroll
     for (int j = 0; j < kLptBuckets; ++j) cnt[j] += __popcll(__ballot(bk == j));
   }
@@ -290,28 +277,95 @@ __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long k
 #pragma unroll
   for (int j = kLptBuckets - 1; j >= 0; --j) {
     if (want < 0) {
-      if (k2 < cnt[j]) want = j;
-      else k2 -= cnt[j];
+      if (k < cnt[j]) want = j;
+      else k -= cnt[j];
     }
   }
-  for (int b0 = 0; b0 < a.batch; b0 += 64) {
-    int np = 0;
-    const int bk = b0 + lane < a.batch ? last_of(b0 + lane, np) : -1;
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const int bk = b0 + lane < batch ? bucket_of(b0 + lane) : -1;
     const unsigned long long mask = __ballot(bk == want);
     const int c = __popcll(mask);
-    if (k2 < c) {
+    if (k < c) {
       const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-      const unsigned long long hit = __ballot(bk == want && below == (int)k2);
-      const int hl = __ffsll((long long)hit) - 1;
-      b = b0 + hl;
-      const int npb = readlane_i(np, hl);
-      p = npb > 0 ? npb - 1 : 0;
+      const unsigned long long hit = __ballot(bk == want && below == (int)k);
+      b = b0 + __ffsll((long long)hit) - 1;
       return true;
     }
-    k2 -= c;
+    k -= c;
   }
-  return false;  // not reached: the bucket counts cover every sequence
+  return false;  // k >= batch
+}
+
+// Item k of a list made of count_of(b) consecutive items per sequence, in
+// sequence order: its sequence b and index j within the sequence, via a
+// wave prefix sum over 64 sequences per step.  Otherwise k is reduced by the
+// list's length and false returned.  Wave-uniform.
+template <typename CountOf>
+__device__ __forceinline__ bool find_in_list(int batch, long long& k, int lane, CountOf count_of,
+                                             int& b, int& j) {
+  long long base = 0;
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const int f = b0 + lane < batch ? count_of(b0 + lane) : 0;
+    const int incl = wave_incl_scan(f, lane);
+    const int excl = incl - f;
+    const unsigned long long hit = __ballot(k >= base + excl && k < base + incl);
+    if (hit) {
+      const int hl = __ffsll((long long)hit) - 1;
+      b = b0 + hl;
+      j = (int)(k - base - readlane_i(excl, hl));
+      return true;
+    }
+    base += readlane_i(incl, 63);
+  }
+  k -= base;
+  return false;
+}
+
+// Work list of one launch, in dispatch order: first every full partition
+// (p < nf(b), PT tokens each) in sequence order, then every part of a
+// sequence's last PT tokens but its last (SUB tokens each) in sequence
+// order, then the last partition of every sequence (p = n_parts(b) - 1;
+// p = 0 with an empty context) from the longest length bucket down,
+// sequence order within a bucket.  Hardware dispatch in grid order then
+// approximates longest-processing-time-first scheduling, and the grid's
+// surplus waves (the host sizes it for the longest context) sit past the
+// end of the list.  Each wave finds its (b, p) from the context lengths.
+__device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long kpair, int lane,
+                            int BS, int& b, int& p) {
+  const int PT = a.part_tokens, SUB = a.sub_tokens;
+  auto layout = [&](int bb, int& nf) { return part_count(clamp_ctx(a, cl[bb], BS), PT, SUB, &nf); };
+  long long k = kpair;
+  int j = 0;
+  if (find_in_list(a.batch, k, lane, [&](int bb) { int nf; layout(bb, nf); return nf; }, b, j)) {
+    p = j;
+    return true;
+  }
+  if (SUB < PT &&
+      find_in_list(a.batch, k, lane, [&](int bb) {
+        int nf;
+        const int np = layout(bb, nf);
+        return np > nf + 1 ? np - nf - 1 : 0;
+      }, b, j)) {
+    int nf;
+    layout(b, nf);
+    p = nf + j;
+    return true;
+  }
+  if (k >= a.batch) return false;
+  // the last partition: its length bucket over (0, SUB]
+  auto last_bucket = [&](int bb) -> int {
+    int nf;
+    const int np = layout(bb, nf);
+    const int ctx = clamp_ctx(a, cl[bb], BS);
+    const int len = np > 0 ? ctx - part_begin(np - 1, nf, PT, SUB) : 0;  // 0 .. SUB
+    return len <= 0 ? 0 : (len - 1) * kLptBuckets / SUB;
+  };
+  if (!nth_by_bucket(a.batch, k, lane, last_bucket, b)) return false;
+  int nf;
+  const int np = layout(b, nf);
+  p = np > 0 ? np - 1 : 0;
+  return true;
 }
 
 // One workgroup of the decode launch: block index bid, LDS in sm.
@@ -332,7 +386,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int H = a.kvh * a.rtot;
   const int rq = a.rq;  // query heads of this launch per group (<= R)
   const int BS = 1 << a.bs_log2;
-  const int PT = a.part_tokens;
+  const int PT = a.part_tokens, SUB = a.sub_tokens;
   const long long item = (long long)bid * kWavesPerBlock + wave;
   const int g = (int)(item % a.kvh);
   int b = 0, p = 0;
@@ -354,14 +408,23 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
 
   const int G = lane >> 4;
   const int col = lane & 15;
-  const int t_begin = p * PT;
+  // The partition's first token and length bound: p * PT with the plain
+  // layout (known before the context length, which the direct mapping has
+  // not read yet), else from the layout of the staged length.
+  int t_begin = p * PT, plen = PT;
+  if (SUB < PT) {  // launch-uniform; work-list launches only
+    int nf;
+    part_count(clamp_ctx(a, cl[b], BS), PT, SUB, &nf);
+    t_begin = part_begin(p, nf, PT, SUB);
+    plen = p < nf ? PT : SUB;
+  }
   const int blk_begin = t_begin >> a.bs_log2;
   // Loads that do not depend on the context length go out first: the block
-  // ids a full partition spans (partitions are block-aligned and span at
-  // most 64 blocks, decode_plan; lane i holds entry blk_begin + i, ids past
-  // the sequence's blocks are never used) and, without RoPE, the Q group as
-  // the MFMA A operand (row = head lane % 16, k-slice lane / 16).
-  const int span = PT >> a.bs_log2 > 1 ? PT >> a.bs_log2 : 1;
+  // ids the partition spans (partitions are block-aligned and span at most
+  // 64 blocks, decode_plan; lane i holds entry blk_begin + i, ids past the
+  // sequence's blocks are never used) and, without RoPE, the Q group as the
+  // MFMA A operand (row = head lane % 16, k-slice lane / 16).
+  const int span = plen >> a.bs_log2 > 1 ? plen >> a.bs_log2 : 1;
   int tbl = 0;
   if (lane < span && blk_begin + lane < a.mbps)
     tbl = a.block_tables[(size_t)b * a.mbps + blk_begin + lane];
@@ -377,7 +440,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int ctx = clamp_ctx(a, ctx_raw, BS);
   const bool clamped = ctx != ctx_raw;
   if (clamped && lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
-  const int n_parts = (ctx + PT - 1) / PT;
+  const int n_parts = part_count(ctx, PT, SUB);
   const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
   const int tg = lane / C::CH;  // token group of a V load
 
@@ -396,7 +459,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   }
   if (p >= n_parts) return;
 
-  const int t_end = min(ctx, t_begin + PT);
+  const int t_end = min(ctx, t_begin + plen);
   const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= span
   const int new_pos = (a.k_new != nullptr && !clamped) ? ctx - 1 : -1;
 

@@ -156,10 +156,11 @@ struct DecodeArgs {
   int in_f32 = 0;  // q, k_new, v_new are f32 (else the pool dtype)
 };
 
-// Partition length (tokens) and number of partitions the decode kernel uses
-// for a launch; both are functions of the pool shape and the arguments only.
-void decode_plan(const pkv_pool* p, int batch, int n_head,
-                 int max_context_len, int* part_tokens, int* max_parts);
+// Partition length (tokens), the length of the parts a context's last
+// part_tokens are cut into, and the most partitions of a sequence, for a
+// decode launch; all are functions of the pool shape and the arguments only.
+void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
+                 int* part_tokens, int* max_parts, int* sub_tokens = nullptr);
 size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
                               int max_context_len);
 bool decode_supported(const pkv_pool* p, int n_head);

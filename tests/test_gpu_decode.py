@@ -161,6 +161,36 @@ def test_many_partitions_merge(gpu, dt, hd, R):
     c.close()
 
 
+def _partials_bytes(pairs, parts, width, hd):
+    ml = -(-pairs * parts * width * 2 * 4 // 256) * 256
+    return ml + pairs * parts * width * hd * 4
+
+
+@pytest.mark.parametrize("dt,hd,R,bs,fused", [(wl.BF16, 128, 4, 16, True), (wl.F16, 64, 8, 32, False),
+                                              (wl.BF16, 128, 4, 256, True), (wl.F32, 128, 2, 16, True),
+                                              (wl.BF16, 64, 3, 64, True)])
+def test_split_last_partition(gpu, dt, hd, R, bs, fused):
+    # 128 sequences x 8 kv heads with contexts up to 4096: a work list of
+    # 4096 items of 1024 tokens, short enough that the kernel cuts each
+    # context's last 1024 tokens in two (5 partitions at most, against 4 for
+    # the 8192-item list of 256 sequences); lengths on and around every
+    # 512-token edge, the rest random
+    edges = [1, 2, 511, 512, 513, 1023, 1024, 1025, 1536, 1537, 2048, 2049, 2560, 2561,
+             3072, 3073, 3584, 3585, 4095, 4096]
+    cl = edges + [int(x) for x in wl.randint(hd + R + bs, 128 - len(edges), 1, 4096)]
+    c = Case(gpu, dt, 8 * R, 8, hd, bs, [x - 1 for x in cl], seed=hd * R + bs, fused=fused)
+    L = pagedkv.lib()
+    w = 1 << (R - 1).bit_length()
+    assert L.pkv_decode_workspace_bytes(c.cache.handle, 128, 8 * R, 4096) == \
+        _partials_bytes(128 * 8, 5, w, hd)
+    assert L.pkv_decode_workspace_bytes(c.cache.handle, 256, 8 * R, 4096) == \
+        _partials_bytes(256 * 8, 4, w, hd)
+    got = c.run()
+    ref, _, _ = c.reference()
+    _close(got, ref, f"split last partition dt={dt} hd={hd} R={R} bs={bs}")
+    c.close()
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64, 256])
 def test_decode_block_sizes(gpu, bs):
     c = Case(gpu, wl.BF16, 8, 2, 128, bs, [0, bs - 2, bs - 1, bs, 3 * bs + 5, 1000], seed=bs)

@@ -25,8 +25,9 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-3, 1e-3
 
 
-@pytest.mark.parametrize("shape,B,lo,hi", [(wl.CFG3, 256, 512, 4096), (wl.CFG4, 128, 2048, 8192)],
-                         ids=["cfg3", "cfg4"])
+@pytest.mark.parametrize("shape,B,lo,hi", [(wl.CFG3, 256, 512, 4096), (wl.CFG4, 128, 2048, 8192),
+                                           (wl.CFG3, 128, 512, 4096)],
+                         ids=["cfg3", "cfg4", "cfg3-B128-split-last-partition"])
 def test_full_shape_relocation_permutation_and_oracle(gpu, shape, B, lo, hi):
     batch = wl.decode_batch(shape, B, lo, hi, seed=1234)
     H, KVH, hd, bs = shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
