@@ -611,9 +611,6 @@ static int profile_slot(pkv_pool* p, hipEvent_t* eb, hipEvent_t* ee) {
   return PKV_OK;
 }
 
-// Shared validation and launch of pkv_decode_attention(_rope, _noalloc).
-// noalloc: the partials go to the static scratch array, and nothing is
-// allocated (no workspace growth, no profile events).
 // Argument checks of a decode call with batch > 0 (PKV_OK or the failure).
 static int decode_validate(pkv_pool* p, const pkv::DecodeArgs& a) {
   if (!a.q || !a.out || !a.block_tables || !a.context_lens)
@@ -638,6 +635,9 @@ static int decode_validate(pkv_pool* p, const pkv::DecodeArgs& a) {
   return PKV_OK;
 }
 
+// Shared validation and launch of pkv_decode_attention(_rope, _noalloc).
+// noalloc: the partials go to the static scratch array, and nothing is
+// allocated (no workspace growth, no profile events).
 static int decode_call(pkv_pool* p, int layer, pkv::DecodeArgs& a, void* stream,
                        bool noalloc = false) {
   if (int rc = check_layer(p, layer)) return rc;
@@ -866,12 +866,13 @@ int pkv_mixed_attention(pkv_pool* p, int layer, const pkv_prefill_batch* pb,
     return decode_call(p, layer, a, stream);
   };
   // one batch (or an invalid count, which the single call reports)
-  if (!hp || !hd || pb->n_seqs < 0 || db->batch < 0 || !pkv::mixed_supported(p, n_head, false)) {
+  if (!hp || !hd || pb->n_seqs < 0 || db->batch < 0) {
     int rc = PKV_OK;
     if (pb) rc = prefill_only();
     if (rc == PKV_OK && db) rc = decode_only();
     return rc;
   }
+  // both batches are checked before either is enqueued
   if (int rc = prefill_validate(p, pb->q, pb->out, pb->out_dtype, pb->cu_q_lens,
                                 pb->context_lens, pb->block_tables, pb->max_blocks_per_seq,
                                 pb->max_q_len, pb->max_context_len, n_head, scale, pb->k_new,
@@ -881,6 +882,11 @@ int pkv_mixed_attention(pkv_pool* p, int layer, const pkv_prefill_batch* pb,
                      db->context_lens, db->max_context_len, db->batch, n_head, scale,
                      db->k_new, db->v_new};
   if (int rc = decode_validate(p, da)) return rc;
+  if (!pkv::mixed_supported(p, n_head, false)) {
+    int rc = prefill_only();
+    if (rc == PKV_OK) rc = decode_only();
+    return rc;
+  }
   DeviceGuard dg(p->device);
   size_t dbytes = 0, pbytes = 0;
   mixed_ws(p, n_head, *pb, *db, &dbytes, &pbytes);

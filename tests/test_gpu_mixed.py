@@ -190,4 +190,20 @@ def test_mixed_rejects_bad_arguments(gpu):
     with pytest.raises(pagedkv.PagedKvError):
         pool.mixed_attention(m.prefill, dict(m.decode, out_dtype=torch.float16), scale=m.scale)
     torch.cuda.synchronize()
+    assert m.pools_equal()  # neither batch stored its rows
+    m.close()
+
+
+def test_mixed_rejection_enqueues_neither_call(gpu):
+    # a shape the one-launch kernel does not take (f32 pool) runs the two
+    # calls in sequence; a bad decode batch still stops the prefill's stores
+    m = Mix(gpu, wl.F32, 16, 4, 64, 16, [100], [50], [300, 20], seed=4)
+    pool = m.caches[1].layer(0)
+    with pytest.raises(pagedkv.PagedKvError):
+        pool.mixed_attention(m.prefill, dict(m.decode, out_dtype=torch.float16), scale=m.scale)
+    torch.cuda.synchronize()
+    assert m.pools_equal()
+    sp, sd = m.separate(torch.float32)
+    mp, md = m.mixed(torch.float32)
+    assert _same(sp, mp) and _same(sd, md) and m.pools_equal()
     m.close()
