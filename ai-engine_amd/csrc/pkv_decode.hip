@@ -91,12 +91,13 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   constexpr int kMergeUnroll = merge_unroll<HD>();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const long long qh = (long long)blockIdx.x * kWavesPerBlock + wave;  // (b, g, h)
-  const long long pair = qh / a.rq;
-  const int h = (int)(qh - pair * a.rq);
-  if (pair >= (long long)a.batch * a.kvh) return;
-  const int b = (int)(pair / a.kvh);
-  const int g = (int)(pair % a.kvh);
+  // (b, g, h) < 2^31: decode_validate refuses larger launches
+  const unsigned qh = blockIdx.x * kWavesPerBlock + wave;
+  const unsigned pair = qh / (unsigned)a.rq;
+  const int h = (int)(qh - pair * (unsigned)a.rq);
+  if (pair >= (unsigned)a.batch * (unsigned)a.kvh) return;
+  const int b = (int)(pair / (unsigned)a.kvh);
+  const int g = (int)(pair - (unsigned)b * (unsigned)a.kvh);
   const int BS = 1 << a.bs_log2;
   const size_t pstride_ml = (size_t)R * 2;   // floats between partitions
   const size_t pstride_o = (size_t)R * HD;
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     mv0[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
   }
   const int ctx = clamp_ctx(a, ctx_raw, BS);
-  const int n_parts = part_count(ctx, a.part_tokens, a.sub_tokens);
+  const int n_parts = part_count(ctx, a.pt_log2, a.sub_log2);
   if (n_parts <= 1) return;
   // entries of partitions past n_parts hold whatever the slots held: select,
   // never multiply, them away
@@ -332,6 +333,8 @@ DecodeKArgs decode_kargs(const pkv_pool* p, int layer, const DecodeArgs& a, char
   k.bs_log2 = ilog2i(p->block_size);
   k.part_tokens = pt;
   k.sub_tokens = sub;
+  k.pt_log2 = ilog2i(pt);
+  k.sub_log2 = ilog2i(sub);
   k.max_parts = mp;
   k.scale_log2 = a.scale * 1.4426950408889634f;
   k.k_new = reinterpret_cast<const char*>(a.k_new);

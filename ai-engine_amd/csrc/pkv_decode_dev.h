@@ -84,6 +84,8 @@ struct DecodeKArgs {
   int bs_log2;
   int part_tokens;
   int sub_tokens;  // the last PT tokens of a context split into parts of this many
+  int pt_log2;     // log2 of part_tokens and sub_tokens (both powers of two)
+  int sub_log2;
   int max_parts;
   float scale_log2;
   const char* k_new;
@@ -114,14 +116,14 @@ struct DecodeKArgs {
 // partitions of PT).  ctx <= 0: none.  Cutting the last PT tokens finer
 // puts short items at the end of the longest-first work list, so the
 // launch's final round of waves is short (the main kernel and the merge use
-// the same layout).
-__host__ __device__ inline int part_count(int ctx, int PT, int SUB, int* nf_out = nullptr) {
-  const int nf = ctx > 0 ? (ctx - 1) / PT : 0;
+// the same layout).  PT = 2^ptl and SUB = 2^subl.
+__device__ __forceinline__ int part_count(int ctx, int ptl, int subl, int* nf_out = nullptr) {
+  const int nf = ctx > 0 ? (ctx - 1) >> ptl : 0;
   if (nf_out) *nf_out = nf;
-  return ctx > 0 ? nf + (ctx - nf * PT + SUB - 1) / SUB : 0;
+  return ctx > 0 ? nf + ((ctx - (nf << ptl) + (1 << subl) - 1) >> subl) : 0;
 }
-__host__ __device__ inline int part_begin(int p, int nf, int PT, int SUB) {
-  return p < nf ? p * PT : nf * PT + (p - nf) * SUB;
+__device__ __forceinline__ int part_begin(int p, int nf, int ptl, int subl) {
+  return p < nf ? p << ptl : (nf << ptl) + ((p - nf) << subl);
 }
 
 // Context lengths of up to kCtxCache sequences are staged in LDS once per
@@ -237,13 +239,17 @@ __device__ __forceinline__ int clamp_ctx(const DecodeKArgs& a, int ctx, int BS) 
   return ctx < 0 ? 0 : min(ctx, min(a.max_context_len, a.mbps * BS));
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
-__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int y = __builtin_amdgcn_ds_bpermute((lane - off) << 2, x);
-    if (lane >= off) x += y;
-  }
+// Inclusive prefix sum across the 64 lanes of a wave in lane order, on DPP:
+// shifts by 1, 2, 4 and 8 lanes within each 16-lane row (lanes shifted in
+// from outside the row add 0), then lane 15's sum broadcast into rows 1 and
+// 3 and lane 31's into rows 2 and 3 (no LDS round trips).
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return x;
 }
 
@@ -307,7 +313,7 @@ __device__ __forceinline__ bool find_in_list(int batch, long long& k, int lane, 
   long long base = 0;
   for (int b0 = 0; b0 < batch; b0 += 64) {
     const int f = b0 + lane < batch ? count_of(b0 + lane) : 0;
-    const int incl = wave_incl_scan(f, lane);
+    const int incl = wave_incl_scan(f);
     const int excl = incl - f;
     const unsigned long long hit = __ballot(k >= base + excl && k < base + incl);
     if (hit) {
@@ -333,8 +339,8 @@ __device__ __forceinline__ bool find_in_list(int batch, long long& k, int lane, 
 // end of the list.  Each wave finds its (b, p) from the context lengths.
 __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long kpair, int lane,
                             int BS, int& b, int& p) {
-  const int PT = a.part_tokens, SUB = a.sub_tokens;
-  auto layout = [&](int bb, int& nf) { return part_count(clamp_ctx(a, cl[bb], BS), PT, SUB, &nf); };
+  const int PT = a.part_tokens, SUB = a.sub_tokens, ptl = a.pt_log2, subl = a.sub_log2;
+  auto layout = [&](int bb, int& nf) { return part_count(clamp_ctx(a, cl[bb], BS), ptl, subl, &nf); };
   long long k = kpair;
   int j = 0;
   if (find_in_list(a.batch, k, lane, [&](int bb) { int nf; layout(bb, nf); return nf; }, b, j)) {
@@ -358,8 +364,8 @@ __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long k
     int nf;
     const int np = layout(bb, nf);
     const int ctx = clamp_ctx(a, cl[bb], BS);
-    const int len = np > 0 ? ctx - part_begin(np - 1, nf, PT, SUB) : 0;  // 0 .. SUB
-    return len <= 0 ? 0 : (len - 1) * kLptBuckets / SUB;
+    const int len = np > 0 ? ctx - part_begin(np - 1, nf, ptl, subl) : 0;  // 0 .. SUB
+    return len <= 0 ? 0 : ((len - 1) * kLptBuckets) >> subl;
   };
   if (!nth_by_bucket(a.batch, k, lane, last_bucket, b)) return false;
   int nf;
@@ -386,24 +392,26 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int H = a.kvh * a.rtot;
   const int rq = a.rq;  // query heads of this launch per group (<= R)
   const int BS = 1 << a.bs_log2;
-  const int PT = a.part_tokens, SUB = a.sub_tokens;
-  const long long item = (long long)bid * kWavesPerBlock + wave;
-  const int g = (int)(item % a.kvh);
+  const int PT = a.part_tokens, SUB = a.sub_tokens, ptl = a.pt_log2, subl = a.sub_log2;
+  // items (and so block ids) < 2^31: decode_validate refuses larger launches
+  const unsigned item = (unsigned)bid * kWavesPerBlock + wave;
+  const unsigned kvh = (unsigned)a.kvh;
+  const unsigned rest = item / kvh;  // item = (b, p) * kvh + g
+  const int g = (int)(item - rest * kvh);
   int b = 0, p = 0;
   CtxLens cl{a.context_lens, ctx_lds, 0};
   if (a.direct) {  // launch-uniform
     // Small launches: (b, p) straight from the item, so the wave issues its
     // context length, table slice and Q loads at once (no staging round
     // trip); slots past a sequence's partitions exit below.
-    const long long rest = item / a.kvh;
-    b = (int)(rest / a.max_parts);
-    p = (int)(rest - (long long)b * a.max_parts);
+    b = (int)(rest / (unsigned)a.max_parts);
+    p = (int)(rest - (unsigned)b * a.max_parts);
     if (b >= a.batch) return;
   } else {
     cl.n = min(a.batch, kCtxCache);
     for (int i = threadIdx.x; i < cl.n; i += kWavesPerBlock * kWave) ctx_lds[i] = a.context_lens[i];
     __syncthreads();
-    if (!locate_pair(a, cl, item / a.kvh, lane, BS, b, p)) return;
+    if (!locate_pair(a, cl, rest, lane, BS, b, p)) return;
   }
 
   const int G = lane >> 4;
@@ -414,8 +422,8 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   int t_begin = p * PT, plen = PT;
   if (SUB < PT) {  // launch-uniform; work-list launches only
     int nf;
-    part_count(clamp_ctx(a, cl[b], BS), PT, SUB, &nf);
-    t_begin = part_begin(p, nf, PT, SUB);
+    part_count(clamp_ctx(a, cl[b], BS), ptl, subl, &nf);
+    t_begin = part_begin(p, nf, ptl, subl);
     plen = p < nf ? PT : SUB;
   }
   const int blk_begin = t_begin >> a.bs_log2;
@@ -440,7 +448,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int ctx = clamp_ctx(a, ctx_raw, BS);
   const bool clamped = ctx != ctx_raw;
   if (clamped && lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
-  const int n_parts = part_count(ctx, PT, SUB);
+  const int n_parts = part_count(ctx, ptl, subl);
   const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
   const int tg = lane / C::CH;  // token group of a V load
 
