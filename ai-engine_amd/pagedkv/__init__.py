@@ -16,6 +16,7 @@ torch tensors are used only as device memory and for the current stream.
 from __future__ import annotations
 
 import ctypes
+import sys
 import math
 from typing import Sequence
 
@@ -41,9 +42,9 @@ class BlockTable:
         if not self._h:
             raise MemoryError("pkv_table_new")
 
-    def __del__(self) -> None:
+    def __del__(self, _finalizing=sys.is_finalizing) -> None:
         h = getattr(self, "_h", None)
-        if h:
+        if h and not _finalizing():
             lib().pkv_table_free(h)
             self._h = None
 
@@ -68,9 +69,9 @@ class BlockAllocator:
             raise ValueError("pkv_allocator_new: bad arguments or out of memory")
         self.block_size = block_size
 
-    def __del__(self) -> None:
+    def __del__(self, _finalizing=sys.is_finalizing) -> None:
         h = getattr(self, "_h", None)
-        if h:
+        if h and not _finalizing():
             lib().pkv_allocator_free(h)
             self._h = None
 
@@ -231,8 +232,11 @@ class Rope:
             lib().pkv_rope_destroy(h)
             self._h = None
 
-    def __del__(self) -> None:
-        self.close()
+    def __del__(self, _finalizing=sys.is_finalizing) -> None:
+        # at interpreter exit the module's globals may already be gone; the
+        # process end releases the device memory
+        if not _finalizing():
+            self.close()
 
     def apply(self, x, positions, out_dtype=None, out=None, stream=None):
         """x: (n_tokens, n_head, rope_dim) f32/f16/bf16 on the device;
@@ -283,8 +287,11 @@ class PagedKvCache:
             lib().pkv_pool_destroy(h)
             self._h = None
 
-    def __del__(self) -> None:
-        self.close()
+    def __del__(self, _finalizing=sys.is_finalizing) -> None:
+        # at interpreter exit the module's globals may already be gone; the
+        # process end releases the device memory
+        if not _finalizing():
+            self.close()
 
     def __enter__(self):
         return self

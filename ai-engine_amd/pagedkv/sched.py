@@ -4,6 +4,7 @@ crates/ai-engine-candle/src/paged/engine.rs:62-237)."""
 from __future__ import annotations
 
 import ctypes
+import sys
 import dataclasses
 
 import numpy as np
@@ -91,9 +92,9 @@ class Scheduler:
         self.block_size = block_size
         self.kv_cache_blocks = kv_cache_blocks
 
-    def __del__(self) -> None:
+    def __del__(self, _finalizing=sys.is_finalizing) -> None:
         h = getattr(self, "_h", None)
-        if h:
+        if h and not _finalizing():
             lib().pkv_sched_destroy(h)
             self._h = None
 
