@@ -577,13 +577,14 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
 }
 
 size_t pkv_decode_workspace_bytes(const pkv_pool* p, int batch, int n_head, int max_context_len) {
-  if (!p || batch <= 0 || n_head <= 0) return 0;
+  if (!p || batch <= 0 || n_head <= 0 || max_context_len > pkv::kMaxLen) return 0;
   return pkv::decode_workspace_bytes(p, batch, n_head, max_context_len);
 }
 
 int pkv_pool_reserve_decode(pkv_pool* p, int batch, int n_head, int max_context_len) {
   CHECK_POOL(p);
-  if (batch <= 0 || n_head <= 0 || max_context_len <= 0 || n_head % p->n_kv_head != 0)
+  if (batch <= 0 || n_head <= 0 || max_context_len <= 0 || max_context_len > pkv::kMaxLen ||
+      n_head % p->n_kv_head != 0)
     return fail(p, PKV_ERR_INVALID, "reserve_decode: bad shape (batch %d, n_head %d, max_context_len %d)",
                 batch, n_head, max_context_len);
   DeviceGuard dg(p->device);
@@ -620,8 +621,9 @@ static int decode_validate(pkv_pool* p, const pkv::DecodeArgs& a) {
   if (!aligned16(a.q) || !aligned16(a.out) ||
       (a.k_new && (!aligned16(a.k_new) || !aligned16(a.v_new))))
     return fail(p, PKV_ERR_INVALID, "q, out, k_new, v_new must be 16-byte aligned");
-  if (a.max_blocks_per_seq <= 0 || a.max_context_len <= 0)
-    return fail(p, PKV_ERR_INVALID, "max_blocks_per_seq (%d) and max_context_len (%d) must be > 0",
+  if (a.max_blocks_per_seq <= 0 || a.max_context_len <= 0 || a.max_context_len > pkv::kMaxLen)
+    return fail(p, PKV_ERR_INVALID,
+                "max_blocks_per_seq (%d) must be > 0 and max_context_len (%d) in 1 .. 2^30",
                 a.max_blocks_per_seq, a.max_context_len);
   if (a.n_head <= 0 || a.n_head % p->n_kv_head != 0)
     return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", a.n_head,
@@ -738,6 +740,9 @@ int prefill_validate(pkv_pool* p, const void* q, const void* out, int out_dtype,
     return fail(p, PKV_ERR_INVALID, "k_new and v_new must be 16-byte aligned");
   if (max_q_len < 0 || max_blocks_per_seq <= 0 || max_context_len <= 0)
     return fail(p, PKV_ERR_INVALID, "max_q_len, max_blocks_per_seq, max_context_len must be > 0");
+  if (max_q_len > pkv::kMaxLen || max_context_len > pkv::kMaxLen)
+    return fail(p, PKV_ERR_INVALID, "max_q_len (%d) and max_context_len (%d) must be <= 2^30",
+                max_q_len, max_context_len);
   if (n_head <= 0 || n_head % p->n_kv_head != 0)
     return fail(p, PKV_ERR_INVALID, "n_head %d is not a multiple of n_kv_head %d", n_head, p->n_kv_head);
   if (!pkv::prefill_supported(p, n_head))
@@ -806,7 +811,9 @@ int pkv_prefill_attention_append(pkv_pool* p, int layer, const void* q, void* ou
 
 size_t pkv_prefill_workspace_bytes(const pkv_pool* p, int n_seqs, int n_head, int max_q_len,
                                    int max_context_len) {
-  if (!p || n_seqs <= 0 || max_q_len <= 0 || n_head <= 0 || n_head % p->n_kv_head) return 0;
+  if (!p || n_seqs <= 0 || max_q_len <= 0 || n_head <= 0 || n_head % p->n_kv_head ||
+      max_q_len > pkv::kMaxLen || max_context_len > pkv::kMaxLen)
+    return 0;
   int pk = 0, mp = 0;
   size_t need = 0;
   pkv::prefill_plan(p, n_seqs, n_head, max_q_len, max_context_len, &pk, &mp, &need);
@@ -816,9 +823,10 @@ size_t pkv_prefill_workspace_bytes(const pkv_pool* p, int n_seqs, int n_head, in
 int pkv_pool_reserve_prefill(pkv_pool* p, int n_seqs, int n_head, int max_q_len,
                              int max_context_len) {
   CHECK_POOL(p);
-  if (n_seqs < 0 || max_q_len < 0 || n_head <= 0 || n_head % p->n_kv_head)
-    return fail(p, PKV_ERR_INVALID, "reserve_prefill: n_seqs %d, max_q_len %d, n_head %d",
-                n_seqs, max_q_len, n_head);
+  if (n_seqs < 0 || max_q_len < 0 || n_head <= 0 || n_head % p->n_kv_head ||
+      max_q_len > pkv::kMaxLen || max_context_len > pkv::kMaxLen)
+    return fail(p, PKV_ERR_INVALID, "reserve_prefill: n_seqs %d, max_q_len %d, n_head %d, "
+                "max_context_len %d", n_seqs, max_q_len, n_head, max_context_len);
   size_t need = pkv_prefill_workspace_bytes(p, n_seqs, n_head, max_q_len, max_context_len);
   if (!need) return PKV_OK;
   DeviceGuard dg(p->device);
@@ -843,6 +851,9 @@ void mixed_ws(const pkv_pool* p, int n_head, const pkv_prefill_batch& pb,
 size_t pkv_mixed_workspace_bytes(const pkv_pool* p, int n_head, const pkv_prefill_batch* pb,
                                  const pkv_decode_batch* db) {
   if (!p || n_head <= 0 || n_head % p->n_kv_head) return 0;
+  if ((pb && (pb->max_q_len > pkv::kMaxLen || pb->max_context_len > pkv::kMaxLen)) ||
+      (db && db->max_context_len > pkv::kMaxLen))
+    return 0;
   const bool hp = pb && pb->n_seqs > 0 && pb->max_q_len > 0;
   const bool hd = db && db->batch > 0;
   if (hp && hd) {

@@ -260,7 +260,7 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
                  int* part_tokens, int* max_parts, int* sub_tokens) {
   (void)n_head;
   long long pairs = (long long)batch * p->n_kv_head;
-  int mc = max_context_len > 0 ? max_context_len : 1;
+  const long long mc = max_context_len > 0 ? max_context_len : 1;
   // Partition length: 1024 tokens (512 KB of K+V per bf16 head of 128).
   // The split-context partials (m, l, O) are written in the middle of the
   // K/V read stream, and those writes cost far more than their bytes
@@ -275,7 +275,7 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   // Partitions start at multiples of pt, so with block_size <= pt they are
   // block-aligned and span pt / block_size blocks (one block otherwise).
   while (pt > 64 && (pt >> ilog2i(p->block_size)) > 64) pt >>= 1;
-  int mp = (mc + pt - 1) / pt;
+  int mp = (int)((mc + pt - 1) / pt);  // <= 2^25 for max_context_len < 2^31
   // Work-list launches of full-length partitions cut each context's last pt
   // tokens in two (block-aligned while block_size <= pt / 2): the final
   // round of waves then holds items of at most pt / 2 tokens instead of

@@ -156,6 +156,10 @@ struct DecodeArgs {
   int in_f32 = 0;  // q, k_new, v_new are f32 (else the pool dtype)
 };
 
+// Longest max_context_len / max_q_len the attention calls accept (tokens):
+// the planners' length arithmetic stays within 32-bit ints below it.
+constexpr int kMaxLen = 1 << 30;
+
 // Partition length (tokens), the length of the parts a context's last
 // part_tokens are cut into, and the most partitions of a sequence, for a
 // decode launch; all are functions of the pool shape and the arguments only.

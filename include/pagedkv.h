@@ -191,6 +191,8 @@ int pkv_compact(pkv_pool* pool, const int32_t* src_host,
  *                (the reference's valid_lens, transformer.rs:289).
  *  max_context_len: host int >= every context_lens[b] (the reference's
  *                kv_len, transformer.rs:241); sizes the partition grid.
+ *                1 .. 2^30, and batch * n_kv_head * ceil(max_context_len /
+ *                1024) below 2^31 (else PKV_ERR_INVALID / _UNSUPPORTED).
  *  scale:        multiplies q.k (the reference uses 1/sqrt(head_dim),
  *                attention.rs:118-120).
  *  k_new, v_new: NULL, or [batch][n_kv_head][head_dim]: then the call first
@@ -261,7 +263,7 @@ int pkv_decode_attention_noalloc(pkv_pool* pool, int layer, const void* q, void*
  *  q:   [total_q][n_head][head_dim] pool dtype;  out: [total_q][n_head*head_dim].
  *  cu_q_lens: [n_seqs+1] int32; context_lens: [n_seqs] int32;
  *  block_tables: [n_seqs][max_blocks_per_seq] int32.
- *  max_q_len, max_context_len: host upper bounds.  scale > 0 and finite
+ *  max_q_len, max_context_len: host upper bounds, at most 2^30.  scale > 0 and finite
  *  (the reference's 1/sqrt(head_dim)); otherwise PKV_ERR_INVALID.
  *  Any GQA ratio n_head / n_kv_head; every pool dtype and head_dim. */
 int pkv_prefill_attention(pkv_pool* pool, int layer, const void* q, void* out,

@@ -2,6 +2,7 @@
 oracle.  Tolerance: |gpu - ref| <= 1e-3 + 2e-3 |ref|,
 fp32 accumulation; the reference output is the fp64 closed form over the
 same stored (dtype-rounded) inputs."""
+import ctypes
 import math
 
 import numpy as np
@@ -259,6 +260,33 @@ def test_out_of_range_block_id_reported(gpu):
     with pytest.raises(pagedkv.PagedKvError):
         c.run()
     c.close()
+
+
+@pytest.mark.parametrize("B,max_cl,rc_name,msg", [
+    (1024, (1 << 31) - 1, "PKV_ERR_INVALID", b"2^30"),
+    (4096, 1 << 30, "PKV_ERR_UNSUPPORTED", b"2^31")])
+def test_refuses_lengths_beyond_the_planners_range(gpu, B, max_cl, rc_name, msg):
+    # max_context_len above 2^30, and B x 8 kv heads x 2^20 partitions of
+    # 1024 tokens (more items than the kernels index in 32 bits): both
+    # refused by the argument checks, before anything is allocated or
+    # enqueued (were the second not, its partials' workspace of several TB
+    # would fail to allocate before any launch)
+    cache = pagedkv.PagedKvCache(1, 64, 16, 8, 128, torch.bfloat16)
+    H, hd = 32, 128
+    q = torch.zeros((B, H, hd), dtype=torch.bfloat16, device=gpu)
+    out = torch.zeros((B, H * hd), dtype=torch.float32, device=gpu)
+    tables = torch.zeros((B, 1), dtype=torch.int32, device=gpu)
+    cl = torch.ones(B, dtype=torch.int32, device=gpu)
+    L = pagedkv.lib()
+    rc = L.pkv_decode_attention(cache.handle, 0, q.data_ptr(), out.data_ptr(), pagedkv.F32,
+                                tables.data_ptr(), 1, cl.data_ptr(), max_cl, B, H,
+                                ctypes.c_float(0.1), None, None, None)
+    assert rc == getattr(pagedkv._lib, rc_name)
+    assert msg in L.pkv_last_error(cache.handle)
+    assert L.pkv_decode_workspace_bytes(cache.handle, B, H, (1 << 31) - 1) == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out) == 0
+    cache.close()
 
 
 @pytest.mark.parametrize("cfg,B,lo,hi", [(wl.CFG1, 8, 128, 1024), (wl.CFG2, 56, 256, 2048),
