@@ -634,14 +634,14 @@ static int decode_validate(pkv_pool* p, const pkv::DecodeArgs& a) {
   if (a.out_dtype != PKV_F32 && a.out_dtype != p->dtype)
     return fail(p, PKV_ERR_INVALID, "out_dtype must be PKV_F32 or the pool dtype");
   if (!(a.scale == a.scale)) return fail(p, PKV_ERR_INVALID, "scale is NaN");
-  // the kernels index (sequence, kv head, partition) items and merged query
-  // heads in 32 bits
+  // one 64-lane wave per (sequence, kv head, partition) item and per merged
+  // query head: the grids' work-items must fit HIP's 32-bit count
   int pt = 0, mp = 0;
   pkv::decode_plan(p, a.batch, a.n_head, a.max_context_len, &pt, &mp);
   const long long pairs = (long long)a.batch * p->n_kv_head;
-  if (pairs * std::max(mp, 16) >= (1LL << 31) - 64)
+  if (pairs * std::max(mp, 16) > (1LL << 26) - 4)
     return fail(p, PKV_ERR_UNSUPPORTED,
-                "decode: batch %d x %d kv heads x %d partitions exceeds 2^31 work items",
+                "decode: batch %d x %d kv heads x %d partitions exceeds 2^26 wave items",
                 a.batch, p->n_kv_head, mp);
   return PKV_OK;
 }

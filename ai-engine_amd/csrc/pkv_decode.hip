@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   constexpr int kMergeUnroll = merge_unroll<HD>();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  // (b, g, h) < 2^31: decode_validate refuses larger launches
+  // (b, g, h) < 2^26: decode_validate refuses larger launches
   const unsigned qh = blockIdx.x * kWavesPerBlock + wave;
   const unsigned pair = qh / (unsigned)a.rq;
   const int h = (int)(qh - pair * (unsigned)a.rq);

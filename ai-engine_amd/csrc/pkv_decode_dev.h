@@ -393,7 +393,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int rq = a.rq;  // query heads of this launch per group (<= R)
   const int BS = 1 << a.bs_log2;
   const int PT = a.part_tokens, SUB = a.sub_tokens, ptl = a.pt_log2, subl = a.sub_log2;
-  // items (and so block ids) < 2^31: decode_validate refuses larger launches
+  // items (and so block ids) < 2^26: decode_validate refuses larger launches
   const unsigned item = (unsigned)bid * kWavesPerBlock + wave;
   const unsigned kvh = (unsigned)a.kvh;
   const unsigned rest = item / kvh;  // item = (b, p) * kvh + g

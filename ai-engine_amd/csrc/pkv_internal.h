@@ -156,6 +156,13 @@ struct DecodeArgs {
   int in_f32 = 0;  // q, k_new, v_new are f32 (else the pool dtype)
 };
 
+// A 1-D launch of `blocks` workgroups of `threads` work-items: HIP counts a
+// grid's work-items in 32 bits, so launchers refuse larger ones
+// (hipErrorInvalidValue) instead of letting the grid size wrap.
+inline bool grid_fits(long long blocks, int threads) {
+  return blocks >= 0 && blocks * (long long)threads <= 0xFFFFFFFFLL;
+}
+
 // Longest max_context_len / max_q_len the attention calls accept (tokens):
 // the planners' length arithmetic stays within 32-bit ints below it.
 constexpr int kMaxLen = 1 << 30;

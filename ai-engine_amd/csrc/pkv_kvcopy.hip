@@ -313,6 +313,8 @@ hipError_t launch_append(const pkv_pool* p, int layer, const void* k,
   if (n <= 0) return hipSuccess;
   int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
   long long total = (long long)n * row_vec;
+  if (!grid_fits((total + kCopyThreads - 1) / kCopyThreads, kCopyThreads))
+    return hipErrorInvalidValue;
   unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
   append_kernel<<<grid, kCopyThreads, 0, stream>>>(
       reinterpret_cast<u32x4*>(p->layer_k(layer)),
@@ -328,6 +330,8 @@ hipError_t launch_gather(const pkv_pool* p, int layer, const int32_t* table,
   if (len <= 0) return hipSuccess;
   int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
   long long total = (long long)len * row_vec;
+  if (!grid_fits((total + kCopyThreads - 1) / kCopyThreads, kCopyThreads))
+    return hipErrorInvalidValue;
   unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
   gather_kernel<<<grid, kCopyThreads, 0, stream>>>(
       reinterpret_cast<const u32x4*>(p->layer_k(layer)),
@@ -344,6 +348,8 @@ hipError_t launch_gather_varlen(const pkv_pool* p, int layer, const int32_t* tab
   if (batch > kVarlenMaxBatch) return hipErrorInvalidValue;
   const int row_vec = (int)(p->row_bytes * p->n_kv_head / 16);
   const long long total = (long long)total_rows * row_vec;
+  if (!grid_fits((total + kCopyThreads - 1) / kCopyThreads, kCopyThreads))
+    return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((total + kCopyThreads - 1) / kCopyThreads);
   gather_varlen_kernel<<<grid, kCopyThreads, 0, stream>>>(
       reinterpret_cast<const u32x4*>(p->layer_k(layer)),

@@ -62,7 +62,7 @@ hipError_t mixed_t(PrefillKArgs pk, const DecodeKArgs& dk, long long ditems, hip
   const long long pgrid = prefill_grid<DT, HD, R>(pk);
   const long long dgrid = (ditems + kWavesPerBlock - 1) / kWavesPerBlock;
   const long long pg = (pgrid + kXcd - 1) / kXcd, dg = (dgrid + kXcd - 1) / kXcd;
-  if ((pg + dg) * kXcd >= (1ll << 31)) return hipErrorInvalidValue;
+  if (!grid_fits((pg + dg) * kXcd, kPT)) return hipErrorInvalidValue;
   if (pg + dg == 0) return hipSuccess;
   mixed_kernel<DT, HD, R, FUSED>
       <<<(unsigned)((pg + dg) * kXcd), kPT, 0, s>>>(pk, dk, (int)pg);

@@ -111,7 +111,7 @@ template <int DT, int HD, int RT>
 hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
   const long long grid = prefill_grid<DT, HD, RT>(k);
   if (grid <= 0) return hipSuccess;
-  if (grid >= (1ll << 31)) return hipErrorInvalidValue;
+  if (!grid_fits(grid, kPT)) return hipErrorInvalidValue;
   if (k.k_new)
     prefill_kernel<DT, HD, RT, true><<<(unsigned)grid, kPT, 0, s>>>(k);
   else
@@ -144,6 +144,7 @@ template <int HD>
 hipError_t pmerge(const PrefillKArgs& k, int R, int rows, int out_dt, hipStream_t s) {
   const long long blocks = (long long)k.n_seqs * k.kvh * k.row_blocks;
   if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks, 256)) return hipErrorInvalidValue;
   prefill_merge_kernel<HD><<<(unsigned)blocks, 256, 0, s>>>(k, R, rows, out_dt);
   return hipGetLastError();
 }

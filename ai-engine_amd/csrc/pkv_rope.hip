@@ -182,6 +182,8 @@ hipError_t launch_append_rope(const pkv_pool* p, int layer, const pkv_rope* r,
   const long long threads =
       (long long)n_tokens * (2 * p->n_kv_head + n_q) * (p->head_dim / 8);
   if (threads <= 0) return hipSuccess;
+  if (!grid_fits((threads + kRopeThreads - 1) / kRopeThreads, kRopeThreads))
+    return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((threads + kRopeThreads - 1) / kRopeThreads);
   append_rope_kernel<<<grid, kRopeThreads, 0, stream>>>(
       static_cast<const char*>(k), static_cast<const char*>(v), static_cast<const char*>(q),
@@ -196,6 +198,8 @@ hipError_t launch_rope_apply(const pkv_rope* r, const void* x, int in_dtype, voi
                              hipStream_t stream) {
   const long long threads = (long long)n_tokens * n_head * (r->rope_dim / 8);
   if (threads <= 0) return hipSuccess;
+  if (!grid_fits((threads + kRopeThreads - 1) / kRopeThreads, kRopeThreads))
+    return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((threads + kRopeThreads - 1) / kRopeThreads);
   rope_apply_kernel<<<grid, kRopeThreads, 0, stream>>>(
       static_cast<const char*>(x), in_dtype, static_cast<char*>(out), out_dtype, r->cos, r->sin,

@@ -1999,6 +1999,7 @@ void launch_exact_rows(const ExactArgs& a, int rows, hipStream_t stream) {
 
 template <int DT, bool VEC>
 hipError_t launch_exact_dt(const ExactArgs& a0, int batch, hipStream_t stream) {
+  if (!grid_fits(batch, kST)) return hipErrorInvalidValue;
   if (!a0.temps || a0.vocab <= 1) {  // every row is argmax: no scratch
     launch_exact_rows<DT, VEC>(a0, batch, stream);
     return hipGetLastError();
@@ -2040,6 +2041,7 @@ int split_groups(int batch, int vocab, const float* temps, int top_k, float top_
 
 template <int DT, bool VEC>
 hipError_t launch_dt(const SampleArgs& a, int batch, hipStream_t stream) {
+  if (!grid_fits(batch, kST)) return hipErrorInvalidValue;
   const int G = split_groups(batch, a.vocab, a.temps, a.top_k, a.top_p);
   if (G > 1) {
     void* p = nullptr;

@@ -191,8 +191,9 @@ int pkv_compact(pkv_pool* pool, const int32_t* src_host,
  *                (the reference's valid_lens, transformer.rs:289).
  *  max_context_len: host int >= every context_lens[b] (the reference's
  *                kv_len, transformer.rs:241); sizes the partition grid.
- *                1 .. 2^30, and batch * n_kv_head * ceil(max_context_len /
- *                1024) below 2^31 (else PKV_ERR_INVALID / _UNSUPPORTED).
+ *                1 .. 2^30, and batch * n_kv_head * max(16, ceil(
+ *                max_context_len / 1024)) below 2^26 (one 64-lane wave
+ *                each; else PKV_ERR_INVALID / _UNSUPPORTED).
  *  scale:        multiplies q.k (the reference uses 1/sqrt(head_dim),
  *                attention.rs:118-120).
  *  k_new, v_new: NULL, or [batch][n_kv_head][head_dim]: then the call first

@@ -264,10 +264,10 @@ def test_out_of_range_block_id_reported(gpu):
 
 @pytest.mark.parametrize("B,max_cl,rc_name,msg", [
     (1024, (1 << 31) - 1, "PKV_ERR_INVALID", b"2^30"),
-    (4096, 1 << 30, "PKV_ERR_UNSUPPORTED", b"2^31")])
+    (4096, 1 << 30, "PKV_ERR_UNSUPPORTED", b"2^26")])
 def test_refuses_lengths_beyond_the_planners_range(gpu, B, max_cl, rc_name, msg):
     # max_context_len above 2^30, and B x 8 kv heads x 2^20 partitions of
-    # 1024 tokens (more items than the kernels index in 32 bits): both
+    # 1024 tokens (more 64-lane waves than a grid's 32-bit count): both
     # refused by the argument checks, before anything is allocated or
     # enqueued (were the second not, its partials' workspace of several TB
     # would fail to allocate before any launch)
