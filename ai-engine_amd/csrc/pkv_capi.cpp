@@ -204,6 +204,18 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
     return fail(nullptr, PKV_ERR_UNSUPPORTED, "head_dim %d: must be 64, 128 or 256", head_dim);
   if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)
     return fail(nullptr, PKV_ERR_INVALID, "dtype %d unknown", dtype);
+  {
+    // the kernels count a block's (and a token row's) 16-byte chunks in
+    // 32-bit ints, and the slab's size must not wrap
+    const unsigned __int128 row = (unsigned __int128)head_dim * pkv::dtype_bytes(dtype);
+    const unsigned __int128 blk = row * (unsigned)block_size * (unsigned)n_kv_head;
+    const unsigned __int128 tot = blk * (unsigned)num_blocks * 2u * (unsigned)n_layers;
+    if (n_kv_head > 1024 || blk / 16 > (unsigned __int128)INT32_MAX ||
+        tot > (unsigned __int128)(SIZE_MAX / 2))
+      return fail(nullptr, PKV_ERR_UNSUPPORTED,
+                  "pool shape out of range: n_kv_head %d (at most 1024), %d blocks of %d tokens, "
+                  "%d layers", n_kv_head, num_blocks, block_size, n_layers);
+  }
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
     return fail(nullptr, PKV_ERR_INVALID, "device %d not available (%d devices)", device, ndev);

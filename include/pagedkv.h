@@ -82,7 +82,9 @@ const char* pkv_last_error(const pkv_pool* pool);
  *  - block_size a power of two in [16, 256].  The reference takes any
  *    usize (block_table.rs:17-30); its engine default and the block size of
  *    its tests is 16 (app.rs:701, tests/paged_parity.rs:33).
- * n_kv_head is any positive count; the GQA ratio n_head / n_kv_head of the
+ * n_kv_head is any count in 1 .. 1024, and the slab (2 * n_layers *
+ * num_blocks * block_size * n_kv_head * head_dim elements) below 2^63
+ * bytes (else PKV_ERR_UNSUPPORTED); the GQA ratio n_head / n_kv_head of the
  * attention calls is any positive integer (repeat_kv, attention.rs:113,
  * 128-136).  The pool is plain device memory from hipMalloc, allocated by
  * the library itself.  No kernel loads pool bytes that the same launch

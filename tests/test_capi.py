@@ -143,5 +143,12 @@ def test_pool_create_validates_before_touching_device():
     assert rc == _lib.PKV_ERR_UNSUPPORTED
     rc = L.pkv_pool_create(ctypes.byref(h), 0, 16, 16, 2, 128, pagedkv.BF16, 0)
     assert rc == _lib.PKV_ERR_INVALID
+    # shapes whose byte counts would overflow the kernels' 32-bit chunk
+    # counts or wrap the slab's size: refused before any device call
+    for n_layers, nb, bs, kvh, hd in ((1, 16, 16, 2048, 128), (1000, 1 << 30, 256, 1024, 256),
+                                      (1 << 22, 1 << 30, 16, 1, 64)):
+        rc = L.pkv_pool_create(ctypes.byref(h), n_layers, nb, bs, kvh, hd, pagedkv.F32, 0)
+        assert rc == _lib.PKV_ERR_UNSUPPORTED and not h.value
+        assert b"pool shape" in L.pkv_last_error(None)
     assert L.pkv_pool_destroy(None) == 0
     assert L.pkv_append(None, 0, None, None, None, 1, None) == _lib.PKV_ERR_INVALID
