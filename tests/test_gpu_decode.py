@@ -192,6 +192,20 @@ def test_split_last_partition(gpu, dt, hd, R, bs, fused):
     c.close()
 
 
+def test_split_layout_with_a_loose_length_bound(gpu):
+    # max_context_len 4096 (the plan cuts every context's last 1024 tokens
+    # in two) while most contexts are far shorter: items past a sequence's
+    # partitions exit, the merge reads only the partitions it has
+    ctx = [0, 1, 100, 511, 512, 513, 1023, 1024, 1500, 2049] + [int(x) for x in wl.randint(91, 118, 1, 800)]
+    c = Case(gpu, wl.BF16, 32, 8, 128, 16, ctx, seed=91, fused=True)
+    assert pagedkv.lib().pkv_decode_workspace_bytes(c.cache.handle, 128, 32, 4096) == \
+        _partials_bytes(128 * 8, 5, 4, 128)
+    got = c.run(max_context_len=4096)
+    ref, _, _ = c.reference()
+    _close(got, ref, "split layout, loose bound")
+    c.close()
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64, 256])
 def test_decode_block_sizes(gpu, bs):
     c = Case(gpu, wl.BF16, 8, 2, 128, bs, [0, bs - 2, bs - 1, bs, 3 * bs + 5, 1000], seed=bs)

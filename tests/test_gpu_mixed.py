@@ -141,6 +141,22 @@ def test_mixed_split_partials_share_the_workspace(gpu):
     m.close()
 
 
+def test_mixed_with_split_last_partitions(gpu):
+    # a decode half of 128 sequences x 8 kv heads up to 4096 tokens, whose
+    # plan cuts each context's last 1024 tokens in two, beside two prompt
+    # chunks: the one-launch result equals the two calls bit for bit
+    dctx = [int(x) for x in wl.randint(17, 128, 1, 4095)]
+    dctx[0] = 4095
+    m = Mix(gpu, wl.BF16, 32, 8, 128, 16, priors=[700, 30], chunks=[64, 200], dctx=dctx, seed=17)
+    c = m.caches[0]
+    assert c.decode_workspace_bytes(128, 32, 4096) == (
+        -(-128 * 8 * 5 * 4 * 2 * 4 // 256) * 256 + 128 * 8 * 5 * 4 * 128 * 4)
+    sp, sd = m.separate(torch.float32)
+    mp, md = m.mixed(torch.float32)
+    assert _same(sp, mp) and _same(sd, md) and m.pools_equal()
+    m.close()
+
+
 def test_mixed_cfg2_shape_and_graph_replay(gpu):
     # the TinyLlama continuous-batching mix: 8 chunks of 256 over priors
     # U[0, 1024] and 56 decodes over U[256, 2048]; replayed from a HIP graph
