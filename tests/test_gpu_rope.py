@@ -126,9 +126,20 @@ class RopeCase:
                                            (wl.BF16, wl.F32, 128, 7), (wl.F32, wl.F32, 64, 7),
                                            (wl.BF16, wl.F32, 128, 5), (wl.BF16, wl.F32, 64, 20)])
 def test_decode_attention_rope_matches_oracle(gpu, dt, in_dt, hd, R):
-    KVH = 2
-    ctx = [0, 1, 15, 16, 300, 1100, 2500]
-    case = RopeCase(gpu, dt, in_dt, R * KVH, KVH, hd, ctx, seed=hd + R + dt)
+    _rope_decode_check(gpu, dt, in_dt, hd, R, 2, [0, 1, 15, 16, 300, 1100, 2500], hd + R + dt)
+
+
+def test_decode_attention_rope_split_last_partition(gpu):
+    # 300 sequences x 2 kv heads with max_context_len 4096 (2,400 work items
+    # of 1024 tokens): the plan cuts each context's last 1024 tokens in two,
+    # with RoPE applied in the same launch; most contexts are short so the
+    # host-side pool stays small
+    ctx = [0, 511, 512, 1023, 1024, 1535, 1536, 4095] + [int(x) for x in wl.randint(33, 292, 1, 40)]
+    _rope_decode_check(gpu, wl.BF16, wl.F32, 128, 4, 2, ctx, 33)
+
+
+def _rope_decode_check(gpu, dt, in_dt, hd, R, KVH, ctx, seed):
+    case = RopeCase(gpu, dt, in_dt, R * KVH, KVH, hd, ctx, seed=seed)
     rope = pagedkv.Rope(hd, 500000.0, case.max_seq)
     cache, got = case.run_fused(rope)
     q, k, v = case.rotated()
