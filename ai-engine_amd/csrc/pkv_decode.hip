@@ -63,22 +63,42 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
 // 64 / (HD / 4) rows per load instruction), all within the launch's
 // max_parts slots of the pair; entries of partitions the sequence does not
 // have are masked out once the length is known.  Longer sequences load the
-// rest in further rounds.  The row groups are summed with lane shuffles at
+// rest in further rounds.  The row groups are summed with permlane swaps at
 // the end.  Context clamping is identical to the main kernel.
 // Row loads in flight per lane: 8 for rows of 64 (32 partitions per round,
 // which covers the small launches of short rows), else 4 (8 or 16 rows).
 template <int HD>
 constexpr int merge_unroll() { return HD == 64 ? 8 : 4; }
 
-__device__ __forceinline__ float wave_max_f(float x) {
-#pragma unroll
-  for (int mk = 1; mk < kWave; mk <<= 1) x = fmaxf(x, shfl_xor_f(x, mk));
-  return x;
+// Cross-lane steps without LDS round trips: DPP rotations within each
+// 16-lane row, and the gfx950 permlane swaps that exchange a lane's value
+// with lane ^ 16 or lane ^ 32 (each returns the pair; either order of the
+// two operands gives the same combination, so every lane of a pair holds
+// the same result).
+template <int ROR>
+__device__ __forceinline__ float row_ror_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + ROR, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_sum_f(float x) {
-#pragma unroll
-  for (int mk = 1; mk < kWave; mk <<= 1) x += shfl_xor_f(x, mk);
-  return x;
+template <bool MAX>
+__device__ __forceinline__ float comb(float a, float b) { return MAX ? fmaxf(a, b) : a + b; }
+template <bool MAX>
+__device__ __forceinline__ float with_lane_xor16(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return comb<MAX>(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+template <bool MAX>
+__device__ __forceinline__ float with_lane_xor32(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return comb<MAX>(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+// Max / sum over the wave, the result in every lane.
+template <bool MAX>
+__device__ __forceinline__ float wave_all(float x) {
+  x = comb<MAX>(x, row_ror_f<8>(x));
+  x = comb<MAX>(x, row_ror_f<4>(x));
+  x = comb<MAX>(x, row_ror_f<2>(x));
+  x = comb<MAX>(x, row_ror_f<1>(x));
+  return with_lane_xor32<MAX>(with_lane_xor16<MAX>(x));
 }
 
 template <int HD>
@@ -141,7 +161,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   float M = m0;
   for (int p0 = kWave; p0 < n_parts; p0 += kWave)
     if (p0 + lane < n_parts) M = fmaxf(M, mlb[(size_t)(p0 + lane) * pstride_ml]);
-  M = wave_max_f(M);
+  M = wave_all<true>(M);
   float L = lane < n_parts ? fast_exp2(m0 - M) * l0 : 0.0f;
   for (int p0 = kWave; p0 < n_parts; p0 += kWave) {
     const int pp = p0 + lane;
@@ -150,7 +170,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       L += fast_exp2(e[0] - M) * e[1];
     }
   }
-  L = wave_sum_f(L);
+  L = wave_all<false>(L);
 
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -177,10 +197,12 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
       for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, ov[u][i], acc[i]);
     }
   }
+  // sum the row groups: lanes c, c + LPR, ... hold one 16-byte chunk
 #pragma unroll
-  for (int mk = LPR; mk < kWave; mk <<= 1)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += shfl_xor_f(acc[i], mk);
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (LPR <= 16) acc[i] = with_lane_xor16<false>(acc[i]);
+    if constexpr (LPR <= 32) acc[i] = with_lane_xor32<false>(acc[i]);
+  }
   if (lane >= LPR) return;
 
   const float inv = 1.0f / L;
