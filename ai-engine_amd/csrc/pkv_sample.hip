@@ -210,19 +210,75 @@ __device__ __forceinline__ unsigned long long mass_of(float d) {
   return (unsigned long long)(e * kFix);
 }
 
-__device__ __forceinline__ unsigned long long shfl_up_u64(unsigned long long v, int d) {
-  const int lo = __shfl_up((int)(uint32_t)v, d, 64);
-  const int hi = __shfl_up((int)(uint32_t)(v >> 32), d, 64);
-  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+// Wave-wide steps without LDS round trips.  Reductions leave the result in
+// every lane: DPP rotations within each 16-lane row, then the gfx950
+// permlane16/32 swaps, which exchange values between lane and lane ^ 16
+// (lane ^ 32) and return both (in either order, so any combination that
+// does not depend on the order gives every lane the same result).  The
+// inclusive scan shifts within rows, then broadcasts the row sums (lanes
+// shifted in from outside a row read 0).  Every combination used here is
+// exact (integer sums, max, min, argmax), so the order is immaterial.
+template <int ROR>
+__device__ __forceinline__ uint32_t ror_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x120 + ROR, 0xf, 0xf, false);
 }
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-  const int lo = __shfl_xor((int)(uint32_t)v, m, 64);
-  const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, 64);
-  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t shr_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xf, false);
+}
+struct Pair32 { uint32_t a, b; };
+__device__ __forceinline__ Pair32 swap16_u32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+__device__ __forceinline__ Pair32 swap32_u32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return {r[0], r[1]};
+}
+__device__ __forceinline__ unsigned long long u64_of(uint32_t lo, uint32_t hi) {
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// f(own, other) applied over the wave (f commutative and associative).
+template <typename T, typename F>
+__device__ __forceinline__ T wave_reduce32(T v, F f) {
+  auto u = [](T x) { return __builtin_bit_cast(uint32_t, x); };
+  auto t = [](uint32_t x) { return __builtin_bit_cast(T, x); };
+  v = f(v, t(ror_u32<8>(u(v))));
+  v = f(v, t(ror_u32<4>(u(v))));
+  v = f(v, t(ror_u32<2>(u(v))));
+  v = f(v, t(ror_u32<1>(u(v))));
+  Pair32 p = swap16_u32(u(v));
+  v = f(t(p.a), t(p.b));
+  p = swap32_u32(u(v));
+  return f(t(p.a), t(p.b));
+}
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+  auto step = [&](uint32_t lo, uint32_t hi) { v += u64_of(lo, hi); };
+  step(ror_u32<8>((uint32_t)v), ror_u32<8>((uint32_t)(v >> 32)));
+  step(ror_u32<4>((uint32_t)v), ror_u32<4>((uint32_t)(v >> 32)));
+  step(ror_u32<2>((uint32_t)v), ror_u32<2>((uint32_t)(v >> 32)));
+  step(ror_u32<1>((uint32_t)v), ror_u32<1>((uint32_t)(v >> 32)));
+  Pair32 lo = swap16_u32((uint32_t)v), hi = swap16_u32((uint32_t)(v >> 32));
+  v = u64_of(lo.a, hi.a) + u64_of(lo.b, hi.b);
+  lo = swap32_u32((uint32_t)v);
+  hi = swap32_u32((uint32_t)(v >> 32));
+  return u64_of(lo.a, hi.a) + u64_of(lo.b, hi.b);
+}
+// Inclusive prefix sum in lane order.
+__device__ __forceinline__ unsigned long long wave_incl_u64(unsigned long long v) {
+  auto step = [&](uint32_t lo, uint32_t hi) { v += u64_of(lo, hi); };
+  step(shr_u32<0x111, 0xf>((uint32_t)v), shr_u32<0x111, 0xf>((uint32_t)(v >> 32)));  // row_shr:1
+  step(shr_u32<0x112, 0xf>((uint32_t)v), shr_u32<0x112, 0xf>((uint32_t)(v >> 32)));  // row_shr:2
+  step(shr_u32<0x114, 0xf>((uint32_t)v), shr_u32<0x114, 0xf>((uint32_t)(v >> 32)));  // row_shr:4
+  step(shr_u32<0x118, 0xf>((uint32_t)v), shr_u32<0x118, 0xf>((uint32_t)(v >> 32)));  // row_shr:8
+  step(shr_u32<0x142, 0xa>((uint32_t)v), shr_u32<0x142, 0xa>((uint32_t)(v >> 32)));  // row_bcast:15
+  step(shr_u32<0x143, 0xc>((uint32_t)v), shr_u32<0x143, 0xc>((uint32_t)(v >> 32)));  // row_bcast:31
+  return v;
 }
 
 __device__ float block_max(SampleSmem& sm, float v) {
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  v = wave_reduce32(v, [](float x, float y) { return fmaxf(x, y); });
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (lane == 0) sm.red_f[wv] = v;
   __syncthreads();
@@ -233,7 +289,7 @@ __device__ float block_max(SampleSmem& sm, float v) {
 }
 
 __device__ unsigned long long block_sum_u64(SampleSmem& sm, unsigned long long v) {
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_u64(v, m);
+  v = wave_sum_u64(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (lane == 0) sm.red_u[wv] = v;
   __syncthreads();
@@ -244,7 +300,7 @@ __device__ unsigned long long block_sum_u64(SampleSmem& sm, unsigned long long v
 }
 
 __device__ int block_min_i(SampleSmem& sm, int v) {
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, 64));
+  v = wave_reduce32(v, [](int x, int y) { return min(x, y); });
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (lane == 0) sm.red_i[wv] = v;
   __syncthreads();
@@ -270,11 +326,7 @@ __device__ void scan_buckets(SampleSmem& sm, const unsigned long long* hist, int
   const int hi = nb - 1 - tid * per;
   unsigned long long seg = 0;
   for (int j = 0; j < per; ++j) seg += hist[hi - j];
-  unsigned long long incl = seg;  // inclusive scan over the wave
-  for (int d = 1; d < 64; d <<= 1) {
-    const unsigned long long o = shfl_up_u64(incl, d);
-    if (lane >= d) incl += o;
-  }
+  unsigned long long incl = wave_incl_u64(seg);  // inclusive scan over the wave
   if (lane == 63) sm.red_u[wv] = incl;
   __syncthreads();
   for (int w = 0; w < wv; ++w) incl += sm.red_u[w];
@@ -510,13 +562,29 @@ __device__ __forceinline__ void block_argmax(SampleSmem& sm, const char* x, int 
       bi = i;
     }
   });
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(bv, m, 64);
-    const int oi = __shfl_xor(bi, m, 64);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
+  {
+    // (value, index) pairs: the larger value, the smaller index on a tie
+    auto take = [&](uint32_t ov_bits, uint32_t oi_bits) {
+      const float ov = __uint_as_float(ov_bits);
+      const int oi = (int)oi_bits;
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    };
+    take(ror_u32<8>(__float_as_uint(bv)), ror_u32<8>((uint32_t)bi));
+    take(ror_u32<4>(__float_as_uint(bv)), ror_u32<4>((uint32_t)bi));
+    take(ror_u32<2>(__float_as_uint(bv)), ror_u32<2>((uint32_t)bi));
+    take(ror_u32<1>(__float_as_uint(bv)), ror_u32<1>((uint32_t)bi));
+    Pair32 pv = swap16_u32(__float_as_uint(bv)), pi = swap16_u32((uint32_t)bi);
+    bv = __uint_as_float(pv.a);
+    bi = (int)pi.a;
+    take(pv.b, pi.b);
+    pv = swap32_u32(__float_as_uint(bv));
+    pi = swap32_u32((uint32_t)bi);
+    bv = __uint_as_float(pv.a);
+    bi = (int)pi.a;
+    take(pv.b, pi.b);
   }
   if (lane == 0) {
     sm.red_f[wv] = bv;
@@ -861,11 +929,7 @@ __global__ void __launch_bounds__(kST) split_finish_kernel(SampleArgs a, SplitWs
     if (tid < kWave) {
       const unsigned long long c =
           tid < G ? (unsigned long long)chunk_counts(ws, (int)gridDim.x, row, G, tid)[b] : 0ull;
-      unsigned long long incl = c;
-      for (int d = 1; d < kWave; d <<= 1) {
-        const unsigned long long o = shfl_up_u64(incl, d);
-        if (tid >= d) incl += o;
-      }
+      const unsigned long long incl = wave_incl_u64(c);
       const unsigned long long hit = __ballot(incl >= n);
       if (tid == 0 && !hit) sm.red_i[0] = -1;  // counts inconsistent: walk the row
       if (hit && tid == __ffsll((long long)hit) - 1) {
