@@ -379,6 +379,21 @@ int pkv_pool_fill_normal(pkv_pool* p, uint64_t seed, void* stream) {
   return PKV_OK;
 }
 
+int pkv_pool_read_blocks(pkv_pool* p, const int32_t* blocks, int n, uint64_t* sum,
+                         void* stream) {
+  CHECK_POOL(p);
+  if (n < 0) return fail(p, PKV_ERR_INVALID, "n %d < 0", n);
+  if (n == 0) return PKV_OK;
+  if (!blocks || !sum) return fail(p, PKV_ERR_INVALID, "blocks and sum must be non-NULL");
+  if ((reinterpret_cast<uintptr_t>(sum) & 7) != 0)
+    return fail(p, PKV_ERR_INVALID, "sum must be 8-byte aligned");
+  DeviceGuard dg(p->device);
+  hipError_t e = pkv::launch_read_blocks(p, blocks, n, reinterpret_cast<unsigned long long*>(sum),
+                                         static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(p, e, "read_blocks launch");
+  return PKV_OK;
+}
+
 int pkv_pool_verify_normal(pkv_pool* p, uint64_t seed, const int32_t* blocks,
                            const int32_t* origin, int n, uint64_t* mismatches, void* stream) {
   CHECK_POOL(p);

@@ -124,6 +124,11 @@ hipError_t launch_verify_normal(const pkv_pool* p, uint64_t seed, const int32_t*
                                 const int32_t* origin, int n, unsigned long long* count,
                                 hipStream_t stream);
 
+// Adds the 32-bit words of blocks[i] (every layer, K and V) into *sum
+// (device, mod 2^64): a read-only stream of the blocks.
+hipError_t launch_read_blocks(const pkv_pool* p, const int32_t* blocks, int n,
+                              unsigned long long* sum, hipStream_t stream);
+
 // Host computation of the RoPE tables (Rope::new, rope.rs:14-23).
 void rope_tables_host(int rope_dim, float freq_base, int max_seq, float* cos_t,
                       float* sin_t);

@@ -299,6 +299,64 @@ __global__ void __launch_bounds__(kCopyThreads)
   if (threadIdx.x == 0 && wg_count) atomicAdd(count, wg_count);
 }
 
+// Read-only stream over blocks[i] in every layer's K and V: items (entry,
+// K/V slab of a layer, 2048-vector chunk of a block), one item per wave and
+// step over a grid of long-lived workgroups.  Each lane issues its 32
+// sixteen-byte non-temporal loads before it adds any of them up, so a wave
+// keeps a whole 32 KiB block slab in flight (three waves per SIMD, 384 KiB
+// per CU).  The 32-bit words are summed (mod 2^64) into *sum,
+// one atomic per workgroup: the loads cannot be dropped, and the sum checks the
+// bytes.  An id out of range sets the block error bit and is skipped.
+constexpr int kReadVec = 32;                    // loads per lane per item
+constexpr int kReadChunk = kWave * kReadVec;    // 16-byte vectors per item
+__global__ void __launch_bounds__(kCopyThreads)
+    read_blocks_kernel(const char* __restrict__ base, size_t layer_bytes, int block_vec,
+                       int num_blocks, const int32_t* __restrict__ blocks, int n, int n_slabs,
+                       int chunks, unsigned long long* sum, uint32_t* err) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long long waves = (long long)gridDim.x * (kCopyThreads / kWave);
+  const long long w0 = (long long)blockIdx.x * (kCopyThreads / kWave) + (threadIdx.x >> 6);
+  unsigned long long acc = 0;
+  const long long items = (long long)n * n_slabs * chunks;
+  for (long long it = w0; it < items; it += waves) {
+    const int chunk = (int)(it % chunks);
+    const long long es = it / chunks;
+    const int slab = (int)(es % n_slabs);
+    const int b = blocks[es / n_slabs];
+    if (b < 0 || b >= num_blocks) {
+      if (lane == 0 && slab == 0 && chunk == 0) atomicOr(err, PKV_EBIT_BLOCK);
+      continue;
+    }
+    // block_vec is a multiple of 64 (block_size >= 16 rows of >= 8
+    // vectors), so whole waves of loads are in or out of the block
+    const u32x4* from = reinterpret_cast<const u32x4*>(base + (size_t)slab * layer_bytes) +
+                        (size_t)b * block_vec + chunk * kReadChunk + lane;
+    const int nj = min(kReadVec, (block_vec - chunk * kReadChunk) / kWave);
+    if (nj == kReadVec) {
+      u32x4 r[kReadVec];
+#pragma unroll
+      for (int j = 0; j < kReadVec; ++j) r[j] = __builtin_nontemporal_load(from + j * kWave);
+#pragma unroll
+      for (int j = 0; j < kReadVec; ++j) {
+        const unsigned long long lo = (unsigned long long)r[j][0] + r[j][1];
+        const unsigned long long hi = (unsigned long long)r[j][2] + r[j][3];
+        acc += lo + hi;
+      }
+    } else {
+      for (int j = 0; j < nj; ++j) {
+        const u32x4 x = __builtin_nontemporal_load(from + j * kWave);
+        acc += (unsigned long long)x[0] + x[1] + x[2] + x[3];
+      }
+    }
+  }
+  __shared__ unsigned long long wg_sum;
+  if (threadIdx.x == 0) wg_sum = 0;
+  __syncthreads();
+  if (acc) atomicAdd(&wg_sum, acc);
+  __syncthreads();
+  if (threadIdx.x == 0 && wg_sum) atomicAdd(sum, wg_sum);
+}
+
 int ilog2(int x) {
   int r = 0;
   while ((1 << r) < x) ++r;
@@ -431,6 +489,24 @@ hipError_t launch_verify_normal(const pkv_pool* p, uint64_t seed, const int32_t*
           count, p->err);
       break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_read_blocks(const pkv_pool* p, const int32_t* blocks, int n,
+                              unsigned long long* sum, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int block_vec = (int)(p->block_bytes / 16);
+  const int chunks = (block_vec + kReadChunk - 1) / kReadChunk;
+  const long long items = (long long)n * 2 * p->n_layers * chunks;
+  // three workgroups (12 waves, 384 KiB of loads) per CU: what the
+  // registers hold (158 per lane, three waves per SIMD)
+  const long long waves_per_wg = kCopyThreads / kWave;
+  const long long cap = p->n_cu > 0 ? 3LL * p->n_cu : kCopyGrid;
+  const unsigned grid =
+      (unsigned)std::min<long long>((items + waves_per_wg - 1) / waves_per_wg, cap);
+  read_blocks_kernel<<<grid, kCopyThreads, 0, stream>>>(p->base, p->layer_bytes, block_vec,
+                                                        p->num_blocks, blocks, n, 2 * p->n_layers,
+                                                        chunks, sum, p->err);
   return hipGetLastError();
 }
 

@@ -327,6 +327,21 @@ class PagedKvCache:
                                            ctypes.byref(n), _stream_ptr(stream)), self._h)
         return int(n.value)
 
+    def read_blocks(self, blocks, out=None, stream=None):
+        """Reads every byte of blocks[i] (all layers, K and V) on the device
+        and adds their 32-bit words (mod 2^64) into out, a device int64
+        tensor of one element holding the unsigned sum's bits (zeroed here
+        unless given); returns out.  Asynchronous."""
+        import torch
+        b = _i32(blocks, self.device)
+        if out is None:
+            out = torch.zeros(1, dtype=torch.int64, device=self.device)
+        if out.dtype != torch.int64 or out.numel() < 1 or not out.is_cuda:
+            raise ValueError("out must be a device int64 tensor")
+        check(lib().pkv_pool_read_blocks(self._h, _dev_ptr(b), b.numel(), _dev_ptr(out),
+                                         _stream_ptr(stream)), self._h)
+        return out
+
     def copy_blocks(self, src, dst, stream=None) -> None:
         """Copy-on-write: block dst[i] <- src[i] in every layer, K and V."""
         s = _i32(src, self.device)

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_pool_fill_normal": (_I, [_P, ctypes.c_uint64, _P]),
     "pkv_pool_verify_normal": (_I, [_P, ctypes.c_uint64, _P, _P, _I,
                                     ctypes.POINTER(ctypes.c_uint64), _P]),
+    "pkv_pool_read_blocks": (_I, [_P, _P, _I, _P, _P]),
     "pkv_append": (_I, [_P, _I, _P, _P, _P, _I, _P]),
     "pkv_append_rope": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
     "pkv_gather_seq": (_I, [_P, _I, _P, _I, _P, _P, _P]),

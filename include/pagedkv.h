@@ -124,6 +124,15 @@ int pkv_pool_verify_normal(pkv_pool* pool, uint64_t seed, const int32_t* blocks,
                            const int32_t* origin, int n, uint64_t* mismatches,
                            void* stream);
 
+/* Read every byte of blocks[i] in every layer's K and V and add their
+ * 32-bit words (mod 2^64) into *sum, a device uint64 the caller zeroes;
+ * asynchronous on `stream`.  No reference counterpart: the read rate of a
+ * random block set (the decode roofline's read ceiling, bytes read / time)
+ * and a checksum of the blocks.  blocks: device int32 [n]; an id out of
+ * range is skipped and reported by pkv_pool_check(). */
+int pkv_pool_read_blocks(pkv_pool* pool, const int32_t* blocks, int n, uint64_t* sum,
+                         void* stream);
+
 /* ---- KV append / scatter (KvPool::write, attention.rs:57-83) -----------
  * k, v: [n_tokens][n_kv_head][head_dim] in the pool dtype.
  * slot_mapping: [n_tokens] int32, slot = block * block_size + offset

@@ -368,3 +368,31 @@ def test_compactions_back_to_back_on_two_streams(gpu):
         oracle.compact(exp, 2, cache.block_bytes, src, dst)
     assert np.array_equal(_all_bytes(cache), exp)
     cache.close()
+
+
+@pytest.mark.parametrize("dt", [wl.BF16, wl.F32])
+def test_read_blocks_sums_every_word_of_the_listed_blocks(gpu, dt):
+    # the read-ceiling stream: its sum equals the numpy sum of the 32-bit
+    # words of blocks[i] over every layer's K and V (ids may repeat); an id
+    # out of range is skipped and reported, the others still summed
+    L, nb, bs, kvh, hd = 3, 300, 16, 4, 64
+    cache = pagedkv.PagedKvCache(L, nb, bs, kvh, hd, {wl.BF16: torch.bfloat16,
+                                                       wl.F32: torch.float32}[dt])
+    cache.fill_normal(41)
+    blocks = np.concatenate([wl.permutation(42, nb)[:170], [5, 5, 299, 0]]).astype(np.int32)
+    want = 0
+    for layer in range(L):
+        for which in (pagedkv.K, pagedkv.V):
+            w = cache.read_bytes(layer, which).view(np.uint32).reshape(nb, -1).astype(np.uint64)
+            want += int(w[blocks].sum())
+    got = cache.read_blocks(torch.from_numpy(blocks))
+    torch.cuda.synchronize()
+    assert int(got.cpu().numpy().view(np.uint64)[0]) == want % (1 << 64)
+    cache.check()
+    bad = np.concatenate([blocks, [nb, -1]]).astype(np.int32)
+    got = cache.read_blocks(torch.from_numpy(bad))
+    torch.cuda.synchronize()
+    assert int(got.cpu().numpy().view(np.uint64)[0]) == want % (1 << 64)
+    with pytest.raises(pagedkv.PagedKvError):
+        cache.check()
+    cache.close()
