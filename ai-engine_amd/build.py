@@ -27,6 +27,7 @@ ARCH = "gfx950"
 SOURCES = [
     "pkv_capi.cpp",
     "block_table.cpp",
+    "compact_plan.cpp",
     "pkv_sched.cpp",
     "pkv_kvcopy.hip",
     "pkv_decode.hip",

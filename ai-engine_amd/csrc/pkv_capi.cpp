@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "compact_plan.h"
 #include "pkv_internal.h"
 
 namespace {
@@ -100,82 +101,6 @@ int release_retired(pkv_pool* p) {
   return PKV_OK;
 }
 
-// ---- compaction planning ------------------------------------------------
-// Bytes of the largest plan for a pool of n blocks: at most n moves (2 ints
-// each), at most n / 2 cycles (a cycle has >= 2 moves) adding 2 ops (4 ints)
-// each, and one start per chain or cycle plus the end marker.
-size_t plan_capacity_bytes(size_t n) { return (5 * n + 2) * sizeof(int32_t); }
-
-// Moves m = (s -> d).  A move whose destination is still some other move's
-// source must wait until that block has been read: the chain is built from
-// a move whose dst is free, then repeatedly the move that fills the block
-// just vacated.  Moves left over form cycles; each cycle first parks one
-// block (dst = -1) and finally restores it (src = -1).
-int plan_compaction(pkv_pool* p, const int32_t* src, const int32_t* dst, int n,
-                    std::vector<int32_t>& ops, std::vector<int32_t>& starts) {
-  const int N = p->num_blocks;
-  std::vector<int32_t> move_from(N, -1);  // move_from[d] = s
-  std::vector<int32_t> move_to(N, -1);    // move_to[s] = d
-  for (int i = 0; i < n; ++i) {
-    int s = src[i], d = dst[i];
-    if (s < 0 || s >= N || d < 0 || d >= N)
-      return fail(p, PKV_ERR_INVALID, "compact: pair %d (%d -> %d) out of range [0, %d)", i, s, d, N);
-    if (move_to[s] != -1)
-      return fail(p, PKV_ERR_INVALID, "compact: source block %d appears twice", s);
-    if (move_from[d] != -1)
-      return fail(p, PKV_ERR_INVALID, "compact: destination block %d appears twice", d);
-    move_to[s] = d;
-    move_from[d] = s;
-  }
-  std::vector<char> done(N, 0);  // indexed by source block
-  starts.clear();
-  ops.clear();
-  for (int i = 0; i < n; ++i) {
-    int s = src[i], d = dst[i];
-    if (s == d) {
-      done[s] = 1;
-      continue;
-    }
-    if (move_to[d] != -1) continue;  // d is still someone's source: not a chain head
-    starts.push_back((int32_t)(ops.size() / 2));
-    // execute s -> d, then the move that fills s, and so on
-    int cs = s, cd = d;
-    while (true) {
-      ops.push_back(cs);
-      ops.push_back(cd);
-      done[cs] = 1;
-      int prev = move_from[cs];
-      if (prev == -1 || prev == cs || done[prev]) break;
-      cd = cs;
-      cs = prev;
-    }
-  }
-  for (int i = 0; i < n; ++i) {
-    int s = src[i];
-    if (done[s]) continue;
-    // s lies on a cycle s -> d -> ... -> s.  Park the block that moves into
-    // s's destination chain end: walk backwards from s.
-    starts.push_back((int32_t)(ops.size() / 2));
-    int first_dst = move_to[s];
-    ops.push_back(first_dst);  // park first_dst's content (it moves on)
-    ops.push_back(-1);
-    int cs = s, cd = first_dst;
-    while (true) {
-      ops.push_back(cs);
-      ops.push_back(cd);
-      done[cs] = 1;
-      int prev = move_from[cs];
-      if (prev == first_dst) break;  // first_dst's content is parked
-      cd = cs;
-      cs = prev;
-    }
-    ops.push_back(-1);  // parked content -> its destination
-    ops.push_back(cs);
-    done[first_dst] = 1;
-  }
-  starts.push_back((int32_t)(ops.size() / 2));
-  return PKV_OK;
-}
 
 }  // namespace
 
@@ -261,7 +186,7 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
   p->err = static_cast<uint32_t*>(err);
   // Compaction plan buffers (device + pinned host staging), sized once for
   // the largest plan so that pkv_compact never allocates.
-  p->plan_bytes = plan_capacity_bytes(num_blocks);
+  p->plan_bytes = pkv::plan_capacity_bytes(num_blocks);
   void* dplan = nullptr;
   void* hplan = nullptr;
   e = hipMalloc(&dplan, p->plan_bytes);
@@ -276,7 +201,7 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
     (void)hipFree(err);
     delete p;
     return fail(nullptr, PKV_ERR_OOM, "compaction plan buffers (%zu bytes): %s",
-                plan_capacity_bytes(num_blocks), hipGetErrorString(e));
+                pkv::plan_capacity_bytes(num_blocks), hipGetErrorString(e));
   }
   p->plan = static_cast<char*>(dplan);
   p->plan_host = static_cast<char*>(hplan);
@@ -565,7 +490,9 @@ int pkv_compact(pkv_pool* p, const int32_t* src_host, const int32_t* dst_host, i
   if (n == 0) return PKV_OK;
   if (!src_host || !dst_host) return fail(p, PKV_ERR_INVALID, "src_host and dst_host must be non-NULL");
   std::vector<int32_t> ops, starts;
-  if (int rc = plan_compaction(p, src_host, dst_host, n, ops, starts)) return rc;
+  std::string why;
+  if (!pkv::plan_compaction(p->num_blocks, src_host, dst_host, n, ops, starts, why))
+    return fail(p, PKV_ERR_INVALID, "compact: %s", why.c_str());
   int n_chains = (int)starts.size() - 1;
   if (n_chains <= 0) return PKV_OK;
   DeviceGuard dg(p->device);

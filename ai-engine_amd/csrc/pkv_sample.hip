@@ -984,7 +984,9 @@ __constant__ unsigned long long kExp2Tab[32] = {
 // glibc's expf: x N / ln2 = k + r (N = 32, k rounded to nearest by adding
 // 1.5 * 2^52), exp(x) = 2^(k/N) * 2^(r/N), the second factor a cubic in r
 // with the published minimax coefficients, evaluated in double and rounded
-// once to float.  The reduction r = x N / ln2 - k is one fused multiply-add
+// once to float.  Algorithm, table values and coefficients: Arm Optimized
+// Routines (math/expf.c, exp2f_data.c; Copyright (c) Arm Limited, MIT OR
+// Apache-2.0 WITH LLVM-exception), the expf glibc has used since 2.28.  The reduction r = x N / ln2 - k is one fused multiply-add
 // (as GCC contracts it when glibc is built for FMA hardware); every other
 // operation is a separately rounded double operation, in glibc's order.
 __device__ __forceinline__ float expf_glibc(float x) {

@@ -969,6 +969,9 @@ int64_t orc_sample(const float* logits, size_t n, float temperature, int top_k, 
 /* (N = 32, k by the 1.5 * 2^52 shift), r by one fused multiply-add,          */
 /* exp(x) = 2^(k/N) (table of 2^(i/32) rounded to double) times a cubic in r */
 /* with the published minimax coefficients, in double, rounded once.         */
+/* Algorithm, table values and coefficients: Arm Optimized Routines          */
+/* (math/expf.c, exp2f_data.c; Copyright (c) Arm Limited, MIT OR Apache-2.0  */
+/* WITH LLVM-exception), the expf glibc has used since 2.28.                 */
 /* orc_expf_mismatches counts the inputs where the two disagree, so a test  */
 /* can pin the restatement to the host libm on every float <= 0.             */
 /* ------------------------------------------------------------------------ */
