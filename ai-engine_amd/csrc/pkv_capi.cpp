@@ -71,33 +71,43 @@ int check_layer(pkv_pool* p, int layer) {
   return PKV_OK;
 }
 
-// Ensure the pool workspace (split-context partials of decode and of split
-// prefill; calls on the pool's stream use it in turn) holds `bytes`.  Growth
-// never waits for the device: work already queued on any stream may still
-// read the old buffer, so it is retired rather than freed (hipFree would
-// block until the device is idle) and released by pkv_pool_destroy or by an
-// explicit reserve call, both of which synchronise anyway.
-int ensure_workspace(pkv_pool* p, size_t need) {
-  if (p->ws && p->ws_bytes >= need) return PKV_OK;
-  const size_t bytes = need + need / 4;  // headroom against regrowth
-  void* ws = nullptr;
-  hipError_t e = hipMalloc(&ws, bytes);
-  if (e != hipSuccess)
-    return fail(p, PKV_ERR_OOM, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-  if (p->ws) p->ws_retired.push_back(p->ws);
-  p->ws = static_cast<char*>(ws);
-  p->ws_bytes = bytes;
-  return PKV_OK;
-}
-
 // Frees retired workspaces once the device has finished with them (the
-// explicit, synchronous reserve calls).
+// explicit, synchronous reserve calls, and workspace growth past the bound
+// below).
 int release_retired(pkv_pool* p) {
   if (p->ws_retired.empty()) return PKV_OK;
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(p, e, "hipDeviceSynchronize");
   for (char* r : p->ws_retired) (void)hipFree(r);
   p->ws_retired.clear();
+  p->ws_retired_bytes = 0;
+  return PKV_OK;
+}
+
+// Ensure the pool workspace (split-context partials of decode and of split
+// prefill; calls on the pool's stream use it in turn) holds `bytes`.  Work
+// already queued may still read the old buffer, so growth retires it rather
+// than freeing it (hipFree would block until the device is idle); retired
+// buffers are released by pkv_pool_destroy and the explicit reserve calls,
+// which synchronise anyway.  Retired bytes are bounded by the new buffer's
+// size: a growth that would keep more synchronises and frees them first.
+// Each growth is at least 1.25x, so this keeps at most one old buffer
+// (< 0.8x of the live one) and synchronises at every second growth at most.
+int ensure_workspace(pkv_pool* p, size_t need) {
+  if (p->ws && p->ws_bytes >= need) return PKV_OK;
+  const size_t bytes = need + need / 4;  // headroom against regrowth
+  if (p->ws && p->ws_retired_bytes + p->ws_bytes > bytes)
+    if (int rc = release_retired(p)) return rc;
+  void* ws = nullptr;
+  hipError_t e = hipMalloc(&ws, bytes);
+  if (e != hipSuccess)
+    return fail(p, PKV_ERR_OOM, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  if (p->ws) {
+    p->ws_retired.push_back(p->ws);
+    p->ws_retired_bytes += p->ws_bytes;
+  }
+  p->ws = static_cast<char*>(ws);
+  p->ws_bytes = bytes;
   return PKV_OK;
 }
 
@@ -825,6 +835,9 @@ int pkv_mixed_attention(pkv_pool* p, int layer, const pkv_prefill_batch* pb,
                         const pkv_decode_batch* db, int n_head, float scale, void* stream) {
   CHECK_POOL(p);
   if (int rc = check_layer(p, layer)) return rc;
+  // negative counts are refused before either batch is enqueued
+  if (pb && pb->n_seqs < 0) return fail(p, PKV_ERR_INVALID, "n_seqs %d < 0", pb->n_seqs);
+  if (db && db->batch < 0) return fail(p, PKV_ERR_INVALID, "batch %d < 0", db->batch);
   const bool hp = pb && !(pb->n_seqs == 0 || pb->max_q_len == 0);
   const bool hd = db && db->batch != 0;
   auto prefill_only = [&]() {
@@ -839,8 +852,8 @@ int pkv_mixed_attention(pkv_pool* p, int layer, const pkv_prefill_batch* pb,
                       db->k_new, db->v_new};
     return decode_call(p, layer, a, stream);
   };
-  // one batch (or an invalid count, which the single call reports)
-  if (!hp || !hd || pb->n_seqs < 0 || db->batch < 0) {
+  // one batch
+  if (!hp || !hd) {
     int rc = PKV_OK;
     if (pb) rc = prefill_only();
     if (rc == PKV_OK && db) rc = decode_only();

@@ -34,6 +34,7 @@ struct pkv_pool {
   char* ws = nullptr;
   size_t ws_bytes = 0;
   std::vector<char*> ws_retired;
+  size_t ws_retired_bytes = 0;
   // this device's copy of the static scratch array of
   // pkv_decode_attention_noalloc (looked up at pool creation)
   char* scratch = nullptr;

@@ -160,10 +160,19 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
     """Token per logits row on the device: argmax / sample() of sample.rs:12-55.
     logits: (batch, vocab) f32/f16/bf16 with unit stride along vocab;
     temperatures: (batch,) float32 on the device (None: all greedy).
-    exact=True (pkv_sample_exact): the reference's f32 arithmetic bit for bit,
-    so the token is the reference's on every row.  exact=False (pkv_sample):
-    faster; sums the probabilities exactly, so a row can differ where the
-    reference's f32 running sum lands within its rounding of r or top_p.
+    exact=True (pkv_sample_exact, the default since the engine needs the
+    reference's tokens): the reference's f32 arithmetic bit for bit, so the
+    token is the reference's on every row.  It allocates its scratch on the
+    stream for each call (hipMallocAsync, freed in stream order after the
+    launch): 1 MiB per row for 16-bit logits (the row's runs of equal
+    values); for f32 logits 8 bytes per logit (1 MiB per 128k-entry row),
+    rows taken in rounds of at most 512 MiB.  top_p=None is the reference's
+    None (no cut; passed as NaN), which differs from Some(1.0): with f32
+    sums, 1.0 cuts where the running sum first reaches 1.0.
+    exact=False (pkv_sample): faster, allocates only for rows split over
+    several workgroups; sums the probabilities exactly, so a row can differ
+    where the reference's f32 running sum lands within its rounding of r or
+    top_p (top_p=None is 1.0 there, the same as no cut in exact sums).
     Returns (batch,) int32 on the device."""
     import torch
     if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):

@@ -232,12 +232,14 @@ int pkv_decode_attention(pkv_pool* pool, int layer, const void* q, void* out,
                          void* stream);
 
 /* Workspace that pkv_decode_attention needs for a given batch/length; the
- * pool grows its internal workspace on demand with a hipMalloc and no
- * synchronisation (the buffer it replaces stays allocated until the next
- * reserve call or pkv_pool_destroy, since queued work may still read it).
- * Callers that must not allocate later (stream capture, serving loops)
- * reserve the largest shape they will use up front; the reserve calls
- * synchronise the device when they free replaced buffers. */
+ * pool grows its internal workspace on demand with a hipMalloc.  The buffer
+ * it replaces stays allocated, since queued work may still read it, until
+ * the next reserve call, pkv_pool_destroy, or a later growth that would
+ * otherwise keep more retired bytes than the new workspace holds (that
+ * growth synchronises the device and frees them).  Callers that must not
+ * allocate or synchronise later (stream capture, serving loops) reserve the
+ * largest shape they will use up front; the reserve calls synchronise the
+ * device when they free replaced buffers. */
 size_t pkv_decode_workspace_bytes(const pkv_pool* pool, int batch, int n_head,
                                   int max_context_len);
 int pkv_pool_reserve_decode(pkv_pool* pool, int batch, int n_head,

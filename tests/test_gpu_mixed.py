@@ -223,3 +223,28 @@ def test_mixed_rejection_enqueues_neither_call(gpu):
     mp, md = m.mixed(torch.float32)
     assert _same(sp, mp) and _same(sd, md) and m.pools_equal()
     m.close()
+
+
+@pytest.mark.parametrize("dt", [wl.F32, wl.BF16])
+@pytest.mark.parametrize("side", ["prefill", "decode"])
+def test_mixed_negative_count_enqueues_neither_call(gpu, monkeypatch, dt, side):
+    # a negative n_seqs or batch in either struct is refused before the
+    # other batch is enqueued, on the two-call path (f32) and the one-launch
+    # path (bf16): no chunk row is stored
+    m = Mix(gpu, dt, 16, 4, 64, 16, [100], [50], [300, 20], seed=5, fused=True)
+    pool = m.caches[1].layer(0)
+    base = pagedkv._lib.PrefillBatch if side == "prefill" else pagedkv._lib.DecodeBatch
+    field = "n_seqs" if side == "prefill" else "batch"
+
+    class Negative(base):
+        def __init__(self, *args):
+            super().__init__(*args)
+            setattr(self, field, -1)
+
+    monkeypatch.setattr(pagedkv._lib, base.__name__, Negative)
+    with pytest.raises(pagedkv.PagedKvError, match="< 0"):
+        pool.mixed_attention(m.prefill, m.decode, scale=m.scale)
+    monkeypatch.undo()
+    torch.cuda.synchronize()
+    assert m.pools_equal()
+    m.close()
