@@ -132,9 +132,9 @@ int pkv_pool_create(pkv_pool** out, int n_layers, int num_blocks,
     return fail(nullptr, PKV_ERR_INVALID,
                 "n_layers (%d), num_blocks (%d), n_kv_head (%d) must be > 0",
                 n_layers, num_blocks, n_kv_head);
-  if (!is_pow2(block_size) || block_size < 16 || block_size > 256)
+  if (!is_pow2(block_size) || block_size < 1 || block_size > 256)
     return fail(nullptr, PKV_ERR_UNSUPPORTED,
-                "block_size %d: must be a power of two in [16, 256]", block_size);
+                "block_size %d: must be a power of two in [1, 256]", block_size);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(nullptr, PKV_ERR_UNSUPPORTED, "head_dim %d: must be 64, 128 or 256", head_dim);
   if (dtype != PKV_F32 && dtype != PKV_F16 && dtype != PKV_BF16)

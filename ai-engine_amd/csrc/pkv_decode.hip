@@ -46,11 +46,11 @@
 namespace pkv {
 namespace {
 
-template <int DT, int HD, int R, bool ROPE>
+template <int DT, int HD, int R, bool ROPE, bool SB>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
   __shared__ DecodeSmem<DT, HD, R> sm;
-  decode_body<DT, HD, R, ROPE>(a, blockIdx.x, sm);
+  decode_body<DT, HD, R, ROPE, SB>(a, blockIdx.x, sm);
 }
 
 // Merge of the partitions of (b, g) for sequences with more than one
@@ -221,13 +221,18 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   }
 }
 
+// Block sizes below 16 take the kernels with per-lane block ids.
 template <int DT, int HD, int R>
 hipError_t launch_t(const DecodeKArgs& k, long long items, hipStream_t s) {
   unsigned grid = (unsigned)((items + kWavesPerBlock - 1) / kWavesPerBlock);
-  if (k.rope_cos)
-    decode_kernel<DT, HD, R, true><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
-  else
-    decode_kernel<DT, HD, R, false><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  const bool sb = k.bs_log2 < 4;
+  if (k.rope_cos) {
+    if (sb) decode_kernel<DT, HD, R, true, true><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+    else decode_kernel<DT, HD, R, true, false><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  } else {
+    if (sb) decode_kernel<DT, HD, R, false, true><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+    else decode_kernel<DT, HD, R, false, false><<<grid, kWavesPerBlock * kWave, 0, s>>>(k);
+  }
   return hipGetLastError();
 }
 

@@ -375,7 +375,11 @@ __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long k
 }
 
 // One workgroup of the decode launch: block index bid, LDS in sm.
-template <int DT, int HD, int R, bool ROPE>
+// SB (block_size below 16): the 16 tokens of a K sub-tile, and the tokens of
+// a V load, span several blocks, so each lane takes its own token's block
+// id from the partition's table slice (an LDS-crossbar permute) instead of
+// one wave-uniform id per sub-tile.
+template <int DT, int HD, int R, bool ROPE, bool SB = false>
 __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
                                             DecodeSmem<DT, HD, R>& sm) {
   using C = DCfg<DT, HD, R>;
@@ -571,20 +575,33 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const int tmask = BS - 1;
   const int lg = a.bs_log2;
 
+  // Block of a token of the partition: lane i of tbl holds the id of block
+  // blk_begin + i.  A wave-uniform token's id is a readlane; with SB each
+  // lane's own token's id is a permute across the lanes.
+  auto lane_block = [&](int tok) {
+    return __builtin_amdgcn_ds_bpermute(((tok >> lg) - blk_begin) << 2, tbl);
+  };
   // K fragment f of sub-tile st: token lane % 16, k-slice lane / 16; the four
-  // lanes of a token read 64 contiguous bytes.  block_size >= 16, so the 16
+  // lanes of a token read 64 contiguous bytes.  With block_size >= 16 the 16
   // tokens of a sub-tile share one block.
   auto k_row = [&](int tile_base, int st) {
     const int t0 = min(tile_base + 16 * st, t_end - 1);
     const int tok = min(tile_base + 16 * st + col, t_end - 1);
+    if constexpr (SB)
+      return kh + (size_t)lane_block(tok) * blk_stride +
+             ((uint32_t)((tok & tmask) * slot_stride) + 16 * G);
     const char* base = kh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
     return base + ((uint32_t)((tok & tmask) * slot_stride) + 16 * G);
   };
-  // V load i of a tile: TPL consecutive tokens (one block), lane = (token
-  // group tg, 16-byte chunk c): consecutive lanes read consecutive bytes.
+  // V load i of a tile: TPL consecutive tokens (one block when block_size
+  // >= TPL), lane = (token group tg, 16-byte chunk c): consecutive lanes
+  // read consecutive bytes.
   auto v_chunk = [&](int tile_base, int i) {
     const int t0 = min(tile_base + i * C::TPL, t_end - 1);
     const int tok = min(tile_base + i * C::TPL + tg, t_end - 1);
+    if constexpr (SB)
+      return vh + (size_t)lane_block(tok) * blk_stride +
+             ((uint32_t)((tok & tmask) * slot_stride) + 16 * c);
     const char* base = vh + (size_t)readlane_i(tbl, (t0 >> lg) - blk_begin) * blk_stride;
     return base + ((uint32_t)((tok & tmask) * slot_stride) + 16 * c);
   };

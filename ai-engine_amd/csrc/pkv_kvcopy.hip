@@ -327,12 +327,10 @@ __global__ void __launch_bounds__(kCopyThreads)
       if (lane == 0 && slab == 0 && chunk == 0) atomicOr(err, PKV_EBIT_BLOCK);
       continue;
     }
-    // block_vec is a multiple of 64 (block_size >= 16 rows of >= 8
-    // vectors), so whole waves of loads are in or out of the block
     const u32x4* from = reinterpret_cast<const u32x4*>(base + (size_t)slab * layer_bytes) +
                         (size_t)b * block_vec + chunk * kReadChunk + lane;
-    const int nj = min(kReadVec, (block_vec - chunk * kReadChunk) / kWave);
-    if (nj == kReadVec) {
+    const int left = block_vec - chunk * kReadChunk;  // vectors of this chunk
+    if (left >= kReadChunk) {
       u32x4 r[kReadVec];
 #pragma unroll
       for (int j = 0; j < kReadVec; ++j) r[j] = __builtin_nontemporal_load(from + j * kWave);
@@ -342,8 +340,9 @@ __global__ void __launch_bounds__(kCopyThreads)
         const unsigned long long hi = (unsigned long long)r[j][2] + r[j][3];
         acc += lo + hi;
       }
-    } else {
-      for (int j = 0; j < nj; ++j) {
+    } else {  // a block's last, partial chunk (or a block under 32 KiB)
+      for (int j = 0; j * kWave < left; ++j) {
+        if (j * kWave + lane >= left) break;
         const u32x4 x = __builtin_nontemporal_load(from + j * kWave);
         acc += (unsigned long long)x[0] + x[1] + x[2] + x[3];
       }

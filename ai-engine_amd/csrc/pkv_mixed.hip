@@ -52,9 +52,9 @@ __global__ void __launch_bounds__(kPT)
   const int gi = blockIdx.x / kXcd;
   const int x = blockIdx.x % kXcd;
   if (gi >= pgroups)
-    decode_body<DT, HD, R, false>(da, (gi - pgroups) * kXcd + x, sm.dec);
+    decode_body<DT, HD, R, false, false>(da, (gi - pgroups) * kXcd + x, sm.dec);
   else
-    prefill_body<DT, HD, R, FUSED>(pa, gi * kXcd + x, sm.pre);
+    prefill_body<DT, HD, R, FUSED, false>(pa, gi * kXcd + x, sm.pre);
 }
 
 template <int DT, int HD, int R, bool FUSED>
@@ -100,7 +100,8 @@ hipError_t mixed_hd(int HD, int R, const PrefillKArgs& pk, const DecodeKArgs& dk
 }  // namespace
 
 bool mixed_supported(const pkv_pool* p, int n_head, bool rope) {
-  if (rope || n_head <= 0 || n_head % p->n_kv_head) return false;
+  // block_size >= 16: the decode body here is the one with uniform block ids
+  if (rope || n_head <= 0 || n_head % p->n_kv_head || p->block_size < 16) return false;
   return mixed_built(p->dtype, p->head_dim, n_head / p->n_kv_head);
 }
 

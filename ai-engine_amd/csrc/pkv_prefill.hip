@@ -43,10 +43,10 @@
 namespace pkv {
 namespace {
 
-template <int DT, int HD, int RT, bool FUSED>
+template <int DT, int HD, int RT, bool FUSED, bool SB>
 __global__ void __launch_bounds__(kPT) prefill_kernel(PrefillKArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[2 * PCfg<DT, HD, RT>::STAGE];
-  prefill_body<DT, HD, RT, FUSED>(a, blockIdx.x, lds);
+  prefill_body<DT, HD, RT, FUSED, SB>(a, blockIdx.x, lds);
 }
 
 // Merge of a split row block (sequence s, kv head g, row block rb): per row,
@@ -113,14 +113,29 @@ hipError_t plaunch(PrefillKArgs k, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   if (!grid_fits(grid, kPT)) return hipErrorInvalidValue;
   if (k.k_new)
-    prefill_kernel<DT, HD, RT, true><<<(unsigned)grid, kPT, 0, s>>>(k);
+    prefill_kernel<DT, HD, RT, true, false><<<(unsigned)grid, kPT, 0, s>>>(k);
   else
-    prefill_kernel<DT, HD, RT, false><<<(unsigned)grid, kPT, 0, s>>>(k);
+    prefill_kernel<DT, HD, RT, false, false><<<(unsigned)grid, kPT, 0, s>>>(k);
+  return hipGetLastError();
+}
+
+// Block sizes below a wave-load's key span: the kernels with per-lane block
+// ids, built once per dtype and head_dim with the GQA ratio at run time.
+template <int DT, int HD>
+hipError_t plaunch_sb(PrefillKArgs k, hipStream_t s) {
+  const long long grid = prefill_grid<DT, HD, 0>(k);
+  if (grid <= 0) return hipSuccess;
+  if (!grid_fits(grid, kPT)) return hipErrorInvalidValue;
+  if (k.k_new)
+    prefill_kernel<DT, HD, 0, true, true><<<(unsigned)grid, kPT, 0, s>>>(k);
+  else
+    prefill_kernel<DT, HD, 0, false, true><<<(unsigned)grid, kPT, 0, s>>>(k);
   return hipGetLastError();
 }
 
 template <int DT, int HD>
 hipError_t plaunch_r(int R, const PrefillKArgs& k, hipStream_t s) {
+  if ((1 << k.bs_log2) < prefill_wave_keys<DT, HD>()) return plaunch_sb<DT, HD>(k, s);
   switch (R) {
     case 1: return plaunch<DT, HD, 1>(k, s);
     case 2: return plaunch<DT, HD, 2>(k, s);

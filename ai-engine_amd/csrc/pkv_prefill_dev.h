@@ -173,9 +173,21 @@ __device__ __forceinline__ uint32_t cvt_pk16(float x0, float x1) {
   }
 }
 
+// Keys one wave's share of a tile load spans (K chunks; f32 pools load V in
+// key pairs, twice as many).  Block sizes at least this large give every
+// wave-load one block id.
+template <int DT, int HD>
+constexpr int prefill_wave_keys() {
+  return (DT == PKV_F32 ? 2 : 1) * kWave / PCfg<DT, HD, 1>::CH;
+}
+
 // RT: the GQA ratio the kernel is built for, or 0 for any ratio (a.rq); the
 // ratio only enters the row <-> (token, head) index arithmetic.
-template <int DT, int HD, int RT, bool FUSED>
+// SB (block_size below prefill_wave_keys): a wave-load's keys span several
+// blocks, so each lane reads its own key's block id from the table where it
+// loads the key (a vector load in the tile's load phase) instead of taking
+// the wave-uniform id prefetched by scalar loads.
+template <int DT, int HD, int RT, bool FUSED, bool SB = false>
 __device__ __forceinline__ void prefill_body(const PrefillKArgs& a, int bid,
                                              char (&lds)[2 * PCfg<DT, HD, RT>::STAGE]) {
   using C = PCfg<DT, HD, RT>;
@@ -337,9 +349,10 @@ __device__ __forceinline__ void prefill_body(const PrefillKArgs& a, int bid,
   // ---- cooperative tile loads.  K chunk i of a thread: key
   //      (tid + kPT i) / CH, bytes 16 (tid % CH); V pair chunk v: keys
   //      2 ((tid + kPT v) / CH) and +1 (kPT = threads per workgroup).  CH divides 64, so one wave's share
-  //      of a load covers at most 16 aligned keys -- one block (block_size
-  //      >= 16): its block id is wave-uniform (a scalar load) and a lane
-  //      adds a 32-bit offset.  Keys past n_keys are clamped to n_keys - 1.
+  //      of a load covers at most 16 aligned keys -- one block when
+  //      block_size >= prefill_wave_keys: its block id is wave-uniform (a
+  //      scalar load) and a lane adds a 32-bit offset (smaller blocks: SB,
+  //      an id per lane).  Keys past n_keys are clamped to n_keys - 1.
   //      Block ids are checked where they are used; a bad one reads block 0
   //      and is reported once at the end. ----
   const int wkey = (wave * kWave) / C::CH;  // wave's first key within a load
@@ -358,12 +371,17 @@ __device__ __forceinline__ void prefill_body(const PrefillKArgs& a, int bid,
   };
   int kb[2][C::NKL], vb[2][C::NVP];  // raw block ids, two sets by tile parity
   auto ids = [&](int t, int (&kbs)[C::NKL], int (&vbs)[C::NVP]) __attribute__((always_inline)) {
+    if constexpr (SB) return;  // per-lane ids are read in the load phase
 #pragma unroll
     for (int i = 0; i < C::NKL; ++i) kbs[i] = table_at(t * C::KT + wkey + kPT * i / C::CH);
     if constexpr (DT == PKV_F32) {  // 16-bit pools load V with K's keys and block ids
 #pragma unroll
       for (int v = 0; v < C::NVP; ++v) vbs[v] = table_at(t * C::KT + 2 * (wkey + kPT * v / C::CH));
     }
+  };
+  // SB: the block of this lane's key (clamped like the keys themselves)
+  auto lane_block = [&](int key) __attribute__((always_inline)) {
+    return table[min(key, n_keys - 1) >> a.bs_log2];
   };
   u32x4 kreg[C::NSET][C::NKL], vreg[C::NSET][C::NVP][2];
   // A tile's K/V rows: from the pool, or (fused store) from the prompt's
@@ -383,21 +401,24 @@ __device__ __forceinline__ void prefill_body(const PrefillKArgs& a, int bid,
 #pragma unroll
     for (int i = 0; i < C::NKL; ++i) {
       const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
-      kr[i] = ld16(src(kh + (size_t)checked(kbs[i]) * blk_stride, kin, key));
+      const int blk = SB ? lane_block(key) : kbs[i];
+      kr[i] = ld16(src(kh + (size_t)checked(blk) * blk_stride, kin, key));
     }
     if constexpr (DT == PKV_F32) {
 #pragma unroll
       for (int v = 0; v < C::NVP; ++v) {
         const int k0 = t * C::KT + 2 * (wkey + kPT * v / C::CH + lkey);
-        const char* base = vh + (size_t)checked(vbs[v]) * blk_stride;
-        vr[v][0] = ld16(src(base, vin, min(k0, n_keys - 1)));
-        vr[v][1] = ld16(src(base, vin, min(k0 + 1, n_keys - 1)));
+        const int b0 = SB ? lane_block(k0) : vbs[v];
+        const int b1 = SB ? lane_block(k0 + 1) : vbs[v];
+        vr[v][0] = ld16(src(vh + (size_t)checked(b0) * blk_stride, vin, min(k0, n_keys - 1)));
+        vr[v][1] = ld16(src(vh + (size_t)checked(b1) * blk_stride, vin, min(k0 + 1, n_keys - 1)));
       }
     } else {  // V chunk 2 v + h: the same key and bytes as K chunk 2 v + h
 #pragma unroll
       for (int i = 0; i < C::NKL; ++i) {
         const int key = min(t * C::KT + wkey + kPT * i / C::CH + lkey, n_keys - 1);
-        vr[i >> 1][i & 1] = ld16(src(vh + (size_t)checked(kbs[i]) * blk_stride, vin, key));
+        const int blk = SB ? lane_block(key) : kbs[i];
+        vr[i >> 1][i & 1] = ld16(src(vh + (size_t)checked(blk) * blk_stride, vin, key));
       }
     }
   };

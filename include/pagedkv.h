@@ -79,9 +79,12 @@ const char* pkv_last_error(const pkv_pool* pool);
  *    (`attention.key_length`, else embedding_length / head_count,
  *    arch.rs:77-83); every llama / qwen2 / qwen3 model of the supported
  *    architectures (arch.rs:27-36) has 64 or 128.
- *  - block_size a power of two in [16, 256].  The reference takes any
+ *  - block_size a power of two in [1, 256].  The reference takes any
  *    usize (block_table.rs:17-30); its engine default and the block size of
- *    its tests is 16 (app.rs:701, tests/paged_parity.rs:33).
+ *    its tests is 16 (app.rs:701, tests/paged_parity.rs:33).  Sizes below
+ *    16 run kernels that read a block id per lane (a 16-token attention
+ *    tile then spans several blocks); other sizes (24, 48, ...) are
+ *    refused: every kernel addresses a token's slot with shifts and masks.
  * n_kv_head is any count in 1 .. 1024, and the slab (2 * n_layers *
  * num_blocks * block_size * n_kv_head * head_dim elements) below 2^63
  * bytes (else PKV_ERR_UNSUPPORTED); the GQA ratio n_head / n_kv_head of the

@@ -213,6 +213,27 @@ def test_decode_block_sizes(gpu, bs):
     c.close()
 
 
+@pytest.mark.parametrize("bs", [1, 2, 4, 8])
+@pytest.mark.parametrize("dt,H,KVH,hd", [(wl.BF16, 32, 8, 128), (wl.F16, 32, 4, 64),
+                                         (wl.F32, 4, 2, 64), (wl.BF16, 2, 2, 256),
+                                         (wl.F16, 14, 2, 64)])
+def test_decode_small_block_sizes(gpu, bs, dt, H, KVH, hd):
+    # block_size below 16 (the reference's config takes any size): a K
+    # sub-tile of 16 tokens spans 16 / bs blocks and each lane reads its
+    # token's block id.  Contexts around block and partition edges (the
+    # planner's partitions are at most 64 blocks: 64 * bs tokens), with the
+    # fused append bit-exact into the pool
+    ctx = [0, 1, bs - 1, bs, bs + 1, 15, 16, 17, 64 * bs - 1, 64 * bs, 64 * bs + 3, 700, 1500]
+    c = Case(gpu, dt, H, KVH, hd, bs, ctx, seed=100 * bs + hd + H, fused=True)
+    got = c.run()
+    ref, kp, vp = c.reference()
+    _close(got, ref, f"bs={bs} dt={dt} H={H}/{KVH} hd={hd}")
+    k1, v1 = _host_pool(c.cache, 0)
+    assert np.array_equal(k1.view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(v1.view(np.uint8), vp.view(np.uint8))
+    c.close()
+
+
 @pytest.mark.parametrize("dt", [wl.BF16, wl.F16, wl.F32])
 def test_fused_append_writes_pool_and_attends(gpu, dt):
     c = Case(gpu, dt, 16, 4, 128, 16, [0, 5, 15, 16, 31, 255, 256, 300, 1023, 2047], seed=77 + dt,

@@ -104,6 +104,23 @@ def test_prefill_block_sizes(gpu, bs):
     c.close()
 
 
+@pytest.mark.parametrize("bs", [1, 2, 4, 8])
+@pytest.mark.parametrize("dt,hd,R", [(wl.BF16, 128, 4), (wl.F16, 64, 8), (wl.F32, 64, 2),
+                                     (wl.F32, 256, 1), (wl.BF16, 64, 7)])
+def test_prefill_small_block_sizes(gpu, bs, dt, hd, R):
+    # block_size below 16: where it is below the keys one wave's share of a
+    # tile load spans (64 / (row bytes / 16), twice that for f32 V), each
+    # lane reads its key's block id; at or above it, the uniform-id kernel
+    # runs.  Priors and chunks starting and ending mid-block, a prior long
+    # enough for the split into parts
+    KVH = 2
+    priors = [0, bs - 1, 37, 300, 2100]
+    chunks = [bs + 3, 1, 45, 70, 16]
+    c = PCase(gpu, dt, R * KVH, KVH, hd, bs, priors, chunks, seed=bs + hd + R)
+    _close(c.run(), c.reference(), f"bs={bs} dt={dt} hd={hd} R={R}")
+    c.close()
+
+
 def test_prefill_out_dtype_pool(gpu):
     c = PCase(gpu, wl.F16, 32, 4, 64, 16, [10, 100], [40, 90], seed=3)
     _close(c.run(out_dtype=torch.float16), c.reference(), "f16 out")
@@ -229,7 +246,9 @@ def _slots(case):
                                         (wl.BF16, 64, 1, 32), (wl.F32, 128, 2, 16),
                                         (wl.BF16, 256, 2, 64), (wl.F16, 128, 8, 128),
                                         (wl.BF16, 64, 7, 16), (wl.F16, 128, 3, 32),
-                                        (wl.F32, 256, 6, 16), (wl.BF16, 128, 20, 16)])
+                                        (wl.F32, 256, 6, 16), (wl.BF16, 128, 20, 16),
+                                        (wl.F16, 64, 8, 4), (wl.BF16, 128, 4, 1),
+                                        (wl.F32, 64, 2, 8), (wl.BF16, 64, 3, 2)])
 def test_fused_store_equals_append_then_prefill(gpu, dt, hd, R, bs):
     # same attention output and same pool bytes, bit for bit, as pkv_append
     # followed by pkv_prefill_attention; chunks that start and end mid-block,

@@ -66,10 +66,11 @@ def test_rope_apply_in_place_and_bad_position(gpu):
 
 
 class RopeCase:
-    def __init__(self, gpu, dt, in_dt, H, KVH, hd, ctx, seed, positions=None, max_seq=9000):
+    def __init__(self, gpu, dt, in_dt, H, KVH, hd, ctx, seed, positions=None, max_seq=9000,
+                 bs=16):
         self.gpu, self.dt, self.in_dt, self.H, self.KVH, self.hd = gpu, dt, in_dt, H, KVH, hd
         self.ctx = np.asarray(ctx, np.int64)
-        B, bs = len(ctx), 16
+        B = len(ctx)
         need = -(-(self.ctx + 1) // bs)
         nb = int(need.sum()) + 7
         perm = wl.permutation(seed, nb)
@@ -138,8 +139,19 @@ def test_decode_attention_rope_split_last_partition(gpu):
     _rope_decode_check(gpu, wl.BF16, wl.F32, 128, 4, 2, ctx, 33)
 
 
-def _rope_decode_check(gpu, dt, in_dt, hd, R, KVH, ctx, seed):
-    case = RopeCase(gpu, dt, in_dt, R * KVH, KVH, hd, ctx, seed=seed)
+@pytest.mark.parametrize("bs", [1, 2, 4, 8])
+@pytest.mark.parametrize("dt,in_dt,hd,R", [(wl.BF16, wl.F32, 128, 4), (wl.F16, wl.F16, 64, 8),
+                                           (wl.F32, wl.F32, 64, 2)])
+def test_decode_attention_rope_small_block_sizes(gpu, dt, in_dt, hd, R, bs):
+    # blocks of fewer than 16 tokens: each lane of a 16-token sub-tile looks
+    # up its own block id, and the appended rotated row lands in block
+    # ctx // bs at slot ctx % bs
+    _rope_decode_check(gpu, dt, in_dt, hd, R, 2, [0, 1, bs - 1, bs, 15, 16, 300, 64 * bs + 3],
+                       hd + R + bs, bs=bs)
+
+
+def _rope_decode_check(gpu, dt, in_dt, hd, R, KVH, ctx, seed, bs=16):
+    case = RopeCase(gpu, dt, in_dt, R * KVH, KVH, hd, ctx, seed=seed, bs=bs)
     rope = pagedkv.Rope(hd, 500000.0, case.max_seq)
     cache, got = case.run_fused(rope)
     q, k, v = case.rotated()
