@@ -1041,9 +1041,10 @@ int pkv_sample(const void* logits, int dtype, long long row_stride, int batch, i
   return PKV_OK;
 }
 
-int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch, int vocab,
-                     const float* temperatures, int top_k, float top_p, uint64_t seed,
-                     int32_t* tokens, void* stream) {
+namespace {
+int sample_exact_impl(const void* logits, int dtype, long long row_stride, int batch, int vocab,
+                      const float* temperatures, int top_k, float top_p, uint64_t seed,
+                      int32_t* tokens, int32_t* routes, void* stream) {
   if (batch < 0 || vocab < 0 || vocab >= (1 << 24))
     return fail(nullptr, PKV_ERR_INVALID, "sample_exact: batch %d, vocab %d (0 .. 2^24 - 1)",
                 batch, vocab);
@@ -1057,16 +1058,34 @@ int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int ba
                 vocab);
   if (reinterpret_cast<uintptr_t>(logits) % pkv::dtype_bytes(dtype))
     return fail(nullptr, PKV_ERR_INVALID, "sample_exact: logits not aligned to the element size");
-  if ((reinterpret_cast<uintptr_t>(temperatures) | reinterpret_cast<uintptr_t>(tokens)) % 4)
+  if ((reinterpret_cast<uintptr_t>(temperatures) | reinterpret_cast<uintptr_t>(tokens) |
+       reinterpret_cast<uintptr_t>(routes)) % 4)
     return fail(nullptr, PKV_ERR_INVALID,
-                "sample_exact: temperatures and tokens must be 4-byte aligned");
+                "sample_exact: temperatures, tokens and routes must be 4-byte aligned");
   if (top_k < 0)
     return fail(nullptr, PKV_ERR_INVALID, "sample_exact: top_k %d < 0 (0 is None)", top_k);
   hipError_t e = pkv::launch_sample_exact(logits, dtype, row_stride, batch, vocab, temperatures,
-                                          top_k, top_p, pkv::sample_draw(seed), tokens,
+                                          top_k, top_p, pkv::sample_draw(seed), tokens, routes,
                                           static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(nullptr, e, "sample_exact launch");
   return PKV_OK;
+}
+}  // namespace
+
+int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch, int vocab,
+                     const float* temperatures, int top_k, float top_p, uint64_t seed,
+                     int32_t* tokens, void* stream) {
+  return sample_exact_impl(logits, dtype, row_stride, batch, vocab, temperatures, top_k, top_p,
+                           seed, tokens, nullptr, stream);
+}
+
+int pkv_sample_exact_routes(const void* logits, int dtype, long long row_stride, int batch,
+                            int vocab, const float* temperatures, int top_k, float top_p,
+                            uint64_t seed, int32_t* tokens, int32_t* routes, void* stream) {
+  if (batch > 0 && !routes)
+    return fail(nullptr, PKV_ERR_INVALID, "sample_exact_routes: NULL routes");
+  return sample_exact_impl(logits, dtype, row_stride, batch, vocab, temperatures, top_k, top_p,
+                           seed, tokens, routes, stream);
 }
 
 int pkv_sample_expf(const float* in, float* out, long long n, void* stream) {

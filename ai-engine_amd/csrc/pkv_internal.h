@@ -91,11 +91,12 @@ float sample_draw(uint64_t seed);
 hipError_t launch_sample(const void* logits, int dtype, long long row_stride, int batch,
                          int vocab, const float* temperatures, int top_k, float top_p,
                          float r, int32_t* tokens, hipStream_t stream);
-// The bit-exact variant (the reference's f32 arithmetic; top_p NaN = None),
-// and the exp it uses.
+// The bit-exact variant (the reference's f32 arithmetic; top_p NaN = None;
+// routes, when not null, gets per row the kernel that selected it), and the
+// exp it uses.
 hipError_t launch_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
                                int vocab, const float* temperatures, int top_k, float top_p,
-                               float r, int32_t* tokens, hipStream_t stream);
+                               float r, int32_t* tokens, int32_t* routes, hipStream_t stream);
 hipError_t launch_expf_glibc(const float* in, float* out, long long n, hipStream_t stream);
 
 // Launchers (defined in the .hip files).  They validate nothing that the

@@ -989,7 +989,9 @@ __constant__ unsigned long long kExp2Tab[32] = {
 // Apache-2.0 WITH LLVM-exception), the expf glibc has used since 2.28.  The reduction r = x N / ln2 - k is one fused multiply-add
 // (as GCC contracts it when glibc is built for FMA hardware); every other
 // operation is a separately rounded double operation, in glibc's order.
-__device__ __forceinline__ float expf_glibc(float x) {
+// The main path (x not NaN, -0x1.9fe368p6 <= x <= 0x1.62e42ep6), the table
+// at tab (kExp2Tab, or a copy in LDS).
+__device__ __forceinline__ float expf_glibc_main(float x, const unsigned long long* tab) {
 #pragma clang fp contract(off)
   constexpr double kN = 32.0;
   constexpr double kInvLn2N = 0x1.71547652b82fep0 * kN;
@@ -997,17 +999,13 @@ __device__ __forceinline__ float expf_glibc(float x) {
   constexpr double kC0 = 0x1.c6af84b912394p-5 / kN / kN / kN;
   constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / kN / kN;
   constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / kN;
-  if (x != x) return x + x;
-  if (x == -INFINITY) return 0.0f;
-  if (x > 0x1.62e42ep6f) return INFINITY;  // overflow (arguments here are <= 0)
-  if (x < -0x1.9fe368p6f) return 0.0f;     // below half the smallest subnormal
   const double xd = (double)x;
   const double z = kInvLn2N * xd;
   double kd = z + kShift;
   const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  const unsigned long long t = kExp2Tab[ki % 32] + (ki << 47);
+  const unsigned long long t = tab[ki % 32] + (ki << 47);
   const double s = __longlong_as_double((long long)t);
   const double zz = __builtin_fma(kC0, r, kC1);
   const double r2 = r * r;
@@ -1015,6 +1013,13 @@ __device__ __forceinline__ float expf_glibc(float x) {
   y = __builtin_fma(zz, r2, y);
   y = y * s;
   return (float)y;
+}
+__device__ __forceinline__ float expf_glibc(float x) {
+  if (x != x) return x + x;
+  if (x == -INFINITY) return 0.0f;
+  if (x > 0x1.62e42ep6f) return INFINITY;  // overflow (arguments here are <= 0)
+  if (x < -0x1.9fe368p6f) return 0.0f;     // below half the smallest subnormal
+  return expf_glibc_main(x, kExp2Tab);
 }
 
 constexpr int kXBits = 8;             // radix sort: bits per pass
@@ -1189,19 +1194,16 @@ __device__ __forceinline__ void split_at(float v, int e, int& a, int& rnd, bool&
   const int E = (int)((b >> 23) & 255u);
   const uint32_t mant = E ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
   const int k = (E ? E - 150 : -149) - e + 23;  // v / u = mant * 2^k
-  rnd = 0;
-  tie = false;
-  if (k >= 0) {
-    a = k >= 7 ? kDeltaCap : (int)min(mant << k, (uint32_t)kDeltaCap);
-  } else if (k < -25) {
-    a = 0;  // v < u / 4
-  } else {
-    const int sh = -k;
-    a = (int)(mant >> sh);
-    const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
-    rnd = rem > half;
-    tie = rem == half;
-  }
+  // k >= 0: a = mant 2^k (capped); k < 0: a = mant >> -k, the bits shifted
+  // out deciding the rounding.  Selects, no branches: a shift of 31 leaves
+  // a = 0 and a remainder below half for every 24-bit mant, as any k < -25
+  // (v < u / 4) must.
+  const int sh = min(max(-k, 1), 31);
+  const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  const uint32_t up = k >= 7 ? (uint32_t)kDeltaCap : min(mant << max(k, 0), (uint32_t)kDeltaCap);
+  a = (int)(k >= 0 ? up : mant >> sh);
+  rnd = k < 0 && rem > half;
+  tie = k < 0 && rem == half;
 }
 
 // (d0, d1) then (b0, b1): the deltas of two consecutive runs composed, for
@@ -1467,11 +1469,15 @@ struct ExactArgs {
   int32_t* tokens;
   uint32_t* scratch;  // 2 * vocab keys per row of the launch
   int row0;           // first row of this launch
-  // f32 logits: per row, 0 when sample_runs_kernel sampled it (every logit
-  // a bf16 value), 1 when it left the row to sample_exact_kernel; null: the
-  // exact kernel samples every row
+  // f32 logits: per row, 0 once a kernel has selected its token, 1 while it
+  // is left to the next kernel (buckets, then runs of equal values, then the
+  // sort); null: the exact kernel samples every row
   int32_t* fallback;
+  int32_t* route;  // optional, per row: the kernel that selected it (kRoute*)
 };
+
+// Which kernel selected a row's token (pkv_sample_exact_routes).
+constexpr int32_t kRouteArgmax = 0, kRouteBuckets = 1, kRouteRuns = 2, kRouteSort = 3;
 
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
@@ -1479,7 +1485,7 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   __shared__ ExactSmem xs;
   const int row = a.row0 + blockIdx.x;
   const int tid = threadIdx.x;
-  if (a.fallback && a.fallback[row] == 0) return;  // sampled by sample_runs_kernel
+  if (a.fallback && a.fallback[row] == 0) return;  // selected by an earlier kernel
   const char* x = a.logits + (long long)row * a.stride_bytes;
   const int V = a.vocab;
   const float T = a.temps ? a.temps[row] : 0.0f;
@@ -1487,7 +1493,10 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
     float bv;
     int bi;
     block_argmax<DT, VEC>(sm, x, 0, V, bv, bi);
-    if (tid == 0) a.tokens[row] = bi == INT_MAX ? 0 : bi;
+    if (tid == 0) {
+      a.tokens[row] = bi == INT_MAX ? 0 : bi;
+      if (a.route) a.route[row] = kRouteArgmax;
+    }
     return;
   }
   uint32_t* ka = a.scratch + (size_t)blockIdx.x * 2 * (size_t)V;
@@ -1554,7 +1563,10 @@ __global__ void __launch_bounds__(kST) sample_exact_kernel(ExactArgs a) {
   }
   Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
   const int tok = nth_tied<false>(sm, rw, kj, (unsigned long long)(j - lo + 1));
-  if (tid == 0) a.tokens[row] = tok;
+  if (tid == 0) {
+    a.tokens[row] = tok;
+    if (a.route) a.route[row] = kRouteSort;
+  }
 }
 
 // ---- 16-bit logits: the sorted sequence as runs of equal values -------------
@@ -1855,6 +1867,7 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
   RunSmem& rs = u.x.rs;
   const int row = a.row0 + blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
+  if (a.fallback && a.fallback[row] == 0) return;  // selected by sample_bucket_kernel
   const char* x = a.logits + (long long)row * a.stride_bytes;
   const int V = a.vocab;
   const float T = a.temps ? a.temps[row] : 0.0f;
@@ -1865,6 +1878,7 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
     if (tid == 0) {
       a.tokens[row] = bi == INT_MAX ? 0 : bi;
       if (a.fallback) a.fallback[row] = 0;
+      if (a.route) a.route[row] = kRouteArgmax;
     }
     return;
   }
@@ -2037,7 +2051,925 @@ __global__ void __launch_bounds__(kST) sample_runs_kernel(ExactArgs a) {
   while (rf > 0 && order_key(y_of(rf - 1)) == kj) --rf;
   Row<DT, VEC> rw{x, V, T, 0.0f, false, 0u, V};
   const int tok = nth_tied<false>(sm, rw, kj, (unsigned long long)(j - (int)ra.start[rf] + 1));
-  if (tid == 0) a.tokens[row] = tok;
+  if (tid == 0) {
+    a.tokens[row] = tok;
+    if (a.route) a.route[row] = kRouteRuns;
+  }
+}
+
+// ---- f32 logits: buckets of y instead of a sort -----------------------------
+// Only the f32 running sums depend on the sorted order, and only in part.
+// While a running sum stays inside one binade, each addition adds an integer
+// number of units that depends on the added value alone (split_at), except
+// at an exact tie, where round-half-even depends on the count so far; so a
+// stretch of the sorted sequence that the sum crosses without leaving its
+// binade, without a tie and without reaching a threshold adds the same total
+// in any order.
+//
+// sample_bucket_kernel cuts y into kBk buckets by its distance below max y (a
+// monotone function of y: each bucket is a contiguous stretch of the sorted
+// sequence, and equal y share a bucket) and counts each bucket's logits and
+// approximate mass (integers).  The mass prefix predicts the binade in which
+// each running sum (the softmax denominator; top_p's; r's) enters each bucket.
+// The keys of the buckets a sum must follow in order are stored and sorted:
+// the top of the order (its first kRegionA logits, where large probabilities
+// make ties common, kept in LDS with their values), the buckets where top_p
+// or r is predicted to be reached (with a margin), and a top_k cut.  Every
+// other bucket is only summed: its unit increments for the binade predicted
+// for it.  A walk then follows each sum: stored stretches 64 sorted logits at
+// a time (a composition scan of the two-parity deltas across the lanes, real
+// f32 additions where the sum leaves its binade), other buckets as prefix
+// sums of their increments -- checked against the actual sum.  Where the
+// actual binade differs from the prediction, one more pass over the row sums
+// the following buckets predicted alike again for the actual binade; where a
+// bucket holds a tie, or the sum would leave its binade or reach its
+// threshold inside it, one more pass stores its keys (and those of the next
+// buckets), which are sorted and walked.
+//
+// Logits kDTail or more below max y have p = expf(y - max y) < 0.84 2^-25.
+// Every sum such a p (or p / S, p / S / S2) meets is at least 1 (the
+// softmax denominator starts with exp(0) = 1), resp. at least the first
+// normalised probability, more than 2^25 times the added value: the addition
+// is below half a unit, changes nothing and is never a tie.  These logits
+// (most of a typical row) are counted but never stored, sorted or summed.
+//
+// A row is left to the later kernels (fallback stays 1) when it holds a NaN
+// or max y is infinite, when a bucket to sort holds more than kBkSortMax
+// logits, or when the running sum never reaches r (sample.rs then takes the
+// last kept token).
+constexpr int kBk = 4096;              // buckets of y per row (index kBk: the tail)
+constexpr int kWaveSortMax = 256;      // largest bucket one wave sorts
+constexpr int kBkSortMax = kSW * kWaveSortMax;  // largest bucket the workgroup sorts
+constexpr int kRegionA = 4096;         // the top logits, always stored (in LDS)
+constexpr int kGatherSpan = 64;        // buckets one extra pass gathers
+constexpr float kDTail = 17.5f;        // y - max y <= -kDTail: the tail
+constexpr float kMargin = 0x1p-6f;     // relative margin of the predictions
+constexpr short kNoBinade = SHRT_MIN;  // no prediction
+constexpr unsigned char kStored = 1, kSorted = 2, kGather = 4;
+static_assert(kBk == 4 * kST, "four buckets per thread in the scans");
+
+struct BucketSmem {
+  unsigned int start[kBk + 2];    // first sorted position of bucket b; [kBk]: the tail's; [kBk+1]: V
+  unsigned int cur[kBk + 1];      // logits per bucket, then store cursors
+  float pm[kBk + 1];              // approximate mass before bucket b ([kBk]: the total)
+  unsigned long long inc[kBk];    // fixed-point mass; then unit increments (bit 63: walk it)
+  short eg[kBk];                  // predicted binade of the running sum entering the bucket
+  unsigned char flag[kBk];        // kStored, kSorted, kGather
+  uint32_t stage[kSW][kWaveSortMax];  // keys being sorted: per wave, or all for one big bucket
+  uint32_t topk[kRegionA];        // the keys of the top of the order, sorted,
+  uint32_t topi[kRegionA];        //   their logits' indices,
+  float topv[kRegionA];           //   and what they add to the current sum
+  float ch_sum[kRegionA / 64];    // chunks of 64 of the top: sums (estimates),
+  int ch_e[kRegionA / 64];        //   the binade predicted at their start,
+  int ch_d0[kRegionA / 64], ch_d1[kRegionA / 64];  // their deltas in it (even / odd start)
+  unsigned long long exptab[32];   // kExp2Tab
+  unsigned long long wu[kSW];
+  unsigned int wtmp[kSW];
+  float wf[kSW], wg[kSW];
+  int wi[kSW];
+  float s;                        // walk: the running sum,
+  int b, todo, why, pos, big;     //   next bucket, bucket to see to and why, position reached
+  int tok;                        // the token found
+};
+union BucketLds {
+  SampleSmem sm;
+  BucketSmem bs;
+};
+
+// What a logit adds to a running sum: p = expf(y - max y) (divs 0), p / S
+// (1) or (p / S) / S2 (2), each division rounded as the reference's, from
+// t = y - max y or from the stored key of x' (y = x' / |T|).
+struct BucketValue {
+  float aT, ymax, S, S2;
+  int divs;
+  const unsigned long long* tab;  // kExp2Tab's copy in LDS
+  // (t > -kDTail: expf's main path)
+  __device__ __forceinline__ float of_t(float t) const {
+    float v = expf_glibc_main(t, tab);
+    if (divs >= 1) v = v / S;
+    if (divs >= 2) v = v / S2;
+    return v;
+  }
+  __device__ __forceinline__ float operator()(uint32_t k) const {
+    return of_t(key_value(k) / aT - ymax);
+  }
+  // an estimate of of_t within 1e-5 (relative)
+  __device__ __forceinline__ float approx(float t) const {
+    return divs == 0 ? __expf(t) : __expf(t) / (divs == 1 ? S : S * S2);
+  }
+};
+
+// Binade of a positive normal float (kNoBinade otherwise).
+__device__ __forceinline__ short binade_of(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const int E = (int)(b >> 23);
+  return v > 0.0f && E >= 1 && E <= 254 ? (short)(E - 127) : kNoBinade;
+}
+
+// Adds v's unit increment in binade e to bucket b; a tie, or a step that
+// alone leaves the binade, marks the bucket to be walked (bit 63).
+__device__ __forceinline__ void add_inc(BucketSmem& bs, int b, float v, int e) {
+  int a, rnd;
+  bool tie;
+  split_at(v, e, a, rnd, tie);
+  if (tie || a >= kDeltaCap)
+    atomicOr(&bs.inc[b], 1ull << 63);
+  else if (a + rnd)
+    atomicAdd(&bs.inc[b], (unsigned long long)(a + rnd));
+}
+
+// Sorts keys[0, n) descending in place, with their indices idx[0, n),
+// n <= kWaveSortMax, by one wave: each key's rank among the n (equal keys
+// keep their order).
+__device__ __forceinline__ void wave_sort_desc(uint32_t* keys, uint32_t* idx, int n,
+                                               uint32_t* stg) {
+  const int lane = threadIdx.x & 63;
+  if (n <= 64) {
+    const uint32_t k = lane < n ? keys[lane] : 0u, x = lane < n ? idx[lane] : 0u;
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint32_t o = (uint32_t)readlane_i((int)k, j);
+      r += o > k || (o == k && j < lane);
+    }
+    if (lane < n) {
+      keys[r] = k;
+      idx[r] = x;
+    }
+    return;
+  }
+  uint32_t mk[kWaveSortMax / 64], mx[kWaveSortMax / 64];
+#pragma unroll
+  for (int q = 0; q < kWaveSortMax / 64; ++q) {
+    const int i = lane + 64 * q;
+    mk[q] = i < n ? keys[i] : 0u;
+    mx[q] = i < n ? idx[i] : 0u;
+    if (i < n) stg[i] = mk[q];
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int q = 0; q < kWaveSortMax / 64; ++q) {
+    const int i = lane + 64 * q;
+    if (i >= n) continue;
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint32_t o = stg[j];
+      r += o > mk[q] || (o == mk[q] && j < i);
+    }
+    keys[r] = mk[q];
+    idx[r] = mx[q];
+  }
+}
+
+// Calls f(valid, i, x) for every logit x = row[i] with the whole wave
+// converged (lanes past the end get valid = false): 16-byte vectors, U in
+// flight, when VEC, then the elements past the last vector.
+template <bool VEC, int U, class F>
+__device__ __forceinline__ void row_converged(const char* row, int V, F&& f) {
+  const int lane = threadIdx.x & 63, w0 = (threadIdx.x >> 6) * 64;
+  int done = 0;
+  if constexpr (VEC) {
+    const int nvec = V / 4;
+    for (int base = w0; base < nvec; base += U * kST) {
+      u32x4 wb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = base + u * kST + lane;
+        wb[u] = v < nvec ? ld16(row + (size_t)v * 16) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int v = base + u * kST + lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f(v < nvec, 4 * v + j, __uint_as_float(wb[u][j]));
+      }
+    }
+    done = nvec * 4;
+  }
+  for (int base = done + w0; base < V; base += kST) {
+    const int i = base + lane;
+    f(i < V, i, i < V ? reinterpret_cast<const float*>(row)[i] : 0.0f);
+  }
+}
+
+// Wave 0: the f32 running sum s over sorted positions [lo, hi) -- the top of
+// the order from bs.topv (positions below nA), the rest from the keys in K --
+// stopping at the first sum >= thr (use_thr; *pos gets its position).  Per
+// 64 positions: while s is a normal number, the two-parity deltas of the 64
+// additions in s's binade, composed across the lanes, give every prefix sum;
+// from the first one that leaves the binade or reaches thr, real f32
+// additions.
+__device__ __forceinline__ void walk_sorted(const BucketSmem& bs, const uint32_t* K, int nA, int lo, int hi,
+                            float& s, int& pos, bool use_thr, float thr, const BucketValue vf) {
+  const int lane = threadIdx.x & 63;
+  for (int i0 = lo; i0 < hi && pos < 0; i0 += 64) {
+    const int m = min(64, hi - i0), i = i0 + lane;
+    const float v = lane >= m ? 0.0f : i < nA ? bs.topv[i] : vf(K[i]);
+    const uint32_t sb = __float_as_uint(s);
+    const int sE = (int)((sb >> 23) & 255u);
+    int j0 = 0;
+    if (sE >= 1 && sE <= 254 && !(sb >> 31)) {
+      const int e = sE - 127;
+      int a, rnd;
+      bool tie;
+      split_at(v, e, a, rnd, tie);
+      int p0 = tie ? a + (a & 1) : min(a + rnd, kDeltaCap);
+      int p1 = tie ? a + ((a + 1) & 1) : min(a + rnd, kDeltaCap);
+      compose_scan(p0, p1);
+      const long long n = (long long)((sb & 0x7fffffu) | 0x800000u);
+      const long long nend = n + ((n & 1) ? p1 : p0);
+      const float send = nend < (1ll << 24) ? ldexpf((float)nend, e - 23) : INFINITY;
+      const unsigned long long bad =
+          __ballot(lane < m && (nend >= (1ll << 24) || (use_thr && send >= thr)));
+      if (!bad) {
+        s = readlane_f(send, m - 1);
+        continue;
+      }
+      j0 = __builtin_ctzll(bad);
+      if (j0 > 0) s = readlane_f(send, j0 - 1);
+    }
+    for (int j = j0; j < m; ++j) {
+      s = s + readlane_f(v, j);
+      if (use_thr && s >= thr) {
+        pos = i0 + j;
+        break;
+      }
+    }
+  }
+}
+
+// Wave 0: the sum over the top of the order, positions [0, hi) (values in
+// bs.topv; chunk c = positions [64 c, 64 c + 64), with its deltas for the
+// binade predicted at its start in bs.ch_*): runs of chunks whose prediction
+// holds are applied with a composition scan across the lanes, one chunk a
+// lane; any other chunk is walked as walk_sorted walks 64 positions.
+__device__ __forceinline__ void walk_top(const BucketSmem& bs, int hi, float& s, int& pos,
+                                         bool use_thr, float thr, const BucketValue vf) {
+  const int lane = threadIdx.x & 63;
+  const int nch = (hi + 63) / 64;  // <= 64
+  int c = 0;
+  while (c < nch && pos < 0) {
+    const uint32_t sb = __float_as_uint(s);
+    const int sE = (int)((sb >> 23) & 255u);
+    const bool sn = sE >= 1 && sE <= 254 && !(sb >> 31);  // wave-uniform
+    const int es = sE - 127;
+    const int g = c + lane;
+    const unsigned long long okm = __ballot(g < nch && sn && bs.ch_e[g] == es);
+    const int run = ~okm ? __builtin_ctzll(~okm) : 64;
+    int d0 = lane < run ? bs.ch_d0[g] : 0, d1 = lane < run ? bs.ch_d1[g] : 0;
+    compose_scan(d0, d1);
+    const long long n = (long long)((sb & 0x7fffffu) | 0x800000u);
+    const long long nend = n + ((n & 1) ? d1 : d0);
+    const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
+    const unsigned long long stm =
+        __ballot(sn && lane < run && (nend >= (1ll << 24) || (use_thr && send >= thr)));
+    const int upto = stm ? __builtin_ctzll(stm) : run;
+    if (sn && upto > 0) s = readlane_f(send, upto - 1);
+    c += upto;
+    if (c >= nch) break;
+    walk_sorted(bs, nullptr, hi, 64 * c, min(64 * c + 64, hi), s, pos, use_thr, thr, vf);
+    ++c;
+  }
+}
+
+// Why walk_scan stopped at bucket bs.todo (not stored): the sum is in another
+// binade than the one its increments were summed for; or the bucket holds a
+// tie, or the sum leaves its binade or reaches thr inside it.
+constexpr int kWhyRebin = 1, kWhyStore = 2;
+
+// Wave 0: continues the walk from bucket bs.b with sum bs.s over buckets
+// [0, nbk) (`part` kept only below position len).  Stored buckets are walked
+// in sorted order; others are applied as prefix sums of their increments
+// while the sum stays in their binade and below thr.  Stops at the first
+// position where the sum reaches thr (bs.pos), at nbk, or at a bucket that
+// needs another pass over the row (bs.todo, bs.why).
+__device__ __forceinline__ void walk_scan(BucketSmem& bs, const uint32_t* K, int nA, int bA,
+                                          int nbk, int part, int len, bool use_thr, float thr,
+                                          const BucketValue vf) {
+  const int lane = threadIdx.x & 63;
+  float s = bs.s;
+  int b = bs.b, todo = -1, why = 0, pos = -1;
+  if (b == 0) {  // the top of the order, buckets [0, bA) (nbk <= bA when top_k cuts there)
+    walk_top(bs, min(nA, len), s, pos, use_thr, thr, vf);
+    b = min(bA, nbk);
+  }
+  while (b < nbk && pos < 0) {
+    if (bs.flag[b] & kStored) {  // the stretch of stored buckets from b
+      int e2 = b;
+      for (;;) {
+        const int g = e2 + lane;
+        const unsigned long long st = __ballot(g < nbk && (bs.flag[g] & kStored));
+        const int k = ~st ? __builtin_ctzll(~st) : 64;
+        e2 += k;
+        if (k < 64) break;
+      }
+      const int hi = e2 - 1 == part ? len : (int)bs.start[e2];
+      walk_sorted(bs, K, nA, (int)bs.start[b], hi, s, pos, use_thr, thr, vf);
+      b = e2;
+      continue;
+    }
+    const int g = b + lane;
+    const bool have = g < nbk;
+    const bool stored = have && (bs.flag[g] & kStored);
+    const int e = have ? bs.eg[g] : kNoBinade;
+    const unsigned c = have ? bs.start[g + 1] - bs.start[g] : 0u;
+    const unsigned long long iv = have ? bs.inc[g] : 0ull;
+    const unsigned d = (unsigned)min(iv, (unsigned long long)kDeltaCap);
+    const uint32_t sb = __float_as_uint(s);
+    const int sE = (int)((sb >> 23) & 255u);
+    const bool sn = sE >= 1 && sE <= 254 && !(sb >> 31);  // wave-uniform
+    const int es = sE - 127;
+    // lanes 0 .. run-1: empty buckets, or buckets summed for this binade
+    const unsigned long long okm =
+        __ballot(have && !stored && (c == 0u || (sn && (iv >> 63) == 0ull && e == es)));
+    const int run = ~okm ? __builtin_ctzll(~okm) : 64;
+    const long long n = (long long)((sb & 0x7fffffu) | 0x800000u);
+    // 64 (2^24 + 1) < 2^32
+    const long long nend = n + (long long)wave_incl_add_u32(lane < run && c ? d : 0u);
+    const float send = nend < (1ll << 24) ? ldexpf((float)nend, es - 23) : INFINITY;
+    const unsigned long long stm = __ballot(sn && lane < run && c != 0u &&
+                                            (nend >= (1ll << 24) || (use_thr && send >= thr)));
+    const int upto = stm ? __builtin_ctzll(stm) : run;
+    if (sn && upto > 0) s = readlane_f(send, upto - 1);
+    b += upto;
+    if (stm) {
+      todo = b;
+      why = kWhyStore;
+      break;
+    }
+    if (b >= nbk || run == 64 || readlane_i(stored, run)) continue;
+    todo = b;  // bucket b: summed for another binade, or a tie
+    why = sn && readlane_i(e, run) != es ? kWhyRebin : kWhyStore;
+    break;
+  }
+  if (lane == 0) {
+    bs.s = s;
+    bs.b = b;
+    bs.todo = todo;
+    bs.why = why;
+    bs.pos = pos;
+  }
+}
+
+template <bool VEC>
+struct BucketRow {
+  const char* x;
+  int V;
+  bool neg;
+  float aT, ymax, scale;
+  // bucket of y, from t = y - max y (smaller t: the same or a later bucket)
+  __device__ __forceinline__ int bucket(float t) const {
+    const float d = -t;
+    if (!(d < kDTail)) return kBk;
+    const float f = d * scale;
+    return f < (float)kBk ? (int)f : kBk - 1;
+  }
+  template <class F>
+  __device__ __forceinline__ void each(F&& f) const {  // f(x', t) for every logit
+    for_each<PKV_F32, VEC, 4>(x, V, [&](int, float v) {
+      const float xp = neg ? -v : v;
+      f(xp, xp / aT - ymax);
+    });
+  }
+};
+
+// Sorts every stored, unsorted bucket in [b0, nbk) (keys in K, indices in
+// KI): one wave per bucket, then the workgroup for those over kWaveSortMax.
+// Returns false when one holds more than kBkSortMax keys.  All threads; ends
+// with a barrier.
+__device__ __forceinline__ bool sort_stored(BucketSmem& bs, uint32_t* K, uint32_t* KI, int b0,
+                                            int nbk) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) bs.big = 0;
+  __syncthreads();
+  for (int b = b0 + wv; b < nbk; b += kSW) {
+    if ((bs.flag[b] & (kStored | kSorted)) != kStored) continue;  // wave-uniform
+    const int st = (int)bs.start[b], n = (int)bs.start[b + 1] - st;
+    if (n > kWaveSortMax) {
+      if (lane == 0) atomicAdd(&bs.big, 1);
+      continue;
+    }
+    wave_sort_desc(K + st, KI + st, n, bs.stage[wv]);
+    if (lane == 0) bs.flag[b] |= kSorted;
+  }
+  __syncthreads();
+  if (bs.big == 0) return true;
+  uint32_t* stg = &bs.stage[0][0];
+  for (int b = b0; b < nbk; ++b) {  // uniform
+    if ((bs.flag[b] & (kStored | kSorted)) != kStored) continue;
+    const int st = (int)bs.start[b], n = (int)bs.start[b + 1] - st;
+    if (n > kBkSortMax) return false;
+    uint32_t mx[kBkSortMax / kST];
+#pragma unroll
+    for (int q = 0; q < kBkSortMax / kST; ++q) {
+      const int i = tid + q * kST;
+      if (i < n) {
+        stg[i] = K[st + i];
+        mx[q] = KI[st + i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kBkSortMax / kST; ++q) {
+      const int i = tid + q * kST;
+      if (i >= n) continue;
+      const uint32_t k = stg[i];
+      int r = 0;
+      for (int j = 0; j < n; ++j) {
+        const uint32_t o = stg[j];
+        r += o > k || (o == k && j < i);
+      }
+      K[st + r] = k;
+      KI[st + r] = mx[q];
+    }
+    __syncthreads();
+    if (tid == 0) bs.flag[b] |= kSorted;
+  }
+  __syncthreads();
+  return true;
+}
+
+// The f32 running sum of vf over the kept sorted positions [0, len) --
+// buckets [0, nbk), `part` (if >= 0) kept only up to len -- up to and
+// including the first sum >= thr (use_thr).  Results: bs.s, and bs.pos the
+// position where thr was reached (-1: not reached).  Returns false when a
+// bucket to sort is too large (the row is left to the sort kernel).  All
+// threads; ends with a barrier.
+template <bool VEC>
+__device__ __forceinline__ bool bucket_walk(BucketSmem& bs, uint32_t* K, uint32_t* KI,
+                                            const BucketRow<VEC>& rw, int nA, int bA, int nbk,
+                                            int part, int len, bool use_thr, float thr,
+                                            const BucketValue vf) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // the top's values, and per chunk of 64 its deltas in the binade the sum
+  // is predicted to enter it with (float prefix sums of the chunks)
+  const int hiA = min(nA, len), nch = (hiA + 63) / 64;
+  for (int i = tid; i < hiA; i += kST) bs.topv[i] = vf(bs.topk[i]);
+  __syncthreads();
+  for (int c = wv; c < nch; c += kSW) {
+    const int i = 64 * c + lane;
+    const float t = wsum_f32(i < hiA ? bs.topv[i] : 0.0f);
+    if (lane == 0) bs.ch_sum[c] = t;
+  }
+  __syncthreads();
+  for (int c = wv; c < nch; c += kSW) {
+    float pre = 0.0f;
+    for (int q = 0; q < c; ++q) pre += bs.ch_sum[q];
+    const int e = use_thr && pre > thr * 1.0625f ? kNoBinade : binade_of(pre);
+    int d0 = 0, d1 = 0;
+    if (e != kNoBinade) {  // wave-uniform
+      const int i = 64 * c + lane;
+      int a, rnd;
+      bool tie;
+      split_at(i < hiA ? bs.topv[i] : 0.0f, e, a, rnd, tie);
+      d0 = tie ? a + (a & 1) : min(a + rnd, kDeltaCap);
+      d1 = tie ? a + ((a + 1) & 1) : min(a + rnd, kDeltaCap);
+      compose_scan(d0, d1);
+    }
+    if (lane == 63) {
+      bs.ch_e[c] = e;
+      bs.ch_d0[c] = d0;
+      bs.ch_d1[c] = d1;
+    }
+  }
+  if (tid == 0) {
+    bs.s = 0.0f;
+    bs.b = 0;
+  }
+  __syncthreads();
+  for (;;) {
+    if (wv == 0) walk_scan(bs, K, nA, bA, nbk, part, len, use_thr, thr, vf);
+    __syncthreads();
+    const int todo = bs.todo, why = bs.why;
+    if (todo < 0) break;  // (every thread reads bs.todo before it changes again)
+    if (why == kWhyRebin) {
+      // the buckets from todo on that were predicted like todo: the actual
+      // binade of the sum, their increments again
+      const int wrong = bs.eg[todo];
+      const uint32_t sb = __float_as_uint(bs.s);
+      const int es = (int)((sb >> 23) & 255u) - 127;
+      __syncthreads();
+      for (int b = todo + tid; b < nbk; b += kST) {
+        if (bs.eg[b] == wrong && !(bs.flag[b] & kStored)) {
+          bs.eg[b] = (short)es;
+          bs.inc[b] = 0ull;
+        }
+      }
+      __syncthreads();
+      rw.each([&](float, float t) {
+        const int b = rw.bucket(t);
+        if (b < todo || b >= nbk || bs.eg[b] != es || (bs.flag[b] & kStored)) return;
+        if (vf.approx(t) >= ldexpf(0.98f, es - 24)) add_inc(bs, b, vf.of_t(t), es);
+      });
+      __syncthreads();
+      continue;
+    }
+    // store the keys of todo and the next buckets not stored
+    for (int b = todo + tid; b < min(nbk, todo + kGatherSpan); b += kST)
+      if (!(bs.flag[b] & kStored)) bs.flag[b] = kGather;
+    __syncthreads();
+    row_converged<VEC, 4>(rw.x, rw.V, [&](bool valid, int i, float v) {
+      const float xp = rw.neg ? -v : v;
+      const int b = valid ? rw.bucket(xp / rw.aT - rw.ymax) : kBk;
+      if (b < kBk && (bs.flag[b] & kGather)) {
+        const unsigned p = bs.start[b] + atomicAdd(&bs.cur[b], 1u);
+        K[p] = order_key(xp);
+        KI[p] = (uint32_t)i;
+      }
+    });
+    __syncthreads();
+    for (int b = tid; b < kBk; b += kST)
+      if (bs.flag[b] & kGather) bs.flag[b] = kStored;
+    __syncthreads();
+    if (!sort_stored(bs, K, KI, todo, nbk)) return false;
+  }
+  __syncthreads();
+  return true;
+}
+
+template <bool VEC>
+__global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
+  __shared__ BucketLds u;
+  SampleSmem& sm = u.sm;
+  BucketSmem& bs = u.bs;
+  const int row = a.row0 + blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const char* x = a.logits + (long long)row * a.stride_bytes;
+  const int V = a.vocab;
+  const float T = a.temps ? a.temps[row] : 0.0f;
+  if (T == 0.0f || V <= 1) {  // sample.rs:13-15
+    float bv;
+    int bi;
+    block_argmax<PKV_F32, VEC>(sm, x, 0, V, bv, bi);
+    if (tid == 0) {
+      a.tokens[row] = bi == INT_MAX ? 0 : bi;
+      a.fallback[row] = 0;
+      if (a.route) a.route[row] = kRouteArgmax;
+    }
+    return;
+  }
+  auto leave = [&]() {
+    if (tid == 0) a.fallback[row] = 1;
+  };
+  const bool neg = T < 0.0f;
+  const float aT = fabsf(T);  // y = x / T = x' / |T| with x' = x, or -x when T < 0
+
+  // 1. the largest and smallest x', and whether a logit is NaN
+  if (tid < 32) bs.exptab[tid] = kExp2Tab[tid];
+  float hi = -INFINITY, lo = INFINITY;
+  bool nan = false;
+  for_each<PKV_F32, VEC, kRowBatch>(x, V, [&](int, float v) {
+    const float xp = neg ? -v : v;
+    hi = fmaxf(hi, xp);
+    lo = fminf(lo, xp);
+    nan |= v != v;
+  });
+  hi = wave_reduce32(hi, [](float p, float q) { return fmaxf(p, q); });
+  lo = wave_reduce32(lo, [](float p, float q) { return fminf(p, q); });
+  const bool wnan = __ballot(nan) != 0ull;
+  if (lane == 0) {
+    bs.wf[wv] = hi;
+    bs.wg[wv] = lo;
+    bs.wi[wv] = wnan;
+  }
+  __syncthreads();
+  bool anynan = false;
+  for (int w = 0; w < kSW; ++w) {
+    hi = fmaxf(hi, bs.wf[w]);
+    lo = fminf(lo, bs.wg[w]);
+    anynan |= bs.wi[w] != 0;
+  }
+  const float ymax = hi / aT, ymin = lo / aT;
+  if (anynan || !(fabsf(ymax) < INFINITY)) {  // uniform
+    leave();
+    return;
+  }
+  const float D = fminf(ymax - ymin, kDTail);
+  const BucketRow<VEC> rw{x, V, neg, aT, ymax,
+                          D > 0.0f ? fminf((float)kBk / D, 0x1p100f) : 0.0f};
+
+  // 2. logits and approximate mass (2^-40 units) per bucket; the tail only
+  // counted
+  for (int i = tid; i <= kBk; i += kST) bs.cur[i] = 0u;
+  for (int i = tid; i < kBk; i += kST) bs.inc[i] = 0ull;
+  __syncthreads();
+  rw.each([&](float, float t) {
+    const int b = rw.bucket(t);
+    const unsigned long long tl = __ballot(b == kBk);
+    if (tl && lane == __builtin_ctzll(__ballot(true)))
+      atomicAdd(&bs.cur[kBk], (unsigned)__popcll(tl));
+    if (b < kBk) {
+      atomicAdd(&bs.cur[b], 1u);
+      atomicAdd(&bs.inc[b], (unsigned long long)(__expf(t) * 0x1p40f));
+    }
+  });
+  __syncthreads();
+
+  // 3. exclusive prefixes: bucket starts (the tail last) and masses
+  {
+    const int b0 = 4 * tid;
+    unsigned c[4];
+    unsigned long long m[4];
+    unsigned cs = 0u;
+    unsigned long long ms = 0ull;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = bs.cur[b0 + j];
+      m[j] = bs.inc[b0 + j];
+      cs += c[j];
+      ms += m[j];
+    }
+    const unsigned tail = bs.cur[kBk];
+    unsigned total;
+    unsigned pre = block_excl_scan(cs, bs.wtmp, total);
+    const unsigned long long mincl = wave_incl_u64(ms);
+    if (lane == 63) bs.wu[wv] = mincl;
+    __syncthreads();
+    unsigned long long mpre = mincl - ms, mtot = 0ull;
+    for (int w = 0; w < kSW; ++w) {
+      if (w < wv) mpre += bs.wu[w];
+      mtot += bs.wu[w];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bs.start[b0 + j] = pre;
+      pre += c[j];
+      bs.pm[b0 + j] = (float)mpre * 0x1p-40f;
+      mpre += m[j];
+    }
+    if (tid == kST - 1) {
+      bs.start[kBk] = pre;
+      bs.start[kBk + 1] = pre + tail;
+      bs.pm[kBk] = (float)mtot * 0x1p-40f;
+    }
+  }
+  __syncthreads();
+
+  // top_k: positions [0, len) are kept; buckets [0, nbk) are in play and
+  // `part` is kept only in part (a cut inside the tail drops nothing that
+  // matters)
+  const int nreg = (int)bs.start[kBk];
+  int len = a.top_k > 0 && a.top_k < V ? a.top_k : V;
+  int nbk = kBk, part = -1;
+  auto cut_at = [&](int n) {
+    nbk = kBk;
+    part = -1;
+    if (n < nreg) {  // the bucket of position n - 1: the last with start < n
+      int l = 0, h = kBk - 1;
+      while (l < h) {
+        const int mid = (l + h + 1) >> 1;
+        if ((int)bs.start[mid] < n) l = mid;
+        else h = mid - 1;
+      }
+      nbk = l + 1;
+      part = (int)bs.start[l + 1] > n ? l : -1;
+    }
+  };
+  cut_at(len);
+  // the top of the order: buckets [0, bA), positions [0, nA), nA <= kRegionA
+  // (bucket 0 must fit)
+  int bA = 0;
+  {
+    int l = 0, h = nbk;
+    while (l < h) {
+      const int mid = (l + h + 1) >> 1;
+      if ((int)bs.start[mid] <= kRegionA) l = mid;
+      else h = mid - 1;
+    }
+    bA = l;
+  }
+  if (bA == 0) {  // uniform: bucket 0 alone holds more than kRegionA logits
+    leave();
+    return;
+  }
+  const int nA = (int)bs.start[bA];
+
+  // 4. which buckets to store: the top, the top_k cut, and (with a margin)
+  // each bucket where top_p's sum of p / S or r's of p / S (/ S2, about top_p
+  // when top_p < 1: the kept sum first reaches top_p) is predicted to reach
+  // its threshold; the others get the binade the denominator is predicted to
+  // have at their start
+  const float Sest = bs.pm[kBk];
+  const bool has_p = a.top_p == a.top_p;  // Some(top_p)
+  const float S3est = Sest * (has_p ? fminf(fmaxf(a.top_p, 0x1p-20f), 1.0f) : 1.0f);
+  auto reaches = [&](int b, float div, float thr) {
+    return bs.pm[b] * (1.0f - kMargin) / div <= thr * (1.0f + kMargin) &&
+           bs.pm[b + 1] * (1.0f + kMargin) / div >= thr * (1.0f - kMargin);
+  };
+  for (int b = tid; b < kBk; b += kST) {
+    const bool st = b < bA || b == part ||
+                    (b < nbk && bs.start[b + 1] > bs.start[b] &&
+                     (reaches(b, S3est, a.r) || (has_p && reaches(b, Sest, a.top_p))));
+    bs.flag[b] = b < bA ? kStored | kSorted : st ? kStored : 0;
+    bs.eg[b] = st ? kNoBinade : binade_of(bs.pm[b]);
+    bs.inc[b] = 0ull;
+    bs.cur[b] = 0u;
+  }
+  __syncthreads();
+
+  // 5. store the flagged buckets' keys (the top in LDS); the others'
+  // increments for the denominator (p below half a unit of the predicted
+  // binade adds nothing)
+  // (the increments go through a per-wave queue in LDS, so that the
+  // exponentials and splits run on full waves)
+  uint32_t* K = a.scratch + (size_t)blockIdx.x * 2 * (size_t)V;  // keys
+  uint32_t* KI = K + V;                                           // their indices
+  const BucketValue p_of{aT, ymax, 1.0f, 1.0f, 0, bs.exptab};
+  {
+    float* qt = reinterpret_cast<float*>(bs.stage[wv]);
+    int* qb = reinterpret_cast<int*>(bs.stage[wv]) + 128;
+    static_assert(kWaveSortMax >= 256, "a queue of 128 (t, bucket) pairs per wave");
+    int qn = 0;  // wave-uniform
+    auto drain = [&](int n) {
+      if (lane < n) {
+        const int b = qb[lane];
+        add_inc(bs, b, p_of.of_t(qt[lane]), bs.eg[b]);
+      }
+    };
+    row_converged<VEC, 4>(x, V, [&](bool valid, int i, float v) {
+      const float xp = neg ? -v : v;
+      const float t = xp / aT - ymax;
+      const int b = valid ? rw.bucket(t) : kBk;
+      const bool play = b < nbk;
+      const unsigned char fl = play ? bs.flag[b] : 0;
+      if (play && (fl & kStored)) {  // the top in LDS, other stored buckets in K
+        const unsigned p = bs.start[b] + atomicAdd(&bs.cur[b], 1u);
+        if (b < bA) {
+          bs.topk[p] = order_key(xp);
+          bs.topi[p] = (uint32_t)i;
+        } else {
+          K[p] = order_key(xp);
+          KI[p] = (uint32_t)i;
+        }
+      }
+      const int e = play && !(fl & kStored) ? bs.eg[b] : kNoBinade;
+      const bool push = e != kNoBinade && __expf(t) >= ldexpf(0.98f, e - 24);
+      const unsigned long long m = __ballot(push);
+      if (m) {  // wave-uniform
+        const int at = qn + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (push) {
+          qt[at] = t;
+          qb[at] = b;
+        }
+        qn += __popcll(m);
+        if (qn >= 64) {
+          drain(64);
+          if (lane < qn - 64) {
+            qt[lane] = qt[64 + lane];
+            qb[lane] = qb[64 + lane];
+          }
+          qn -= 64;
+        }
+      }
+    });
+    drain(qn);
+  }
+  __syncthreads();
+  // the top, sorted in LDS: each key's rank within its bucket
+  {
+    uint32_t* stg = &bs.stage[0][0];
+    static_assert(kRegionA <= kBkSortMax, "the top is staged in one piece");
+    uint32_t mk[kRegionA / kST], mx[kRegionA / kST];
+#pragma unroll
+    for (int q = 0; q < kRegionA / kST; ++q) {
+      const int i = tid + q * kST;
+      if (i < nA) {
+        mk[q] = bs.topk[i];
+        mx[q] = bs.topi[i];
+        stg[i] = mk[q];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kRegionA / kST; ++q) {
+      const int i = tid + q * kST;
+      if (i >= nA) continue;
+      int l = 0, h = bA - 1;  // the bucket of position i: the last with start <= i
+      while (l < h) {
+        const int mid = (l + h + 1) >> 1;
+        if ((int)bs.start[mid] <= i) l = mid;
+        else h = mid - 1;
+      }
+      const int st = (int)bs.start[l], en = (int)bs.start[l + 1];
+      int r = 0;
+      for (int j = st; j < en; ++j) {
+        const uint32_t o = stg[j];
+        r += o > mk[q] || (o == mk[q] && j < i);
+      }
+      bs.topk[st + r] = mk[q];
+      bs.topi[st + r] = mx[q];
+    }
+    __syncthreads();
+  }
+  if (!sort_stored(bs, K, KI, bA, nbk) ||
+      !bucket_walk(bs, K, KI, rw, nA, bA, nbk, part, len, false, 0.0f, p_of)) {
+    leave();  // sum += p
+    return;
+  }
+  const float S = bs.s;
+
+  // predictions (mass prefixes over div) and increments of vf for a
+  // threshold run, for the buckets not stored below the first one predicted
+  // past thr (the walk stops before it); one more pass over the row when any
+  // bucket needs them
+  auto prepare = [&](float div, float thr, const BucketValue& vf) {
+    int bc = nbk;
+    for (int b = tid; b < nbk; b += kST)
+      if (bs.pm[b] / div > thr * 1.0625f) {
+        bc = b;
+        break;
+      }
+    bc = wave_reduce32(bc, [](int p, int q) { return min(p, q); });
+    if (lane == 0) bs.wi[wv] = bc;
+    __syncthreads();
+    for (int w = 0; w < kSW; ++w) bc = min(bc, bs.wi[w]);
+    bool need = false;
+    for (int b = tid; b < kBk; b += kST) {
+      const bool pr = b < bc && !(bs.flag[b] & kStored) && bs.start[b + 1] > bs.start[b];
+      bs.eg[b] = pr ? binade_of(bs.pm[b] / div) : kNoBinade;
+      bs.inc[b] = 0ull;
+      need |= pr;
+    }
+    need = __ballot(need) != 0ull;
+    if (lane == 0) bs.wtmp[wv] = need;
+    __syncthreads();
+    bool any = false;
+    for (int w = 0; w < kSW; ++w) any |= bs.wtmp[w] != 0u;
+    if (any) {
+      rw.each([&](float, float t) {
+        const int b = rw.bucket(t);
+        if (b >= nbk) return;
+        const int e = bs.eg[b];
+        if (e != kNoBinade && vf.approx(t) >= ldexpf(0.98f, e - 24)) add_inc(bs, b, vf.of_t(t), e);
+      });
+    }
+    __syncthreads();
+  };
+
+  float S2 = 1.0f;
+  if (has_p) {  // cumulative q until it reaches top_p; keep that prefix
+    const BucketValue q_of{aT, ymax, S, 1.0f, 1, bs.exptab};
+    prepare(S, a.top_p, q_of);
+    if (!bucket_walk(bs, K, KI, rw, nA, bA, nbk, part, len, true, a.top_p, q_of)) {
+      leave();
+      return;
+    }
+    S2 = bs.s;  // the f32 sum of the kept q
+    if (bs.pos >= 0) {
+      len = bs.pos + 1;
+      cut_at(len);
+    }
+  }
+  const BucketValue r_of{aT, ymax, S, S2, has_p ? 2 : 1, bs.exptab};
+  prepare(has_p ? S * S2 : S, a.r, r_of);
+  if (!bucket_walk(bs, K, KI, rw, nA, bA, nbk, part, len, true, a.r, r_of) || bs.pos < 0) {
+    leave();  // (not reached: the reference takes the last kept token)
+    return;
+  }
+  // the token at sorted position j: the tokens of its y (all in its bucket,
+  // stored and sorted by key; equal keys in any order) are in index order in
+  // the reference's stable sort, so it is the (j - g0)-th smallest index of
+  // that group, g0 its first position
+  const int j = bs.pos;
+  auto key_at = [&](int i) { return i < nA ? bs.topk[i] : K[i]; };
+  auto idx_at = [&](int i) { return i < nA ? bs.topi[i] : KI[i]; };
+  const float yj = key_value(key_at(j)) / aT;
+  const uint32_t ky = order_key(yj);
+  const int bj = rw.bucket(yj - ymax);
+  const int st = (int)bs.start[bj], en = (int)bs.start[bj + 1];
+  int before = 0, all = 0;
+  for (int i = st + tid; i < en; i += kST) {
+    const bool same = order_key(key_value(key_at(i)) / aT) == ky;
+    before += same && i < j;
+    all += same;
+  }
+  before = wsum_i32(before);
+  all = wsum_i32(all);
+  if (lane == 0) {
+    bs.wi[wv] = before;
+    bs.wtmp[wv] = (unsigned)all;
+  }
+  if (tid == 0) bs.tok = 0;
+  __syncthreads();
+  int g0 = j, g1 = 0;
+  for (int w = 0; w < kSW; ++w) {
+    g0 -= bs.wi[w];
+    g1 += (int)bs.wtmp[w];
+  }
+  g1 += g0;
+  const int want = j - g0;  // the rank wanted among the group's indices
+  for (int i = g0 + tid; i < g1; i += kST) {
+    const uint32_t xi = idx_at(i);
+    int r = 0;
+    for (int q = g0; q < g1; ++q) r += idx_at(q) < xi;
+    if (r == want) bs.tok = (int)xi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    a.tokens[row] = bs.tok;
+    a.fallback[row] = 0;
+    if (a.route) a.route[row] = kRouteBuckets;
+  }
 }
 
 // The exp the exact path uses, for verification: out[i] = expf_glibc(in[i]).
@@ -2054,9 +2986,13 @@ constexpr size_t kExactScratch = 512ull << 20;
 template <int DT, bool VEC>
 void launch_exact_rows(const ExactArgs& a, int rows, hipStream_t stream) {
   if constexpr (DT == PKV_F32) {
-    // rows whose logits are all bf16 values run on runs of equal values;
-    // the sort kernel takes the others (a.fallback)
-    if (a.fallback) sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
+    // sampled rows go to the buckets first; the rows they leave (a.fallback)
+    // to the runs of equal values when every logit is a bf16 value, then to
+    // the sort
+    if (a.fallback) {
+      sample_bucket_kernel<VEC><<<rows, kST, 0, stream>>>(a);
+      sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
+    }
     sample_exact_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
   } else {
     sample_runs_kernel<DT, VEC><<<rows, kST, 0, stream>>>(a);
@@ -2150,10 +3086,10 @@ hipError_t launch_sample(const void* logits, int dtype, long long row_stride, in
 
 hipError_t launch_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
                                int vocab, const float* temperatures, int top_k, float top_p,
-                               float r, int32_t* tokens, hipStream_t stream) {
+                               float r, int32_t* tokens, int32_t* routes, hipStream_t stream) {
   const long long sb = row_stride * (long long)dtype_bytes(dtype);
   ExactArgs a{static_cast<const char*>(logits), sb, vocab, temperatures, top_k, top_p, r,
-              tokens, nullptr, 0, nullptr};
+              tokens, nullptr, 0, nullptr, routes};
   const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (batch == 1 || sb % 16 == 0);
   if (dtype == PKV_F32) return vec ? launch_exact_dt<PKV_F32, true>(a, batch, stream)
                                    : launch_exact_dt<PKV_F32, false>(a, batch, stream);

@@ -156,7 +156,7 @@ def sample_draw(seed: int = 42) -> float:
 
 
 def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | None = None,
-           seed: int = 42, out=None, stream=None, exact: bool = True):
+           seed: int = 42, out=None, stream=None, exact: bool = True, routes=None):
     """Token per logits row on the device: argmax / sample() of sample.rs:12-55.
     logits: (batch, vocab) f32/f16/bf16 with unit stride along vocab;
     temperatures: (batch,) float32 on the device (None: all greedy).
@@ -173,6 +173,9 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
     several workgroups; sums the probabilities exactly, so a row can differ
     where the reference's f32 running sum lands within its rounding of r or
     top_p (top_p=None is 1.0 there, the same as no cut in exact sums).
+    routes (exact=True only): a (batch,) int32 device tensor that receives
+    the kernel that selected each row (pkv_sample_exact_routes: 0 argmax,
+    1 buckets of f32 logits, 2 runs of equal 16-bit values, 3 radix sort).
     Returns (batch,) int32 on the device."""
     import torch
     if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
@@ -187,10 +190,17 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
     s = cur if stream is None else stream
     if s != cur:
         s.wait_stream(cur)
+    if routes is not None and not exact:
+        raise ValueError("routes are reported by the exact path only")
     if exact:  # top_p None is NaN; any other value is Some(top_p)
         fn, tp = lib().pkv_sample_exact, float("nan") if top_p is None else float(top_p)
     else:      # top_p None is 1.0 (no cut in exact arithmetic)
         fn, tp = lib().pkv_sample, 1.0 if top_p is None else float(top_p)
+    extra = ()
+    if routes is not None:
+        if routes.dtype != torch.int32 or routes.numel() != B or not routes.is_contiguous():
+            raise ValueError("routes must be a contiguous int32 tensor of one entry per row")
+        fn, extra = lib().pkv_sample_exact_routes, (_dev_ptr(routes),)
     with torch.cuda.stream(s):
         if out is None:
             out = torch.empty(B, dtype=torch.int32, device=dev)
@@ -202,7 +212,7 @@ def sample(logits, temperatures=None, top_k: int | None = None, top_p: float | N
         check(fn(_dev_ptr(logits) if V else None, pkv_dtype(logits.dtype),
                  logits.stride(0) if B > 1 else V, B, V,
                  _dev_ptr(t) if t is not None else None, top_k or 0, tp, seed, _dev_ptr(out),
-                 _stream_ptr(s)), None)
+                 *extra, _stream_ptr(s)), None)
     return out
 
 

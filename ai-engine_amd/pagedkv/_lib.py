@@ -108,6 +108,8 @@ SIGNATURES: dict[str, tuple] = {
                         ctypes.c_uint64, _P, _P]),
     "pkv_sample_exact": (_I, [_P, _I, ctypes.c_longlong, _I, _I, _P, _I, ctypes.c_float,
                               ctypes.c_uint64, _P, _P]),
+    "pkv_sample_exact_routes": (_I, [_P, _I, ctypes.c_longlong, _I, _I, _P, _I, ctypes.c_float,
+                                     ctypes.c_uint64, _P, _P, _P]),
     "pkv_sample_expf": (_I, [_P, _P, ctypes.c_longlong, _P]),
     "pkv_sample_draw": (ctypes.c_float, [ctypes.c_uint64]),
     "pkv_pool_profile": (_I, [_P, _I]),

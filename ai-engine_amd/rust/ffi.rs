@@ -255,6 +255,11 @@ extern "C" {
         temperatures: *const f32, top_k: c_int, top_p: f32, seed: u64, tokens: *mut i32,
         stream: *mut c_void
     ) -> c_int;
+    pub fn pkv_sample_exact_routes(
+        logits: *const c_void, dtype: c_int, row_stride: c_longlong, batch: c_int, vocab: c_int,
+        temperatures: *const f32, top_k: c_int, top_p: f32, seed: u64, tokens: *mut i32,
+        routes: *mut i32, stream: *mut c_void
+    ) -> c_int;
     pub fn pkv_sample_expf(
         in: *const f32, out: *mut f32, n: c_longlong, stream: *mut c_void
     ) -> c_int;

@@ -490,6 +490,16 @@ int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
 int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
                      int vocab, const float* temperatures, int top_k, float top_p,
                      uint64_t seed, int32_t* tokens, void* stream);
+/* pkv_sample_exact that also reports, for verification (no reference
+ * counterpart), which kernel selected each row: routes (device int32
+ * [batch]) gets 0 (argmax: temperature 0 or vocab <= 1), 1 (f32 logits:
+ * buckets of y, sorted only where a running sum needs the order), 2 (runs
+ * of equal 16-bit values; f32 rows whose logits are all bf16 values when
+ * the buckets left them) or 3 (the radix sort of every logit).  Tokens are
+ * those of pkv_sample_exact. */
+int pkv_sample_exact_routes(const void* logits, int dtype, long long row_stride, int batch,
+                            int vocab, const float* temperatures, int top_k, float top_p,
+                            uint64_t seed, int32_t* tokens, int32_t* routes, void* stream);
 /* The exp pkv_sample_exact uses, exposed for verification (no reference
  * counterpart): out[i] = expf(in[i]) as glibc computes it; device arrays of
  * n floats, on `stream`. */

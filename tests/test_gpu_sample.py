@@ -322,11 +322,12 @@ def test_exact_batch_over_several_launches(gpu):
 
 
 def test_exact_f32_rows_of_bf16_values(gpu):
-    # f32 logits that are bf16 values (a bf16 model's logits upcast) run on
-    # runs of equal values, the others on the radix sort, in one call: every
-    # row equals the f32 restatement, and the bf16-valued rows equal the same
-    # logits passed as bf16; batches over several launches keep each row's
-    # route (70 rows of 2^20: 64 rows per launch)
+    # f32 logits that are bf16 values (a bf16 model's logits upcast) and
+    # genuine f32 logits in one call (buckets first, runs of equal values or
+    # the radix sort for the rows they leave): every row equals the f32
+    # restatement, and the bf16-valued rows equal the same logits passed as
+    # bf16; batches over several launches keep each row's result (70 rows of
+    # 2^20: 64 rows per launch)
     rng = np.random.default_rng(17)
     for B, V in ((24, 128256), (70, 1 << 20)):
         x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
@@ -393,3 +394,124 @@ def test_exact_replays_in_a_graph(gpu):
         assert torch.equal(eager, ref[:3])
     x32 = lg.float().cpu().numpy()
     assert ref.cpu().tolist() == [oracle.sample(x32[b], 0.9)[0] for b in range(B)]
+
+
+# -- f32 logits on buckets of y (sample_bucket_kernel) -------------------------
+ROUTE_ARGMAX, ROUTE_BUCKETS, ROUTE_RUNS, ROUTE_SORT = 0, 1, 2, 3
+
+
+def _sample_routes(lg, temps, **kw):
+    routes = torch.full((lg.shape[0],), -1, dtype=torch.int32, device=lg.device)
+    tok = pagedkv.sample(lg, temps, routes=routes, **kw)
+    return tok.cpu().tolist(), routes.cpu().tolist()
+
+
+def _f32_rows(rng, B, V):
+    """Genuine f32 logits (low bits set) of several shapes."""
+    rows = []
+    for b in range(B):
+        kind = b % 7
+        if kind == 0:
+            x = rng.standard_normal(V) * [0.5, 3.0, 10.0][(b // 7) % 3]
+        elif kind == 1:  # a language model's: a flat bulk and a few strong tokens
+            x = rng.standard_normal(V) * 2.5
+            x[rng.integers(0, V, 5)] = rng.uniform(15, 25, 5)
+        elif kind == 2:  # one very low logit stretches the range
+            x = rng.standard_normal(V) * 3
+            x[rng.integers(0, V)] = -1e4
+        elif kind == 3:  # half the vocabulary masked
+            x = rng.standard_normal(V) * 3
+            x[rng.permutation(V)[:V // 2]] = -np.inf
+        elif kind == 4:  # a narrow range
+            x = rng.uniform(-1, 1, V)
+        elif kind == 5:  # heavy tail towards the top
+            x = rng.gumbel(0, 2, V)
+        else:            # few distinct values: ties inside buckets
+            x = rng.integers(-40, 40, V) * 0.173
+        rows.append(x.astype(np.float32))
+    return np.stack(rows)
+
+
+def _expected_routes(temps):
+    # greedy rows: argmax; half the vocabulary at -inf (row kind 3) with T < 0:
+    # max y is +inf, left to the sort; every other row: the buckets
+    return [ROUTE_ARGMAX if t == 0 else ROUTE_SORT if b % 7 == 3 and t < 0 else ROUTE_BUCKETS
+            for b, t in enumerate(temps)]
+
+
+@pytest.mark.parametrize("top_k,top_p", [(None, None), (50, None), (3000, None), (None, 0.9),
+                                         (None, 0.3), (200, 0.95), (None, 1.0), (1, None)])
+def test_exact_f32_buckets_equal_reference(gpu, top_k, top_p):
+    # every sampled f32 row is selected by the bucket kernel (none left to the
+    # sort), and each token is the f32 restatement's
+    rng = np.random.default_rng(31 + (top_k or 0) + int(100 * (top_p or 0)))
+    B, V = 28, 128256
+    x = _f32_rows(rng, B, V)
+    temps = np.array([[0.8, 1.0, 0.3, -1.1, 1.7, 0.0, 5.0, 0.05][b % 8] for b in range(B)],
+                     np.float32)
+    lg = torch.from_numpy(x).to(gpu)
+    got, routes = _sample_routes(lg, torch.from_numpy(temps).to(gpu), top_k=top_k, top_p=top_p)
+    want = [oracle.sample(x[b], float(temps[b]), top_k=top_k, top_p=top_p)[0] for b in range(B)]
+    assert got == want
+    expect = _expected_routes(temps)
+    assert routes == expect, [(b, routes[b], expect[b]) for b in range(B) if routes[b] != expect[b]]
+
+
+@pytest.mark.parametrize("V", [2, 3, 7, 64, 1000, 4097, 50000])
+def test_exact_f32_buckets_small_vocab(gpu, V):
+    rng = np.random.default_rng(V)
+    B = 21
+    x = _f32_rows(rng, B, V)
+    temps = np.array([[0.8, 1.0, 0.3, -1.1, 1.7, 5.0, 0.05][b % 7] for b in range(B)], np.float32)
+    lg = torch.from_numpy(x).to(gpu)
+    for top_k, top_p in ((None, None), (2, None), (None, 0.5)):
+        got, routes = _sample_routes(lg, torch.from_numpy(temps).to(gpu), top_k=top_k,
+                                     top_p=top_p)
+        want = [oracle.sample(x[b], float(temps[b]), top_k=top_k, top_p=top_p)[0]
+                for b in range(B)]
+        assert got == want, (top_k, top_p)
+        assert routes == _expected_routes(temps), routes
+
+
+def test_exact_f32_rows_the_buckets_leave(gpu):
+    # rows the bucket kernel leaves to the later kernels, with the reference's
+    # tokens: all logits equal (one bucket of 60,000), a dense cluster of
+    # 10,000 distinct values at the top (a top bucket above the 4,096 logits
+    # kept in LDS), the same cluster of bf16 values (runs of equal values),
+    # and a NaN (outside the contract: a token in range, from the sort); a
+    # cluster of 3,000 stays on the buckets
+    rng = np.random.default_rng(5)
+    V = 60000
+    flat = np.full(V, 0.7310585, np.float32)
+    cluster = (rng.standard_normal(V) * 3).astype(np.float32)
+    cluster[:10000] = (20.0 + rng.uniform(0, 1e-3, 10000)).astype(np.float32)
+    cl16 = torch.from_numpy(cluster).to(torch.bfloat16).float().numpy()
+    cl16[:10000] = 20.0
+    small = cluster.copy()
+    small[3000:10000] = (rng.standard_normal(7000) * 3).astype(np.float32)
+    nanrow = (rng.standard_normal(V) * 3).astype(np.float32)
+    nanrow[123] = np.nan
+    x = np.stack([flat, cluster, cl16, nanrow, small])
+    temps = torch.tensor([1.0, 0.9, 0.9, 1.0, 0.9], device=gpu)
+    got, routes = _sample_routes(torch.from_numpy(x).to(gpu), temps)
+    assert routes == [ROUTE_SORT, ROUTE_SORT, ROUTE_RUNS, ROUTE_SORT, ROUTE_BUCKETS], routes
+    for b in (0, 1, 2, 4):
+        assert got[b] == oracle.sample(x[b], float(temps[b]))[0], b
+    assert 0 <= got[3] < V
+
+
+def test_exact_f32_buckets_agree_with_the_sort_on_shuffled_rows(gpu):
+    # the same logits in another order give the token at the same sorted
+    # position (positions of equal logits aside): bucket scatter order and
+    # atomics do not leak into the result
+    rng = np.random.default_rng(8)
+    V, B = 128256, 8
+    base = (rng.standard_normal(V) * 3).astype(np.float32)
+    perms = [rng.permutation(V) for _ in range(B)]
+    x = np.stack([base[p] for p in perms])
+    temps = torch.full((B,), 0.8, device=gpu)
+    got, routes = _sample_routes(torch.from_numpy(x).to(gpu), temps, top_p=0.9)
+    assert set(routes) == {ROUTE_BUCKETS}
+    picked = {float(base[perms[b][got[b]]]) for b in range(B)}
+    assert len(picked) == 1, picked
+    assert got == [oracle.sample(x[b], 0.8, top_p=0.9)[0] for b in range(B)]
