@@ -2101,7 +2101,7 @@ constexpr int kBk = 4096;              // buckets of y per row (index kBk: the t
 constexpr int kWaveSortMax = 256;      // largest bucket one wave sorts
 constexpr int kBkSortMax = kSW * kWaveSortMax;  // largest bucket the workgroup sorts
 constexpr int kRegionA = 4096;         // the top logits, always stored (in LDS)
-constexpr int kGatherSpan = 64;        // buckets one extra pass gathers
+constexpr int kGatherSpan = 4;         // buckets one extra pass gathers
 constexpr float kDTail = 17.5f;        // y - max y <= -kDTail: the tail
 constexpr float kMargin = 0x1p-6f;     // relative margin of the predictions
 constexpr short kNoBinade = SHRT_MIN;  // no prediction
@@ -2689,18 +2689,41 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
       if (w < wv) mpre += bs.wu[w];
       mtot += bs.wu[w];
     }
+    // ... and the denominator's f32 running sum predicted at each bucket's
+    // start (into cur, as floats): a bucket of small probabilities adds each
+    // rounded to whole units of the sum's binade (its logits are within a
+    // factor exp(1 / scale) of its centre), which the mass alone misses
+    float est[4], es = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const float pmj = (float)mpre * 0x1p-40f, mj = (float)m[j] * 0x1p-40f;
       bs.start[b0 + j] = pre;
       pre += c[j];
-      bs.pm[b0 + j] = (float)mpre * 0x1p-40f;
+      bs.pm[b0 + j] = pmj;
       mpre += m[j];
+      const int e = binade_of(pmj);
+      const float unit = e == kNoBinade ? 0.0f : ldexpf(1.0f, e - 23);
+      const float z = e == kNoBinade ? 1e9f : __expf(-((float)(b0 + j) + 0.5f) / rw.scale) / unit;
+      est[j] = z < 256.0f ? (float)c[j] * rintf(z) * unit : mj;
+      es += est[j];
     }
     if (tid == kST - 1) {
       bs.start[kBk] = pre;
       bs.start[kBk + 1] = pre + tail;
       bs.pm[kBk] = (float)mtot * 0x1p-40f;
     }
+    const float ein = wave_incl_add_f32(es);
+    if (lane == 63) bs.wf[wv] = ein;
+    __syncthreads();  // (every read of cur as counts is done)
+    float epre = ein - es;
+    for (int w = 0; w < wv; ++w) epre += bs.wf[w];
+    float* pc = reinterpret_cast<float*>(bs.cur);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pc[b0 + j] = epre;
+      epre += est[j];
+    }
+    if (tid == kST - 1) pc[kBk] = epre;
   }
   __syncthreads();
 
@@ -2743,11 +2766,21 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
   }
   const int nA = (int)bs.start[bA];
 
-  // 4. which buckets to store: the top, the top_k cut, and (with a margin)
-  // each bucket where top_p's sum of p / S or r's of p / S (/ S2, about top_p
-  // when top_p < 1: the kept sum first reaches top_p) is predicted to reach
-  // its threshold; the others get the binade the denominator is predicted to
-  // have at their start
+  // 4. which buckets to store: the top, the top_k cut, the buckets around
+  // each one where the denominator is predicted to leave its binade, and
+  // (with a margin) each bucket where top_p's sum of p / S or r's of p / S
+  // (/ S2, about top_p when top_p < 1: the kept sum first reaches top_p) is
+  // predicted to reach its threshold; the others get the binade the
+  // denominator is predicted to have at their start
+  const float* pc = reinterpret_cast<const float*>(bs.cur);
+  for (int b = tid; b < kBk; b += kST)
+    bs.flag[b] = b >= bA && b < nbk && bs.start[b + 1] > bs.start[b] &&
+                 binade_of(pc[b]) != binade_of(pc[b + 1]) ? kGather : 0;
+  __syncthreads();
+  short egp[kBk / kST];
+#pragma unroll
+  for (int q = 0; q < kBk / kST; ++q) egp[q] = binade_of(pc[tid + q * kST]);
+  __syncthreads();  // (cur is cleared below)
   const float Sest = bs.pm[kBk];
   const bool has_p = a.top_p == a.top_p;  // Some(top_p)
   const float S3est = Sest * (has_p ? fminf(fmaxf(a.top_p, 0x1p-20f), 1.0f) : 1.0f);
@@ -2755,15 +2788,23 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
     return bs.pm[b] * (1.0f - kMargin) / div <= thr * (1.0f + kMargin) &&
            bs.pm[b + 1] * (1.0f + kMargin) / div >= thr * (1.0f - kMargin);
   };
-  for (int b = tid; b < kBk; b += kST) {
+  unsigned char fl[kBk / kST];
+#pragma unroll
+  for (int q = 0; q < kBk / kST; ++q) {
+    const int b = tid + q * kST;
+    bool near = false;
+    for (int o = max(b - 2, 0); o <= min(b + 2, kBk - 1); ++o) near |= bs.flag[o] == kGather;
     const bool st = b < bA || b == part ||
                     (b < nbk && bs.start[b + 1] > bs.start[b] &&
-                     (reaches(b, S3est, a.r) || (has_p && reaches(b, Sest, a.top_p))));
-    bs.flag[b] = b < bA ? kStored | kSorted : st ? kStored : 0;
-    bs.eg[b] = st ? kNoBinade : binade_of(bs.pm[b]);
+                     (near || reaches(b, S3est, a.r) || (has_p && reaches(b, Sest, a.top_p))));
+    fl[q] = b < bA ? kStored | kSorted : st ? kStored : 0;
+    bs.eg[b] = st ? kNoBinade : egp[q];
     bs.inc[b] = 0ull;
     bs.cur[b] = 0u;
   }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kBk / kST; ++q) bs.flag[tid + q * kST] = fl[q];
   __syncthreads();
 
   // 5. store the flagged buckets' keys (the top in LDS); the others'

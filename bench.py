@@ -211,6 +211,9 @@ def main() -> int:
     ap.add_argument("--kv-dtype", choices=["f32", "f16", "bf16"], default=None,
                     help="decode configs: pool dtype instead of the config's (f32 is the "
                          "reference's KvPool dtype)")
+    ap.add_argument("--logits", choices=["bf16", "f32"], default="bf16",
+                    help="sample: the logits' dtype (f32: genuine f32 values, which take the "
+                         "bucket kernel; bf16: the runs of equal 16-bit values)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-layers", type=int, default=2,
                     help="minimum layer passes of the CPU baseline sample (0 = skip it)")
@@ -222,8 +225,8 @@ def main() -> int:
                          "from HBM, not the 256 MB Infinity Cache (0 = auto: >= 1 GB per "
                          "rotation)")
     ap.add_argument("--no-secondary", dest="secondary", action="store_false",
-                    help="cfg3: skip the in-process runs of cfg1, cfg2, cfg4, cfg5 and append "
-                         "reported under 'secondary' in the same line")
+                    help="cfg3: skip the in-process runs of cfg1, cfg2, cfg4, cfg5, append "
+                         "and sample_f32 reported under 'secondary' in the same line")
     ap.add_argument("--graph", choices=["auto", "on", "off"], default="auto",
                     help="replay each step as a captured HIP graph (auto: when a layer's "
                          "launch moves < 128 MB, i.e. launch overhead would show)")
@@ -252,7 +255,7 @@ def main() -> int:
     if args.config == "cfg2":
         return emit(mix(args, dev))
     if args.config == "sample":
-        return sample_bench(args, dev)
+        return emit(sample_bench(args, dev))
     if args.config == "gather":
         return gather_bench(args, dev)
     if args.config == "append":
@@ -274,14 +277,19 @@ def secondary(args, dev) -> dict:
     """The other hot-path workloads, timed in the same process right after
     the headline: cfg1 and cfg4 decode, the cfg2 prefill+decode mix, the
     cfg5 block churn (copy-on-write, eviction, in-place compaction, with the
-    full-pool validation outside timing) and the KV append line, each with
+    full-pool validation outside timing), the KV append line and exact token
+    selection over 256 rows of f32 logits (pkv_sample_exact), each with
     its own pool (the previous one freed), up to 10 timed steps after 2
     warmup steps, no CPU baseline.  A failure is recorded under that
     config's name and does not touch the headline figures."""
     import torch
 
+    def sample_f32(a, d):  # exact token selection over genuine f32 logits
+        a.logits = "f32"
+        return sample_bench(a, d)
+
     runs = {"cfg1": decode_bench, "cfg2": mix, "cfg4": decode_bench, "cfg5": churn,
-            "append": append_bench}
+            "append": append_bench, "sample_f32": sample_f32}
     out = {}
     for name, fn in runs.items():
         a = argparse.Namespace(**vars(args))
@@ -304,7 +312,7 @@ def secondary(args, dev) -> dict:
                      "roofline": {k: r["roofline"][k] for k in keep},
                      "wall_s": round(time.time() - t0, 1)}
         for extra in ("roofline_prefill", "roofline_decode", "read_ceiling_GBps", "validation",
-                      "cow", "compaction", "bit_exact"):
+                      "cow", "compaction", "bit_exact", "fast", "greedy"):
             if extra in r:
                 v = r[extra]
                 out[name][extra] = ({k: v[k] for k in keep} if extra.startswith("roofline_")
@@ -756,16 +764,17 @@ def gather_bench(args, dev) -> int:
     return 0
 
 
-def sample_bench(args, dev) -> int:
+def sample_bench(args, dev) -> dict:
     """Token selection on the device (sample.rs:12-55 as the engine calls it,
     engine.rs:145-162): 256 rows of Llama-3's 128,256-entry vocabulary in
-    bf16, every row sampled at temperature 0.8 (seed 42, no top-k / top-p, as
-    the engine's sample_cfg).  value = rows/s of pkv_sample_exact, which
-    reproduces sample.rs's f32 arithmetic bit for bit (checked against the
-    oracle's f32 restatement); the faster pkv_sample (exact probability mass,
-    equal tokens except where the reference's f32 rounding alone moves the
-    pick) and greedy rows are timed beside it.  roofline = one read of the
-    logits per launch against HBM peak."""
+    bf16 (--logits f32: genuine f32 values), every row sampled at temperature
+    0.8 (seed 42, no top-k / top-p, as the engine's sample_cfg).  value =
+    rows/s of pkv_sample_exact, which reproduces sample.rs's f32 arithmetic
+    bit for bit (checked against the oracle's f32 restatement); the faster
+    pkv_sample (exact probability mass, equal tokens except where the
+    reference's f32 rounding alone moves the pick) and greedy rows are timed
+    beside it.  roofline = one read of the logits per launch against HBM
+    peak."""
     import numpy as np
     import torch
 
@@ -773,9 +782,13 @@ def sample_bench(args, dev) -> int:
     import pagedkv
 
     B, V = 256, 128256
+    f32 = args.logits == "f32"
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
-    logits = (torch.randn((B, V), generator=g, device=dev) * 3.0).to(torch.bfloat16)
+    logits = torch.randn((B, V), generator=g, device=dev) * 3.0
+    if not f32:
+        logits = logits.to(torch.bfloat16)
+    ldt = pagedkv.F32 if f32 else pagedkv.BF16
     temps = torch.full((B,), 0.8, device=dev)
     out = torch.empty(B, dtype=torch.int32, device=dev)
     lib = pagedkv.lib()
@@ -783,7 +796,7 @@ def sample_bench(args, dev) -> int:
 
     def run(t, exact=False, rows=B, o=None):
         fn = lib.pkv_sample_exact if exact else lib.pkv_sample
-        rc = fn(logits.data_ptr(), pagedkv.BF16, V, rows, V,
+        rc = fn(logits.data_ptr(), ldt, V, rows, V,
                 t.data_ptr() if t is not None else None, 0, float("nan") if exact else 1.0, 42,
                 (o if o is not None else out).data_ptr(), sp)
         if rc:
@@ -803,6 +816,11 @@ def sample_bench(args, dev) -> int:
 
     ms_exact = time_it(temps, exact=True)
     got_exact = out.cpu().numpy().copy()
+    routes = torch.empty(B, dtype=torch.int32, device=dev)
+    pagedkv.sample(logits, temps, routes=routes)
+    rnames = ("argmax", "buckets", "runs", "sort")
+    route_counts = {rnames[k]: int(v) for k, v in
+                    enumerate(torch.bincount(routes.long().cpu(), minlength=4).tolist()) if v}
     ms = time_it(temps)
     got = out.cpu().numpy().copy()
     ms_greedy = time_it(None)
@@ -817,13 +835,12 @@ def sample_bench(args, dev) -> int:
         tok, margin = oracle.sample(x32[b], 0.8, precise=True)
         ok &= int(got[b]) == tok or margin < 1e-6
         ok &= int(got_exact[b]) == oracle.sample(x32[b], 0.8)[0]
-    log(f"[bench] sample: exact {ms_exact * 1e3:.1f} us, fast {ms * 1e3:.1f} us sampled, "
-        f"{ms_greedy * 1e3:.1f} us greedy for {B} x {V} bf16 rows; "
-        f"oracle check {'ok' if ok else 'FAILED'}")
+    log(f"[bench] sample: exact {ms_exact * 1e3:.1f} us (rows by kernel: {route_counts}), "
+        f"fast {ms * 1e3:.1f} us sampled, {ms_greedy * 1e3:.1f} us greedy for {B} x {V} "
+        f"{args.logits} rows; oracle check {'ok' if ok else 'FAILED'}")
     if not ok:
-        print(json.dumps({"error": "token selection differs from the oracle"}))
-        return 1
-    rbytes = B * V * 2 + B * 4
+        return {"error": "token selection differs from the oracle"}
+    rbytes = B * V * (4 if f32 else 2) + B * 4
     # small batches (the split path: each row over several workgroups), the
     # first rows of the same logits; checked against the full batch's tokens
     small, small_exact = {}, {}
@@ -838,8 +855,7 @@ def sample_bench(args, dev) -> int:
         + ", ".join(f"{k} rows exact {small_exact[k]['us']} / fast {v['us']}"
                     for k, v in small.items()))
     if not ok:
-        print(json.dumps({"error": "small-batch tokens differ from the full batch's"}))
-        return 1
+        return {"error": "small-batch tokens differ from the full batch's"}
     cpu = None
     if args.cpu_layers > 0:
         # the reference procedure (sort, f32 softmax, running sum) on host rows
@@ -852,15 +868,19 @@ def sample_bench(args, dev) -> int:
         "metric": "on-device token selection rows/s (sample.rs at T=0.8), Llama-3 vocabulary, 1 GPU",
         "value": round(B / (ms_exact / 1e3), 1), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_exact, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded N(0, 9) logits)",
-        "config": {"workload": f"sample: {B} rows x {V} logits, temperature 0.8, seed 42",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.logits,
+        "data": "synthetic (seeded N(0, 9) logits" + (", genuine f32 values)" if f32 else ")"),
+        "config": {"workload": f"sample: {B} rows x {V} {args.logits} logits, temperature 0.8, "
+                               f"seed 42",
                    "entry_point": "pkv_sample_exact (bit-identical to sample.rs)",
+                   "rows_by_kernel": route_counts,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(rbytes / (ms_exact / 1e3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(rbytes / (ms_exact / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "pkv::sample_runs_kernel",
+                     "traffic": None,
+                     "kernel": "pkv::sample_bucket_kernel" if f32 else "pkv::sample_runs_kernel",
                      "kernel_avg_us": round(ms_exact * 1e3, 2),
                      "algorithmic_bytes_per_launch": rbytes},
         "small_batches_exact": small_exact,
@@ -872,8 +892,7 @@ def sample_bench(args, dev) -> int:
                    "GBps": round(rbytes / (ms_greedy / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
-    return 0
+    return res
 
 
 def cpu_baseline(cache, batch, shape, args, q, k_new, v_new, out, log):

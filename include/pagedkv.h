@@ -479,14 +479,16 @@ int pkv_sample(const void* logits, int dtype, long long row_stride, int batch,
  * is Some(top_p), as in the reference, where Some(1.0) still truncates once
  * the f32 running sum reaches 1.  Exponentials are glibc's expf (what
  * f32::exp calls on x86-64 Linux), restated on the device and equal to the
- * host libm on every argument the path uses (<= 0); the sort is a stable
- * radix sort (f32 logits) or, for 16-bit logits, runs of equal values from
- * a histogram of their 65,536 possible keys; every f32 running sum (the
- * softmax denominator, top_p's cumulative sum, the r threshold) takes
- * exactly the reference's rounding steps.  Scratch: 1 MB per row for
- * f16/bf16 logits, 8 bytes per logit per row for f32, at most 512 MB per
- * launch (larger batches run in several launches), in a stream-ordered
- * allocation on `stream`.  One 1024-thread workgroup per row. */
+ * host libm on every argument the path uses (<= 0); the order is, for f32
+ * logits, buckets of y sorted only where a running sum needs the order
+ * (rows that need more: a stable radix sort of every key), and for 16-bit
+ * logits runs of equal values from a histogram of their 65,536 possible
+ * keys; every f32 running sum (the softmax denominator, top_p's cumulative
+ * sum, the r threshold) takes exactly the reference's rounding steps.
+ * Scratch: 1 MB per row for f16/bf16 logits, 8 bytes per logit per row for
+ * f32, at most 512 MB per launch (larger batches run in several launches),
+ * in a stream-ordered allocation on `stream`.  One 1024-thread workgroup per
+ * row. */
 int pkv_sample_exact(const void* logits, int dtype, long long row_stride, int batch,
                      int vocab, const float* temperatures, int top_k, float top_p,
                      uint64_t seed, int32_t* tokens, void* stream);
