@@ -49,7 +49,7 @@ namespace {
 template <int DT, int HD, int R, bool ROPE, bool SB>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     decode_kernel(DecodeKArgs a) {
-  __shared__ DecodeSmem<DT, HD, R> sm;
+  __shared__ DecodeSmem<DT, HD, R, ROPE> sm;
   decode_body<DT, HD, R, ROPE, SB>(a, blockIdx.x, sm);
 }
 

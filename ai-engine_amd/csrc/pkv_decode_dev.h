@@ -13,8 +13,9 @@ namespace pkv {
 
 constexpr int kWavesPerBlock = 4;
 
-// Largest decode tile in tokens (K and V of one tile are held in registers
-// while the tile is processed); 64 or 32.
+// Largest decode tile in tokens of the RoPE kernels with fewer than eight
+// query heads per wave (K and V of one tile are held in registers while the
+// tile is processed); 64 or 32.
 #ifndef PKV_DECODE_TILE
 #define PKV_DECODE_TILE 64
 #endif
@@ -40,21 +41,28 @@ constexpr int kWavesPerBlock = 4;
 // R is the number of query heads a wave carries (1, 2, 4, 8 or 16): the
 // GQA ratio itself, or the next of these widths above it, the extra heads
 // being zero rows of the MFMA A operand whose results are never stored.
-template <int DT, int HD, int R>
+template <int DT, int HD, int R, bool ROPE = false>
 struct DCfg {
   static constexpr int E = DT == PKV_F32 ? 4 : 2;  // element bytes
   static constexpr int RB = HD * E;                // row bytes
   static constexpr int NF = RB / 64;               // QK fragments per lane per row
   static constexpr int NST0 = 16 / NF;
-  // GQA 8 holds twice the P.V accumulators.  Two waves per SIMD fit a
-  // 48-token tile for bf16 rows of 128 (238 registers; f16 widening needs
-  // more) and a 32-token tile otherwise.  The kernel is bound by the loads
-  // in flight, so the larger tile is faster where it fits (-3 % on the
-  // Llama-3-70B shape); narrower rows keep 32, where the shorter partitions
-  // of small batches would waste more of a 48-token tile.  Sixteen heads
-  // hold four times the GQA-4 accumulators: 16-token tiles.
+  // Tile (tokens in flight per wave): 32, 16 for sixteen heads (four times
+  // the GQA-4 accumulators).  A K fragment load reads 64 bytes of each of 16
+  // rows (the MFMA operand layout); streams of such loads lose bandwidth as
+  // more of them are in flight per CU: 32-token tiles at two waves per SIMD
+  // (128 KiB per CU) read 6.9 TB/s in a probe of this access pattern, 64-token
+  // ones (256 KiB) 6.2 TB/s, and the decode follows (Llama-3-8B shape 394
+  // against 406-411 us, Llama-3-70B 449 against 460 us, Llama-3.2-1B 8.5
+  // against 8.7-8.8 us).  The RoPE kernels (more registers live around the
+  // loop) measured the other way (410 against 400 us) and keep 64 tokens
+  // below GQA 8, and 48 for bf16 rows of 128 at GQA 8.
   static constexpr int NSTMAX =
-      (R >= 16 ? 16 : R >= 8 ? (DT == PKV_BF16 && HD == 128 ? 48 : 32) : PKV_DECODE_TILE) / 16;
+      (R >= 16  ? 16
+       : !ROPE  ? 32
+       : R >= 8 ? (DT == PKV_BF16 && HD == 128 ? 48 : 32)
+                : PKV_DECODE_TILE) /
+      16;
   static constexpr int NST = NST0 < 1 ? 1 : (NST0 > NSTMAX ? NSTMAX : NST0);  // sub-tiles
   static constexpr int TILE = 16 * NST;            // tokens per tile
   static constexpr int CH = RB / 16;               // 16-byte chunks per row
@@ -133,9 +141,9 @@ constexpr int kCtxCache = 2048;
 // LDS of one decode workgroup: each wave's P slice, the staged context
 // lengths, and each wave's copy of the new token's K and V rows as stored
 // (fused append).
-template <int DT, int HD, int R>
+template <int DT, int HD, int R, bool ROPE = false>
 struct DecodeSmem {
-  using C = DCfg<DT, HD, R>;
+  using C = DCfg<DT, HD, R, ROPE>;
   float p[kWavesPerBlock][C::TILE * C::PP];
   int ctx[kCtxCache];
   alignas(16) char nl[kWavesPerBlock][2 * C::RB];
@@ -381,8 +389,8 @@ __device__ bool locate_pair(const DecodeKArgs& a, const CtxLens& cl, long long k
 // one wave-uniform id per sub-tile.
 template <int DT, int HD, int R, bool ROPE, bool SB = false>
 __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
-                                            DecodeSmem<DT, HD, R>& sm) {
-  using C = DCfg<DT, HD, R>;
+                                            DecodeSmem<DT, HD, R, ROPE>& sm) {
+  using C = DCfg<DT, HD, R, ROPE>;
   auto& p_lds_all = sm.p;
   auto& ctx_lds = sm.ctx;
   auto& new_lds_all = sm.nl;

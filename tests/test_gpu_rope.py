@@ -172,13 +172,16 @@ def _rope_decode_check(gpu, dt, in_dt, hd, R, KVH, ctx, seed, bs=16):
     err = np.abs(got.astype(np.float64) - ref)
     assert np.all(err <= 1e-3 + 2e-3 * np.abs(ref)), err.max()
     # and the plain kernel fed the oracle's rotated rows gives the same output
+    # up to f32 summation order (the two kernels tile the context
+    # differently): within a twentieth of the tolerance against the oracle
     c2 = case.cache()
     out2 = c2.layer(0).decode_attention(
         _dev(q, dt, gpu), torch.from_numpy(case.tables).to(gpu),
         torch.from_numpy((case.ctx + 1).astype(np.int32)).to(gpu), k_new=_dev(k, dt, gpu),
         v_new=_dev(v, dt, gpu), out_dtype=torch.float32)
     torch.cuda.synchronize()
-    assert np.array_equal(out2.cpu().numpy(), got)
+    diff = np.abs(out2.cpu().numpy().astype(np.float64) - got)
+    assert np.all(diff <= 5e-5 + 1e-4 * np.abs(ref)), diff.max()
     cache.close()
     c2.close()
     rope.close()
