@@ -2153,7 +2153,7 @@ struct BucketValue {
   __device__ __forceinline__ float operator()(uint32_t k) const {
     return of_t(key_value(k) / aT - ymax);
   }
-  // an estimate of of_t within 1e-5 (relative)
+  // an estimate of of_t within 1.3e-6 (relative; see quick_inc)
   __device__ __forceinline__ float approx(float t) const {
     return divs == 0 ? __expf(t) : __expf(t) / (divs == 1 ? S : S * S2);
   }
@@ -2164,6 +2164,25 @@ __device__ __forceinline__ short binade_of(float v) {
   const uint32_t b = __float_as_uint(v);
   const int E = (int)(b >> 23);
   return v > 0.0f && E >= 1 && E <= 254 ? (short)(E - 127) : kNoBinade;
+}
+
+// The unit increment of a value v in binade e decided from an estimate va:
+// round to nearest of v / u (u = 2^(e-23)).  __expf is within 9.9e-7
+// (relative) of the exact expf on every float argument of this path (all
+// 1.1e9 floats in [-17.5, 0], checked on the device), and each division
+// after it adds at most one more rounding, so |va - v| < 1.3e-6 v: when
+// va / u lies farther than 1e-5 va / u + 1e-6 from a half-integer, v / u
+// lies on the same side of it and is no tie.  Returns false (v is needed
+// exactly) otherwise, or from 2^15 units up.
+__device__ __forceinline__ bool quick_inc(float va, int e, unsigned& inc) {
+  const float z = ldexpf(va, 23 - e);
+  inc = 0u;
+  if (z < 0.49f) return true;
+  if (!(z < 32768.0f)) return false;
+  const float fl = floorf(z), f = z - fl;  // exact: z < 2^15
+  if (fabsf(f - 0.5f) <= 1e-5f * z + 1e-6f) return false;
+  inc = (unsigned)fl + (f > 0.5f ? 1u : 0u);
+  return true;
 }
 
 // Adds v's unit increment in binade e to bucket b; a tie, or a step that
@@ -2558,7 +2577,9 @@ __device__ __forceinline__ bool bucket_walk(BucketSmem& bs, uint32_t* K, uint32_
       rw.each([&](float, float t) {
         const int b = rw.bucket(t);
         if (b < todo || b >= nbk || bs.eg[b] != es || (bs.flag[b] & kStored)) return;
-        if (vf.approx(t) >= ldexpf(0.98f, es - 24)) add_inc(bs, b, vf.of_t(t), es);
+        unsigned qi;
+        if (!quick_inc(vf.approx(t), es, qi)) add_inc(bs, b, vf.of_t(t), es);
+        else if (qi) atomicAdd(&bs.inc[b], (unsigned long long)qi);
       });
       __syncthreads();
       continue;
@@ -2808,10 +2829,10 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
   __syncthreads();
 
   // 5. store the flagged buckets' keys (the top in LDS); the others'
-  // increments for the denominator (p below half a unit of the predicted
-  // binade adds nothing)
-  // (the increments go through a per-wave queue in LDS, so that the
-  // exponentials and splits run on full waves)
+  // increments for the denominator, decided from __expf where it settles
+  // the rounding (quick_inc) and otherwise from the exact value (through a
+  // per-wave queue in LDS, so that the exact exponentials and splits run on
+  // full waves)
   uint32_t* K = a.scratch + (size_t)blockIdx.x * 2 * (size_t)V;  // keys
   uint32_t* KI = K + V;                                           // their indices
   const BucketValue p_of{aT, ymax, 1.0f, 1.0f, 0, bs.exptab};
@@ -2843,7 +2864,12 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
         }
       }
       const int e = play && !(fl & kStored) ? bs.eg[b] : kNoBinade;
-      const bool push = e != kNoBinade && __expf(t) >= ldexpf(0.98f, e - 24);
+      bool push = false;
+      if (e != kNoBinade) {
+        unsigned qi;
+        if (!quick_inc(__expf(t), e, qi)) push = true;  // the exact value, through the queue
+        else if (qi) atomicAdd(&bs.inc[b], (unsigned long long)qi);
+      }
       const unsigned long long m = __ballot(push);
       if (m) {  // wave-uniform
         const int at = qn + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -2941,7 +2967,10 @@ __global__ void __launch_bounds__(kST) sample_bucket_kernel(ExactArgs a) {
         const int b = rw.bucket(t);
         if (b >= nbk) return;
         const int e = bs.eg[b];
-        if (e != kNoBinade && vf.approx(t) >= ldexpf(0.98f, e - 24)) add_inc(bs, b, vf.of_t(t), e);
+        if (e == kNoBinade) return;
+        unsigned qi;
+        if (!quick_inc(vf.approx(t), e, qi)) add_inc(bs, b, vf.of_t(t), e);
+        else if (qi) atomicAdd(&bs.inc[b], (unsigned long long)qi);
       });
     }
     __syncthreads();
