@@ -652,6 +652,20 @@ int pkv_decode_attention(pkv_pool* p, int layer, const void* q, void* out, int o
   return decode_call(p, layer, a, stream);
 }
 
+int pkv_decode_attention_positions(pkv_pool* p, int layer, const void* q, void* out,
+                                   int out_dtype, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* context_lens,
+                                   const int32_t* positions, int max_context_len, int batch,
+                                   int n_head, float scale, const void* k_new, const void* v_new,
+                                   void* stream) {
+  CHECK_POOL(p);
+  if (!positions && batch > 0) return fail(p, PKV_ERR_INVALID, "positions is NULL");
+  pkv::DecodeArgs a{q, out, out_dtype, block_tables, max_blocks_per_seq, context_lens,
+                    max_context_len, batch, n_head, scale, k_new, v_new};
+  a.positions = positions;
+  return decode_call(p, layer, a, stream);
+}
+
 int pkv_decode_attention_noalloc(pkv_pool* p, int layer, const void* q, void* out,
                                  int out_dtype, const int32_t* block_tables,
                                  int max_blocks_per_seq, const int32_t* context_lens,

@@ -143,7 +143,8 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     mv0[u] = ok ? mlb[(size_t)pp * pstride_ml] : -INFINITY;
   }
-  const int ctx = clamp_ctx(a, ctx_raw, BS);
+  // the attended keys, as the main kernel lays them out
+  const int ctx = clamp_ctx(a, attended_len(a, b, ctx_raw), BS);
   const int n_parts = part_count(ctx, a.pt_log2, a.sub_log2);
   if (n_parts <= 1) return;
   // entries of partitions past n_parts hold whatever the slots held: select,

@@ -262,11 +262,25 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 }
 
 
+// Keys row b attends: context_lens[b] (ctx_raw), bounded by positions[b] + 1
+// when positions are given -- build_mask's two bounds k < seq_lens[b] and
+// k <= q_positions[b] (attention.rs:22).  A negative position attends
+// nothing (reported by the kernel).  Unclamped, like ctx_raw.
+__device__ __forceinline__ int attended_len(const DecodeKArgs& a, int b, int ctx_raw) {
+  if (!a.positions) return ctx_raw;
+  const int pos = a.positions[b];
+  return pos < 0 ? 0 : (pos >= ctx_raw ? ctx_raw : pos + 1);
+}
+
+// Attended lengths (attended_len) of the batch: the first n from LDS, the
+// rest from global memory.
 struct CtxLens {
-  const int32_t* g;  // global context_lens
+  const DecodeKArgs* a;
   const int* lds;    // LDS copy of the first n entries
   int n;
-  __device__ __forceinline__ int operator[](int b) const { return b < n ? lds[b] : g[b]; }
+  __device__ __forceinline__ int operator[](int b) const {
+    return b < n ? lds[b] : attended_len(*a, b, a->context_lens[b]);
+  }
 };
 
 // Buckets of the last partitions' lengths, (j * SUB / NB, (j + 1) * SUB / NB].
@@ -411,7 +425,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const unsigned rest = item / kvh;  // item = (b, p) * kvh + g
   const int g = (int)(item - rest * kvh);
   int b = 0, p = 0;
-  CtxLens cl{a.context_lens, ctx_lds, 0};
+  CtxLens cl{&a, ctx_lds, 0};
   if (a.direct) {  // launch-uniform
     // Small launches: (b, p) straight from the item, so the wave issues its
     // context length, table slice and Q loads at once (no staging round
@@ -421,7 +435,8 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
     if (b >= a.batch) return;
   } else {
     cl.n = min(a.batch, kCtxCache);
-    for (int i = threadIdx.x; i < cl.n; i += kWavesPerBlock * kWave) ctx_lds[i] = a.context_lens[i];
+    for (int i = threadIdx.x; i < cl.n; i += kWavesPerBlock * kWave)
+      ctx_lds[i] = attended_len(a, i, a.context_lens[i]);
     __syncthreads();
     if (!locate_pair(a, cl, rest, lane, BS, b, p)) return;
   }
@@ -456,10 +471,15 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
       qf[f] = col < rq ? ld16(qrow + 64 * f + 16 * G) : u32x4{0, 0, 0, 0};
   }
 
-  const int ctx_raw = cl[b];
-  const int ctx = clamp_ctx(a, ctx_raw, BS);
-  const bool clamped = ctx != ctx_raw;
+  // ctx: the keys attended (the partition layout's length); ctx_raw: the
+  // context length, where the new token goes
+  const int alen = cl[b];
+  const int ctx_raw = a.positions ? a.context_lens[b] : alen;
+  const int ctx_c = clamp_ctx(a, ctx_raw, BS);
+  const bool clamped = ctx_c != ctx_raw;
   if (clamped && lane == 0 && p == 0) atomicOr(a.err, PKV_EBIT_LENGTH);
+  if (a.positions && lane == 0 && p == 0 && a.positions[b] < 0) atomicOr(a.err, PKV_EBIT_POSITION);
+  const int ctx = min(clamp_ctx(a, alen, BS), ctx_c);
   const int n_parts = part_count(ctx, ptl, subl);
   const int c = lane % C::CH;   // 16-byte chunk of a row (PV / output mapping)
   const int tg = lane / C::CH;  // token group of a V load
@@ -481,7 +501,9 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
 
   const int t_end = min(ctx, t_begin + plen);
   const int nblk = ((t_end - 1) >> a.bs_log2) - blk_begin + 1;  // <= span
-  const int new_pos = (a.k_new != nullptr && !clamped) ? ctx - 1 : -1;
+  // the new token's position (stored by the last partition's wave, also
+  // when the positions bound leaves it out of the attended keys)
+  const int new_pos = (a.k_new != nullptr && !clamped) ? ctx_c - 1 : -1;
 
   int rpos = 0;  // RoPE position of this sequence's new token
   if constexpr (ROPE) {
@@ -510,7 +532,9 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
       qf[f + C::NF / 2] = col < rq ? pack16<DT, C::EPL>(x2) : u32x4{0, 0, 0, 0};
     }
   }
-  if (lane < nblk && (tbl < 0 || tbl >= a.num_blocks)) {
+  const bool tbl_bad = lane < nblk && (tbl < 0 || tbl >= a.num_blocks);
+  const uint64_t bad_blocks = __ballot(tbl_bad);
+  if (tbl_bad) {
     atomicOr(a.err, PKV_EBIT_BLOCK);
     tbl = 0;
   }
@@ -524,10 +548,25 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   // never reads back the pool bytes this launch writes, so no ordering of a
   // store before a load of the same address is assumed, on any memory type.
   char* new_lds = new_lds_all[wave];
-  const bool has_new = new_pos >= 0 && p == n_parts - 1;
-  if (has_new) {
-    int blk = readlane_i(tbl, (new_pos >> a.bs_log2) - blk_begin);
-    size_t off = ((size_t)blk * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
+  const bool store_here = new_pos >= 0 && p == n_parts - 1;
+  const bool has_new = store_here && new_pos == ctx - 1;  // the last tile attends it
+  if (store_here) {
+    // its block: from the partition's table slice, or (past the attended
+    // keys) read from the table and checked
+    // keys) read from the table and checked; a bad id stores nothing
+    const int nb_idx = new_pos >> a.bs_log2;
+    int blk;
+    bool bad_store;
+    if (nb_idx - blk_begin < nblk) {
+      blk = readlane_i(tbl, nb_idx - blk_begin);
+      bad_store = (bad_blocks >> (nb_idx - blk_begin)) & 1;
+    } else {
+      blk = a.block_tables[(size_t)b * a.mbps + nb_idx];
+      bad_store = blk < 0 || blk >= a.num_blocks;
+      if (bad_store && lane == 0) atomicOr(a.err, PKV_EBIT_BLOCK);
+    }
+    const bool do_store = a.store_new && !bad_store;
+    size_t off = ((size_t)(bad_store ? 0 : blk) * BS + (new_pos & (BS - 1))) * slot_stride + head_off;
     char* kst = a.k_pool + off;
     char* vst = a.v_pool + off;
     if constexpr (ROPE) {
@@ -549,7 +588,7 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
         const u32x4 k1 = pack16<DT, C::EPL>(x1), k2 = pack16<DT, C::EPL>(x2);
         st16(new_lds + lane * 16, k1);
         st16(new_lds + (lane + C::CH / 2) * 16, k2);
-        if (a.store_new) {
+        if (do_store) {
           st16(kst + lane * 16, k1);
           st16(kst + (lane + C::CH / 2) * 16, k2);
         }
@@ -559,14 +598,14 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
         load_elems<DT, C::EPL>(vrow, lane * C::EPL, a.in_f32, x);
         const u32x4 v1 = pack16<DT, C::EPL>(x);
         st16(new_lds + C::RB + lane * 16, v1);
-        if (a.store_new) st16(vst + lane * 16, v1);
+        if (do_store) st16(vst + lane * 16, v1);
       }
     } else if (lane < C::CH) {
       const u32x4 k1 = ld16(a.k_new + ((size_t)b * a.kvh + g) * C::RB + lane * 16);
       const u32x4 v1 = ld16(a.v_new + ((size_t)b * a.kvh + g) * C::RB + lane * 16);
       st16(new_lds + lane * 16, k1);
       st16(new_lds + C::RB + lane * 16, v1);
-      if (a.store_new) {
+      if (do_store) {
         st16(kst + lane * 16, k1);
         st16(vst + lane * 16, v1);
       }

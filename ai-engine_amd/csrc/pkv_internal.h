@@ -78,7 +78,7 @@ enum : uint32_t {
   PKV_EBIT_SLOT = 1u,      // append/gather slot out of range
   PKV_EBIT_BLOCK = 2u,     // block table entry out of range
   PKV_EBIT_LENGTH = 4u,    // context length beyond max_context_len / table
-  PKV_EBIT_POSITION = 8u,  // RoPE position outside the table
+  PKV_EBIT_POSITION = 8u,  // RoPE position outside the table, or a negative query position
 };
 
 namespace pkv {

@@ -538,7 +538,10 @@ class KvPool:
         (B, n_kv, hd) the new token is stored at position context_lens-1 first.
         With `rope`, q and k_new are the projections before rotation (f32 or
         the pool dtype) and the kernel applies the rotary embedding at
-        `positions` (default context_lens - 1).  Returns (B, H*hd)."""
+        `positions` (default context_lens - 1).  Given, `positions` ((B,)
+        int32 device) also bound the keys attended: k <= positions[b]
+        (build_mask's second bound; pkv_decode_attention_positions without
+        rope).  Returns (B, H*hd)."""
         if rope is not None:
             return self._decode_attention_rope(q, block_tables, context_lens, max_context_len,
                                                k_new, v_new, scale, out_dtype, out, stream,
@@ -564,11 +567,19 @@ class KvPool:
         qq = q.contiguous()
         if qq.dtype != c.dtype:
             raise TypeError("q must have the pool dtype")
+        kv = (_dev_ptr(k_new) if k_new is not None else None,
+              _dev_ptr(v_new) if v_new is not None else None, _stream_ptr(stream))
+        if positions is not None:
+            pos = _i32(positions, c.device)
+            check(lib().pkv_decode_attention_positions(
+                self._h, self.layer_index, _dev_ptr(qq), _dev_ptr(out), pkv_dtype(out.dtype),
+                _dev_ptr(bt), bt.shape[1], _dev_ptr(cl), _dev_ptr(pos), int(max_context_len), B,
+                H, float(scale), *kv), self._h)
+            return out
         check(lib().pkv_decode_attention(
             self._h, self.layer_index, _dev_ptr(qq), _dev_ptr(out), pkv_dtype(out.dtype),
             _dev_ptr(bt), bt.shape[1], _dev_ptr(cl), int(max_context_len), B, H, float(scale),
-            _dev_ptr(k_new) if k_new is not None else None,
-            _dev_ptr(v_new) if v_new is not None else None, _stream_ptr(stream)), self._h)
+            *kv), self._h)
         return out
 
     def _decode_attention_rope(self, q, block_tables, context_lens, max_context_len, k_new,

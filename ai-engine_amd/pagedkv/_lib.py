@@ -73,6 +73,8 @@ SIGNATURES: dict[str, tuple] = {
                                   ctypes.c_float, _P, _P, _P]),
     "pkv_decode_attention_noalloc": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I,
                                           ctypes.c_float, _P, _P, _P]),
+    "pkv_decode_attention_positions": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _I,
+                                            ctypes.c_float, _P, _P, _P]),
     "pkv_decode_workspace_bytes": (_SZ, [_P, _I, _I, _I]),
     "pkv_pool_reserve_decode": (_I, [_P, _I, _I, _I]),
     "pkv_prefill_attention": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,

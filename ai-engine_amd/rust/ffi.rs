@@ -177,6 +177,12 @@ extern "C" {
     pub fn pkv_pool_reserve_decode(
         pool: *mut PkvPool, batch: c_int, n_head: c_int, max_context_len: c_int
     ) -> c_int;
+    pub fn pkv_decode_attention_positions(
+        pool: *mut PkvPool, layer: c_int, q: *const c_void, out: *mut c_void, out_dtype: c_int,
+        block_tables: *const i32, max_blocks_per_seq: c_int, context_lens: *const i32,
+        positions: *const i32, max_context_len: c_int, batch: c_int, n_head: c_int, scale: f32,
+        k_new: *const c_void, v_new: *const c_void, stream: *mut c_void
+    ) -> c_int;
     pub fn pkv_decode_attention_noalloc(
         pool: *mut PkvPool, layer: c_int, q: *const c_void, out: *mut c_void, out_dtype: c_int,
         block_tables: *const i32, max_blocks_per_seq: c_int, context_lens: *const i32,

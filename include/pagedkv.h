@@ -223,16 +223,31 @@ int pkv_compact(pkv_pool* pool, const int32_t* src_host,
  * reference's build_mask(seq_lens + 1, positions, kv_len) as the decode step
  * calls it, where positions == seq_lens (transformer.rs:289-290,
  * engine.rs:130-133), so its second bound k <= positions[b]
- * (attention.rs:22) coincides with the first.  A caller whose positions
- * differ from seq_lens gets that mask by passing context_lens[b] =
- * min(seq_lens[b] + 1, positions[b] + 1) without k_new / v_new (which are
- * stored at context_lens[b] - 1), after storing the row with pkv_append. */
+ * (attention.rs:22) coincides with the first.  Callers whose positions
+ * differ from seq_lens use pkv_decode_attention_positions. */
 int pkv_decode_attention(pkv_pool* pool, int layer, const void* q, void* out,
                          int out_dtype, const int32_t* block_tables,
                          int max_blocks_per_seq, const int32_t* context_lens,
                          int max_context_len, int batch, int n_head,
                          float scale, const void* k_new, const void* v_new,
                          void* stream);
+
+/* pkv_decode_attention with build_mask's second bound (attention.rs:11-28):
+ * key k of row b is attended iff k < context_lens[b] and k <= positions[b],
+ * positions being the rows' query positions (the reference's q_positions,
+ * transformer.rs:290).  positions: device int32 [batch], non-NULL.  k_new /
+ * v_new are still stored at context_lens[b] - 1 (KvPool::write at seq_lens,
+ * transformer.rs:276) and attended only when positions[b] >=
+ * context_lens[b] - 1.  A negative position attends no key: the row is
+ * zero, nothing is stored for it, and pkv_pool_check() reports
+ * PKV_ERR_DEVICE_DATA.  Other arguments and limits as pkv_decode_attention;
+ * the split-context merge uses the same bounded lengths. */
+int pkv_decode_attention_positions(pkv_pool* pool, int layer, const void* q, void* out,
+                                   int out_dtype, const int32_t* block_tables,
+                                   int max_blocks_per_seq, const int32_t* context_lens,
+                                   const int32_t* positions, int max_context_len, int batch,
+                                   int n_head, float scale, const void* k_new, const void* v_new,
+                                   void* stream);
 
 /* Workspace that pkv_decode_attention needs for a given batch/length; the
  * pool grows its internal workspace on demand with a hipMalloc.  The buffer
@@ -412,6 +427,9 @@ int pkv_rope_check(pkv_rope* rope);
  * the rotated q and k are rounded to the pool dtype, as stored k rows are.
  * positions: device int32 [batch] or NULL; NULL uses context_lens[b] - 1,
  * the reference's decode position (positions == seq_lens, engine.rs:130-133).
+ * Given, they also bound the keys attended as in
+ * pkv_decode_attention_positions (the reference's decode step passes the
+ * same positions to the rotation and to build_mask, transformer.rs:237,290).
  * rope->rope_dim must equal the pool's head_dim.  A position outside
  * [0, max_seq) is reported by pkv_pool_check() and rotates by position 0. */
 int pkv_decode_attention_rope(pkv_pool* pool, int layer, const pkv_rope* rope,

@@ -76,28 +76,39 @@ class Case:
     def context_lens(self):
         return (self.ctx + 1).astype(np.int32)
 
-    def run(self, out_dtype=None, max_context_len=None):
+    def run(self, out_dtype=None, max_context_len=None, positions=None, check=True):
         pool = self.cache.layer(0)
         kn = _to_dev(self.kn, self.dt, self.gpu) if self.fused else None
         vn = _to_dev(self.vn, self.dt, self.gpu) if self.fused else None
+        pos = None if positions is None else torch.from_numpy(
+            np.asarray(positions, np.int32)).to(self.gpu)
         out = pool.decode_attention(_to_dev(self.q, self.dt, self.gpu),
                                     torch.from_numpy(self.tables).to(self.gpu),
                                     torch.from_numpy(self.context_lens).to(self.gpu),
                                     max_context_len=max_context_len or int(self.context_lens.max()),
                                     k_new=kn, v_new=vn, scale=self.scale,
-                                    out_dtype=out_dtype or torch.float32)
+                                    out_dtype=out_dtype or torch.float32, positions=pos)
         torch.cuda.synchronize()
-        self.cache.check()
+        if check:
+            self.cache.check()
         return out.float().cpu().numpy()
 
-    def reference(self):
+    def reference(self, positions=None):
+        """fp64 closed form after the oracle's append of the new rows at
+        seq_lens; with positions, the keys are bounded by build_mask's
+        k <= positions[b] too (attention.rs:22)."""
         kp, vp = self.kp.copy(), self.vp.copy()
+        lens = self.context_lens
+        if positions is not None:
+            pos = np.asarray(positions, np.int64)
+            lens = np.where(pos < 0, 0, np.minimum(lens, pos + 1)).astype(np.int32)
         if self.fused:
             for b in range(len(self.ctx)):
-                oracle.kv_write(kp, vp, self.bs, self.tables[b].astype(np.uint32), int(self.ctx[b]),
-                                self.kn[b:b + 1], self.vn[b:b + 1])
+                if positions is None or positions[b] >= 0:
+                    oracle.kv_write(kp, vp, self.bs, self.tables[b].astype(np.uint32),
+                                    int(self.ctx[b]), self.kn[b:b + 1], self.vn[b:b + 1])
         ref = oracle.paged_attention_f64(kp, vp, self.dt, self.bs, self.tables.astype(np.uint32),
-                                         self.context_lens, wl.widen(self.q, self.dt), self.scale)
+                                         lens, wl.widen(self.q, self.dt), self.scale)
         return ref, kp, vp
 
     def close(self):
@@ -461,4 +472,94 @@ def test_positions_bound_of_build_mask(gpu):
     full = oracle.paged_attention_f64(kp, vp, wl.F32, bs, c.tables.astype(np.uint32),
                                       (c.ctx + 1).astype(np.int32), c.q, c.scale)
     assert np.abs(full - ref).max() > 1e-2
+    c.close()
+
+
+def _positions(ctx, seed):
+    # per row: the reference's own position (== seq_len), one below it, a
+    # random earlier one, 0, or one past the context (no effect)
+    r = np.random.default_rng(seed)
+    pos = []
+    for i, c in enumerate(ctx):
+        k = i % 5
+        pos.append([c, max(c - 1, 0), int(r.integers(0, c + 1)), 0, c + int(r.integers(1, 5000))][k])
+    return pos
+
+
+@pytest.mark.parametrize("dt,H,KVH,hd,bs", [(wl.BF16, 32, 8, 128, 16), (wl.F16, 32, 4, 64, 16),
+                                           (wl.F32, 16, 8, 64, 16), (wl.BF16, 32, 8, 128, 4),
+                                           (wl.BF16, 28, 4, 64, 32)])
+def test_decode_positions_bound(gpu, dt, H, KVH, hd, bs):
+    # pkv_decode_attention_positions: both build_mask bounds with the new
+    # row stored at seq_lens (attended only when positions >= seq_lens), on
+    # contexts that span several partitions (the merge uses the bounded
+    # lengths too)
+    ctx = [0, 1, 15, 16, 17, 40, 700, 1023, 1024, 1025, 2100, 3000] + \
+        [int(x) for x in wl.randint(hd + bs, 28, 1, 3000)]
+    pos = _positions(ctx, hd + bs)
+    c = Case(gpu, dt, H, KVH, hd, bs, ctx, seed=hd + H + bs, fused=True)
+    got = c.run(max_context_len=3001, positions=pos)
+    ref, kp, vp = c.reference(pos)
+    _close(got, ref, f"positions bound dt={dt} hd={hd} bs={bs}")
+    k1, v1 = _host_pool(c.cache, 0)
+    assert np.array_equal(k1, kp) and np.array_equal(v1, vp)
+    c.close()
+
+
+def test_decode_positions_bound_work_list(gpu):
+    # 200 sequences x 4 kv heads x 3 partitions: a work-list launch (items
+    # ordered from the bounded lengths, the last 1024 tokens split in two)
+    ctx = [0, 1023, 1024, 2047, 2048, 2999] + [int(x) for x in wl.randint(7, 194, 1, 3000)]
+    pos = _positions(ctx, 7)
+    c = Case(gpu, wl.BF16, 16, 4, 64, 16, ctx, seed=7, fused=True)
+    got = c.run(max_context_len=3001, positions=pos)
+    ref, kp, vp = c.reference(pos)
+    _close(got, ref, "positions bound, work list")
+    k1, v1 = _host_pool(c.cache, 0)
+    assert np.array_equal(k1, kp) and np.array_equal(v1, vp)
+    c.close()
+
+
+def test_decode_positions_equal_seq_lens_is_plain_decode(gpu):
+    # positions == seq_lens (the reference's engine, engine.rs:130-133):
+    # bit for bit pkv_decode_attention
+    ctx = [3, 500, 1500, 2500, 77]
+    a = Case(gpu, wl.BF16, 32, 8, 128, 16, ctx, seed=3, fused=True)
+    b = Case(gpu, wl.BF16, 32, 8, 128, 16, ctx, seed=3, fused=True)
+    x = a.run()
+    y = b.run(positions=ctx)
+    assert np.array_equal(x, y)
+    ka, va = _host_pool(a.cache, 0)
+    kb, vb = _host_pool(b.cache, 0)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.close()
+    b.close()
+
+
+def test_decode_negative_position_reported(gpu):
+    ctx = [30, 40, 50]
+    pos = [30, -1, 20]
+    c = Case(gpu, wl.BF16, 32, 8, 128, 16, ctx, seed=5, fused=True)
+    got = c.run(positions=pos, check=False)
+    with pytest.raises(pagedkv.PagedKvError):
+        c.cache.check()
+    ref, kp, vp = c.reference(pos)
+    assert np.all(got[1] == 0.0)
+    _close(got, ref, "negative position")
+    k1, v1 = _host_pool(c.cache, 0)
+    assert np.array_equal(k1, kp) and np.array_equal(v1, vp)  # row 1 stored nothing
+    c.close()
+
+
+def test_decode_positions_refuses_null(gpu):
+    c = Case(gpu, wl.BF16, 32, 8, 128, 16, [10, 20], seed=1)
+    L = pagedkv.lib()
+    q = _to_dev(c.q, c.dt, gpu)
+    out = torch.empty((2, 32 * 128), dtype=torch.float32, device=gpu)
+    t = torch.from_numpy(c.tables).to(gpu)
+    cl = torch.from_numpy(c.context_lens).to(gpu)
+    rc = L.pkv_decode_attention_positions(c.cache.handle, 0, q.data_ptr(), out.data_ptr(),
+                                          pagedkv.F32, t.data_ptr(), t.shape[1], cl.data_ptr(),
+                                          None, 64, 2, 32, c.scale, None, None, None)
+    assert rc == pagedkv._lib.PKV_ERR_INVALID
     c.close()

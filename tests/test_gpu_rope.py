@@ -188,7 +188,9 @@ def _rope_decode_check(gpu, dt, in_dt, hd, R, KVH, ctx, seed, bs=16):
 
 
 def test_decode_attention_rope_explicit_positions(gpu):
-    # positions need not equal seq_lens (decode_step takes them separately)
+    # positions need not equal seq_lens (decode_step takes them separately):
+    # they rotate q and k and bound the keys attended (build_mask's
+    # k <= positions[b], attention.rs:22); the new row is stored at seq_lens
     ctx = [40, 700, 1200]
     case = RopeCase(gpu, wl.BF16, wl.F32, 16, 4, 128, ctx, seed=21, positions=[5, 8000, 1199])
     rope = pagedkv.Rope(128, 500000.0, case.max_seq)
@@ -198,11 +200,14 @@ def test_decode_attention_rope_explicit_positions(gpu):
     for b in range(len(ctx)):
         oracle.kv_write(kp, vp, case.bs, case.tables[b].astype(np.uint32), int(case.ctx[b]),
                         k[b:b + 1], v[b:b + 1])
+    lens = np.minimum(case.ctx + 1, case.pos.astype(np.int64) + 1).astype(np.int32)  # [6, 701, 1200]
     ref = oracle.paged_attention_f64(kp, vp, wl.BF16, case.bs, case.tables.astype(np.uint32),
-                                     (case.ctx + 1).astype(np.int32), wl.widen(q, wl.BF16),
-                                     1 / math.sqrt(128))
+                                     lens, wl.widen(q, wl.BF16), 1 / math.sqrt(128))
     err = np.abs(got.astype(np.float64) - ref)
     assert np.all(err <= 1e-3 + 2e-3 * np.abs(ref)), err.max()
+    k1 = cache.read_bytes(0, pagedkv.K).view(np.uint16).reshape(kp.shape)
+    v1 = cache.read_bytes(0, pagedkv.V).view(np.uint16).reshape(vp.shape)
+    assert np.array_equal(k1, kp) and np.array_equal(v1, vp)
     cache.close()
     rope.close()
 
