@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   const int b = (int)(pair / (unsigned)a.kvh);
   const int g = (int)(pair - (unsigned)b * (unsigned)a.kvh);
   const int BS = 1 << a.bs_log2;
-  const size_t pstride_ml = (size_t)R * 2;   // floats between partitions
+  const size_t pstride_ml = kMlFloats;       // floats between partitions
   const size_t pstride_o = (size_t)R * HD;
   const float* mlb = a.part_ml + (size_t)pair * a.max_parts * pstride_ml + 2 * h;
   const int q = lane / LPR;  // row group
@@ -207,7 +207,12 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
   if (lane >= LPR) return;
 
   const float inv = 1.0f / L;
-  const size_t eo = ((size_t)b * a.kvh * a.rtot + g * a.rtot + a.h0 + h) * HD + 4 * c;
+  // chunk c of a partial row holds elements (c % CH) EPL + 4 (c / CH) ..
+  // (the main kernel's store order; CH = HD / EPL 16-byte chunks of a row)
+  const int epl = dt == PKV_F32 ? 4 : 8;
+  const int chs = HD / epl;
+  const size_t eo = ((size_t)b * a.kvh * a.rtot + g * a.rtot + a.h0 + h) * HD +
+                    (c % chs) * epl + 4 * (c / chs);
   if (a.out_f32) {
     *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + eo) =
         f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
@@ -333,7 +338,7 @@ size_t decode_workspace_bytes(const pkv_pool* p, int batch, int n_head,
   size_t pairs = (size_t)batch * p->n_kv_head;
   size_t R = (size_t)group_width(n_head / p->n_kv_head);  // partial heads per partition
   if (mp <= 1) return 256;
-  size_t ml = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
+  size_t ml = ((pairs * mp * kMlFloats * 4 + 255) / 256) * 256;
   size_t po = pairs * mp * R * (size_t)p->head_dim * 4;
   return ml + po;
 }
@@ -375,7 +380,7 @@ DecodeKArgs decode_kargs(const pkv_pool* p, int layer, const DecodeArgs& a, char
   k.rtot = rtot;
   // small launches (every wave resident at once): direct wave mapping
   k.direct = (long long)pairs * mp <= kDirectMaxItems;
-  size_t ml_bytes = ((pairs * mp * R * 2 * 4 + 255) / 256) * 256;
+  size_t ml_bytes = ((pairs * mp * kMlFloats * 4 + 255) / 256) * 256;
   k.part_ml = reinterpret_cast<float*>(partials);
   k.part_o = reinterpret_cast<float*>(partials + ml_bytes);
   k.err = p->err;

@@ -174,7 +174,8 @@ def test_many_partitions_merge(gpu, dt, hd, R):
 
 
 def _partials_bytes(pairs, parts, width, hd):
-    ml = -(-pairs * parts * width * 2 * 4 // 256) * 256
+    # (m, l) of an item's heads in one 128-byte line, then the partial rows
+    ml = -(-pairs * parts * 32 * 4 // 256) * 256
     return ml + pairs * parts * width * hd * 4
 
 

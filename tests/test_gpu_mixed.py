@@ -150,7 +150,7 @@ def test_mixed_with_split_last_partitions(gpu):
     m = Mix(gpu, wl.BF16, 32, 8, 128, 16, priors=[700, 30], chunks=[64, 200], dctx=dctx, seed=17)
     c = m.caches[0]
     assert c.decode_workspace_bytes(128, 32, 4096) == (
-        -(-128 * 8 * 5 * 4 * 2 * 4 // 256) * 256 + 128 * 8 * 5 * 4 * 128 * 4)
+        -(-128 * 8 * 5 * 32 * 4 // 256) * 256 + 128 * 8 * 5 * 4 * 128 * 4)
     sp, sd = m.separate(torch.float32)
     mp, md = m.mixed(torch.float32)
     assert _same(sp, mp) and _same(sd, md) and m.pools_equal()
