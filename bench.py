@@ -274,36 +274,43 @@ def emit(res: dict) -> int:
 
 
 def secondary(args, dev) -> dict:
-    """The other hot-path workloads, timed in the same process right after
-    the headline: cfg1 and cfg4 decode, the cfg2 prefill+decode mix, the
-    cfg5 block churn (copy-on-write, eviction, in-place compaction, with the
-    full-pool validation outside timing), the KV append line and exact token
-    selection over 256 rows of f32 logits (pkv_sample_exact), each with
-    its own pool (the previous one freed), up to 10 timed steps after 2
-    warmup steps, no CPU baseline.  A failure is recorded under that
-    config's name and does not touch the headline figures."""
+    """The other hot-path workloads, timed right after the headline: cfg1 and
+    cfg4 decode, the cfg2 prefill+decode mix, the cfg5 block churn
+    (copy-on-write, eviction, in-place compaction, with the full-pool
+    validation outside timing), the KV append line and exact token selection
+    over 256 rows of f32 logits (pkv_sample_exact), up to 10 timed steps
+    after 2 warmup steps, no CPU baseline.  Each runs in a child process of
+    its own, exactly as `bench.py --config NAME` (its pool allocated in a
+    fresh process, as in a standalone run: allocated in this process after
+    the headline's pool was freed, cfg4's pool landed on slower HBM
+    placements, 465.7-468.7 us per layer against 441.4-461.2 us for every
+    fresh-process run).  A failure is recorded under that config's name and
+    does not touch the headline figures."""
+    import subprocess
+
     import torch
-
-    def sample_f32(a, d):  # exact token selection over genuine f32 logits
-        a.logits = "f32"
-        return sample_bench(a, d)
-
-    runs = {"cfg1": decode_bench, "cfg2": mix, "cfg4": decode_bench, "cfg5": churn,
-            "append": append_bench, "sample_f32": sample_f32}
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()  # the headline's tensors, before the children allocate
+    runs = {"cfg1": ["--config", "cfg1"], "cfg2": ["--config", "cfg2"],
+            "cfg4": ["--config", "cfg4"], "cfg5": ["--config", "cfg5"],
+            "append": ["--config", "append"],
+            "sample_f32": ["--config", "sample", "--logits", "f32"]}
+    steps = max(1, min(args.steps, 10))
     out = {}
-    for name, fn in runs.items():
-        a = argparse.Namespace(**vars(args))
-        a.config, a.steps, a.warmup, a.cpu_layers = name, max(1, min(args.steps, 10)), 2, 0
-        a.replicas, a.graph = 0, "auto"
+    for name, cfg_args in runs.items():
+        cmd = [sys.executable, os.path.abspath(__file__), *cfg_args, "--steps", str(steps),
+               "--warmup", "2", "--cpu-layers", "0", "--seed", str(args.seed)]
         t0 = time.time()
         try:
-            r = fn(a, dev)
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+            lines = [l for l in p.stdout.splitlines() if l.startswith("{")]
+            r = json.loads(lines[-1]) if lines else {
+                "error": f"exit status {p.returncode}: {p.stderr.strip()[-400:]}"}
         except Exception as e:  # recorded, the headline stands
             r = {"error": f"{type(e).__name__}: {e}"}
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
         if "error" in r:
             out[name] = {"error": r["error"]}
+            log(f"[bench] secondary {name}: {r['error']}")
             continue
         keep = ("bound", "achieved", "unit", "frac", "kernel", "kernel_avg_us")
         out[name] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
