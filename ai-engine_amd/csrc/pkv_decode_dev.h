@@ -556,7 +556,6 @@ __device__ __forceinline__ void decode_body(const DecodeKArgs& a, int bid,
   const bool has_new = store_here && new_pos == ctx - 1;  // the last tile attends it
   if (store_here) {
     // its block: from the partition's table slice, or (past the attended
-    // keys) read from the table and checked
     // keys) read from the table and checked; a bad id stores nothing
     const int nb_idx = new_pos >> a.bs_log2;
     int blk;
