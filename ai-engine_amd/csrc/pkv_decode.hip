@@ -313,12 +313,14 @@ void decode_plan(const pkv_pool* p, int batch, int n_head, int max_context_len,
   // tokens in two (block-aligned while block_size <= pt / 2): the final
   // round of waves then holds items of at most pt / 2 tokens instead of
   // 0 .. pt.
-  // Measured on the Llama-3-8B layer shape (ctx U[512, 4096], bf16): 205-211
-  // against 225 us per launch at B = 128 (4096 items), within the
-  // launch-to-launch spread at B = 256 (8192 items: 396-417 against
-  // 403-405 us) and 3 % slower at B = 512, where the extra partial writes
-  // and merge reads outweigh the shorter tail.  So only lists of up to
-  // PKV_DECODE_SUB_SPLIT_MAX_ITEMS full-length items are split.
+  // Measured on the Llama-3-8B layer shape (ctx U[512, 4096], bf16), both
+  // plans launched on one pool (one HBM placement), alternating: 205-211
+  // against 225 us per launch at B = 128 (4096 items); 0.5-1.4 % faster at
+  // B = 256 (8192 items; four processes), and on the Llama-3-70B stage
+  // (B = 128, 8192 items) -1.0 to +0.5 %; 1.0 % slower at B = 384 and 2.6 %
+  // at B = 512, where the extra partial writes and merge reads outweigh the
+  // shorter tail.  So only lists of up to PKV_DECODE_SUB_SPLIT_MAX_ITEMS
+  // full-length items are split.
   int sub = pt;
   if (pt == PKV_DECODE_PART_MAX && pairs * mp > kDirectMaxItems &&
       pairs * mp <= PKV_DECODE_SUB_SPLIT_MAX_ITEMS &&

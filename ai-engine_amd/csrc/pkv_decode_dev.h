@@ -35,7 +35,7 @@ constexpr int kWavesPerBlock = 4;
 #define PKV_DECODE_SUB_SPLIT 2
 #endif
 #ifndef PKV_DECODE_SUB_SPLIT_MAX_ITEMS
-#define PKV_DECODE_SUB_SPLIT_MAX_ITEMS 4096
+#define PKV_DECODE_SUB_SPLIT_MAX_ITEMS 8192
 #endif
 
 // R is the number of query heads a wave carries (1, 2, 4, 8 or 16): the

@@ -185,9 +185,9 @@ def _partials_bytes(pairs, parts, width, hd):
 def test_split_last_partition(gpu, dt, hd, R, bs, fused):
     # 128 sequences x 8 kv heads with contexts up to 4096: a work list of
     # 4096 items of 1024 tokens, short enough that the kernel cuts each
-    # context's last 1024 tokens in two (5 partitions at most, against 4 for
-    # the 8192-item list of 256 sequences); lengths on and around every
-    # 512-token edge, the rest random
+    # context's last 1024 tokens in two (5 partitions at most; so does the
+    # 8192-item list of 256 sequences, against 4 for the 16384-item list of
+    # 512); lengths on and around every 512-token edge, the rest random
     edges = [1, 2, 511, 512, 513, 1023, 1024, 1025, 1536, 1537, 2048, 2049, 2560, 2561,
              3072, 3073, 3584, 3585, 4095, 4096]
     cl = edges + [int(x) for x in wl.randint(hd + R + bs, 128 - len(edges), 1, 4096)]
@@ -197,7 +197,9 @@ def test_split_last_partition(gpu, dt, hd, R, bs, fused):
     assert L.pkv_decode_workspace_bytes(c.cache.handle, 128, 8 * R, 4096) == \
         _partials_bytes(128 * 8, 5, w, hd)
     assert L.pkv_decode_workspace_bytes(c.cache.handle, 256, 8 * R, 4096) == \
-        _partials_bytes(256 * 8, 4, w, hd)
+        _partials_bytes(256 * 8, 5, w, hd)
+    assert L.pkv_decode_workspace_bytes(c.cache.handle, 512, 8 * R, 4096) == \
+        _partials_bytes(512 * 8, 4, w, hd)
     got = c.run()
     ref, _, _ = c.reference()
     _close(got, ref, f"split last partition dt={dt} hd={hd} R={R} bs={bs}")
