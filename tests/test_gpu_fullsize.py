@@ -88,3 +88,39 @@ def test_full_shape_relocation_permutation_and_oracle(gpu, shape, B, lo, hi):
                 f"row {b}: max err {err.max():.3g}")
     finally:
         cache.close()
+
+
+def test_full_shape_positions_bound_equals_shorter_context(gpu):
+    # build_mask's second bound at the full cfg3 shape: attention with
+    # positions (k <= positions[b], attention.rs:22) equals plain decode over
+    # min(context_lens, positions + 1) keys bit for bit -- both lay the
+    # partitions out over that bounded length; positions at, below and past
+    # each context
+    shape, B = wl.CFG3, 256
+    batch = wl.decode_batch(shape, B, 512, 4096, seed=1234)
+    H, KVH, hd, bs = shape.n_head, shape.n_kv_head, shape.head_dim, shape.block_size
+    print(f"[fullsize] positions bound: B={B}, num_blocks={batch.num_blocks}", flush=True)
+    cache = pagedkv.PagedKvCache(1, batch.num_blocks, bs, KVH, hd, torch.bfloat16)
+    try:
+        cache.fill_normal(78)
+        pool = cache.layer(0)
+        g = torch.Generator(device="cpu").manual_seed(6)
+        q = (torch.randn((B, H, hd), generator=g) / math.sqrt(hd)).to(torch.bfloat16).to(gpu)
+        tables = torch.from_numpy(np.where(batch.tables < 0, 0, batch.tables).astype(np.int32)).to(gpu)
+        cl = batch.context_lens.astype(np.int64)
+        r = np.random.default_rng(11)
+        pos = np.where(np.arange(B) % 4 == 0, cl - 1,                     # the engine's own position
+                       np.where(np.arange(B) % 4 == 1, cl + r.integers(0, 900, B),  # past the context
+                                r.integers(0, cl)))                        # somewhere before it
+        mcl = int(cl.max())
+        out_p = pool.decode_attention(q, tables, torch.from_numpy(cl.astype(np.int32)).to(gpu),
+                                      max_context_len=mcl, out_dtype=torch.float32,
+                                      positions=torch.from_numpy(pos.astype(np.int32)).to(gpu))
+        short = np.minimum(cl, pos + 1).astype(np.int32)
+        out_s = pool.decode_attention(q, tables, torch.from_numpy(short).to(gpu),
+                                      max_context_len=mcl, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        cache.check()
+        assert torch.equal(out_p, out_s), "positions bound differs from the shorter context"
+    finally:
+        cache.close()
